@@ -1,0 +1,233 @@
+/*
+ * wkv7.h -- C ABI of the MI355X (gfx950) WKV7 time-mix recurrence.
+ *
+ * Drop-in boundary for the WKV7 operator of rwkv-rs (crate rwkv-nn). Every
+ * entry point replaces one method of the reference's Burn backend traits and
+ * keeps its argument order and meaning:
+ *
+ *   reference (under /root/reference/crates/rwkv-nn/src/kernels/)   entry point
+ *   wkv7_pretrain/mod.rs:19-27   Wkv7PretrainBackend::wkv7_pretrain_forward     wkv7_pretrain_forward
+ *   wkv7_pretrain/mod.rs:29-40   Wkv7PretrainBackend::wkv7_pretrain_backward    wkv7_pretrain_backward
+ *   wkv7_statepass/mod.rs:19-28  Wkv7StatePassBackend::wkv7_statepass_forward   wkv7_statepass_forward
+ *   wkv7_statepass/mod.rs:30-42  Wkv7StatePassBackend::wkv7_statepass_backward  wkv7_statepass_backward
+ *   wkv7_statetune/mod.rs:19-28  Wkv7StateTuneBackend::wkv7_statetune_forward   wkv7_statetune_forward
+ *   wkv7_statetune/mod.rs:30-41  Wkv7StateTuneBackend::wkv7_statetune_backward  wkv7_statetune_backward
+ *   wkv7_infer/mod.rs:30-51      Wkv7InferBackend::wkv7_infer_forward           wkv7_infer_forward
+ *   wkv7_common/host.rs:29-41    wkv7_forward_impl (flags)                      wkv7_forward
+ *   wkv7_common/host.rs:185-199  wkv7_backward_impl (flags)                     wkv7_backward
+ *
+ * Operand names follow the reference: weight_decay (w, a raw logit; the
+ * kernel forms exp(-e^{-1/2} sigmoid(w))), receptance (r), key (k), value
+ * (v), removal (a), replacement (b). Layouts (row-major, last index fastest):
+ *
+ *   per-token tensors            [batch, context_len, num_heads, head_size]
+ *   initial/final state, grads   [batch, num_heads, head_size(value), head_size(key)]   fp32
+ *   state (checkpoints)          [batch, num_heads, context_len/chunk_len,
+ *                                 head_size(key), head_size(value)]  fp32, i.e. the
+ *                                state after step c*chunk_len + chunk_len - 1, transposed
+ *   removal_state                [batch, context_len, num_heads, head_size]  fp32
+ *
+ * dtype (WKV7_DTYPE_*) is the element type of the per-token tensors and of
+ * output / the six input gradients. State-family tensors (initial and final
+ * state, checkpoints, removal_state, their gradients) are always fp32 and all
+ * arithmetic is fp32, as in the reference, which casts non-fp32 inputs to fp32
+ * and the outputs back (wkv7_common/host.rs:45-64, 204-229).
+ *
+ * Ownership and threading: the caller allocates every buffer on the device
+ * (use wkv7_checkpoint_numel for the checkpoint tensor); the library
+ * allocates nothing, keeps no state and is reentrant. Work is enqueued on
+ * `stream` (a hipStream_t, NULL = the default stream) and the call returns
+ * without synchronising. Outputs must not overlap each other or any input
+ * (the infer state buffer, which is updated in place, is the only in/out
+ * operand). Per-token tensors must be 8-byte aligned (bf16) or 16-byte
+ * aligned (fp32); fp32 state-family tensors 16-byte aligned.
+ *
+ * Errors: every entry point returns WKV7_OK (0) or a wkv7_status code and never
+ * aborts. All checks are done on the host before any HIP call; a failed
+ * kernel launch returns WKV7_ERR_HIP and wkv7_last_hip_error() gives the
+ * hipError_t of that failure on the calling thread. The reference panics on
+ * the same conditions ("chunk_len must divide sequence length",
+ * wkv7_common/host.rs:109-112).
+ *
+ * Supported shapes: head_size == 64 (RWKV-7's head size); batch_size and
+ * num_heads up to 65535; context_len up to 2^31-1; context_len == 0 is
+ * allowed (the final state is the initial state, the initial-state gradient
+ * is the final-state gradient).
+ *
+ * Numerics: the backward rebuilds S_{t-1} = (S_t - v k^T - sa b^T) / w~ from
+ * the last checkpoint, exactly like the reference (kernel.rs:239-246). Each
+ * rebuilt step multiplies the rounding error by 1/w~ >= 1, so the gradient
+ * error grows with chunk_len: about 4e-6 relative at chunk_len = 16, unusable
+ * beyond about 32. The reference uses chunk_len = 16 (time_mixer/mod.rs:190).
+ */
+#ifndef RWKV_RS_AMD_WKV7_H
+#define RWKV_RS_AMD_WKV7_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define WKV7_ABI_VERSION 1
+
+typedef enum wkv7_status {
+  WKV7_OK = 0,
+  WKV7_ERR_NULL_POINTER = 1, /* a required pointer is NULL */
+  WKV7_ERR_SHAPE = 2,        /* negative or out-of-range dimension */
+  WKV7_ERR_CHUNK_LEN = 3,    /* chunk_len <= 0 or does not divide context_len */
+  WKV7_ERR_HEAD_SIZE = 4,    /* head_size != 64 */
+  WKV7_ERR_DTYPE = 5,        /* unknown dtype code */
+  WKV7_ERR_ALIGNMENT = 6,    /* a tensor pointer is misaligned */
+  WKV7_ERR_OVERLAP = 7,      /* an output overlaps another operand */
+  WKV7_ERR_FLAGS = 8,        /* a flag is not 0/1 or contradicts a pointer */
+  WKV7_ERR_HIP = 9           /* the kernel launch failed */
+} wkv7_status;
+
+typedef enum wkv7_dtype { WKV7_DTYPE_F32 = 0, WKV7_DTYPE_BF16 = 1 } wkv7_dtype;
+
+/* Library facts and error reporting. */
+int wkv7_abi_version(void);
+const char *wkv7_strerror(int status);
+int wkv7_last_hip_error(void);
+
+/* Number of fp32 elements of the checkpoint ("state") tensor,
+ * batch * num_heads * (context_len / chunk_len) * head_size^2, or -1 when the
+ * arguments are invalid. */
+int64_t wkv7_checkpoint_numel(int64_t batch_size, int64_t context_len,
+                              int64_t num_heads, int64_t head_size,
+                              int64_t chunk_len);
+
+/* ---------------------------------------------------------------------------
+ * Generic forward: wkv7_forward_impl (wkv7_common/host.rs:29-183) with its two
+ * flags. use_initial_state = 0 starts from zeros (initial_state may be NULL);
+ * return_final_state = 0 skips final_state (may be NULL).
+ * Outputs: state (checkpoints), removal_state, output, final_state.
+ * ------------------------------------------------------------------------- */
+int wkv7_forward(const void *weight_decay, const void *receptance,
+                 const void *key, const void *value, const void *removal,
+                 const void *replacement, const float *initial_state,
+                 int64_t batch_size, int64_t context_len, int64_t num_heads,
+                 int64_t head_size, int64_t chunk_len, int dtype,
+                 int use_initial_state, int return_final_state, float *state,
+                 float *removal_state, void *output, float *final_state,
+                 void *stream);
+
+/* ---------------------------------------------------------------------------
+ * Generic backward: wkv7_backward_impl (wkv7_common/host.rs:185-369) with its
+ * two flags. use_final_state_grad = 0 starts from a zero state gradient
+ * (final_state_grad may be NULL); write_initial_state_grad = 0 skips
+ * initial_state_grad (may be NULL).
+ * ------------------------------------------------------------------------- */
+int wkv7_backward(const void *weight_decay, const void *receptance,
+                  const void *key, const void *value, const void *removal,
+                  const void *replacement, const float *state,
+                  const float *removal_state, const void *output_grad,
+                  const float *final_state_grad, int64_t batch_size,
+                  int64_t context_len, int64_t num_heads, int64_t head_size,
+                  int64_t chunk_len, int dtype, int use_final_state_grad,
+                  int write_initial_state_grad, void *weight_decay_grad,
+                  void *receptance_grad, void *key_grad, void *value_grad,
+                  void *removal_grad, void *replacement_grad,
+                  float *initial_state_grad, void *stream);
+
+/* Wkv7PretrainBackend (wkv7_pretrain/mod.rs:18-41; CubeBackend impl
+ * wkv7_pretrain/forward.rs:13-85): no initial state, no final state. */
+int wkv7_pretrain_forward(const void *weight_decay, const void *receptance,
+                          const void *key, const void *value,
+                          const void *removal, const void *replacement,
+                          int64_t batch_size, int64_t context_len,
+                          int64_t num_heads, int64_t head_size,
+                          int64_t chunk_len, int dtype, float *state,
+                          float *removal_state, void *output, void *stream);
+
+int wkv7_pretrain_backward(const void *weight_decay, const void *receptance,
+                           const void *key, const void *value,
+                           const void *removal, const void *replacement,
+                           const float *state, const float *removal_state,
+                           const void *output_grad, int64_t batch_size,
+                           int64_t context_len, int64_t num_heads,
+                           int64_t head_size, int64_t chunk_len, int dtype,
+                           void *weight_decay_grad, void *receptance_grad,
+                           void *key_grad, void *value_grad,
+                           void *removal_grad, void *replacement_grad,
+                           void *stream);
+
+/* Wkv7StatePassBackend (wkv7_statepass/mod.rs:18-43; CubeBackend impl
+ * wkv7_statepass/forward.rs:11-70): initial state in, final state out,
+ * final-state gradient in, initial-state gradient out. */
+int wkv7_statepass_forward(const void *weight_decay, const void *receptance,
+                           const void *key, const void *value,
+                           const void *removal, const void *replacement,
+                           const float *initial_state, int64_t batch_size,
+                           int64_t context_len, int64_t num_heads,
+                           int64_t head_size, int64_t chunk_len, int dtype,
+                           float *state, float *removal_state, void *output,
+                           float *final_state, void *stream);
+
+int wkv7_statepass_backward(const void *weight_decay, const void *receptance,
+                            const void *key, const void *value,
+                            const void *removal, const void *replacement,
+                            const float *state, const float *removal_state,
+                            const void *output_grad,
+                            const float *final_state_grad, int64_t batch_size,
+                            int64_t context_len, int64_t num_heads,
+                            int64_t head_size, int64_t chunk_len, int dtype,
+                            void *weight_decay_grad, void *receptance_grad,
+                            void *key_grad, void *value_grad,
+                            void *removal_grad, void *replacement_grad,
+                            float *initial_state_grad, void *stream);
+
+/* Wkv7StateTuneBackend (wkv7_statetune/mod.rs:18-42; CubeBackend impl
+ * wkv7_statetune/forward.rs:19-76): initial state in, no final state,
+ * initial-state gradient out. */
+int wkv7_statetune_forward(const void *weight_decay, const void *receptance,
+                           const void *key, const void *value,
+                           const void *removal, const void *replacement,
+                           const float *initial_state, int64_t batch_size,
+                           int64_t context_len, int64_t num_heads,
+                           int64_t head_size, int64_t chunk_len, int dtype,
+                           float *state, float *removal_state, void *output,
+                           void *stream);
+
+int wkv7_statetune_backward(const void *weight_decay, const void *receptance,
+                            const void *key, const void *value,
+                            const void *removal, const void *replacement,
+                            const float *state, const float *removal_state,
+                            const void *output_grad, int64_t batch_size,
+                            int64_t context_len, int64_t num_heads,
+                            int64_t head_size, int64_t chunk_len, int dtype,
+                            void *weight_decay_grad, void *receptance_grad,
+                            void *key_grad, void *value_grad,
+                            void *removal_grad, void *replacement_grad,
+                            float *initial_state_grad, void *stream);
+
+/* Wkv7InferBackend::wkv7_infer_forward (wkv7_infer/mod.rs:30-51; host
+ * wkv7_infer/host.rs:27-187). Per-token tensors are
+ * [active_batch_size, context_len, num_heads, 64]. Row b uses and updates, in
+ * place, slot batch_ids[b] of `state` ([full_batch_size, num_heads, 64, 64],
+ * fp32); batch_ids must be distinct and in [0, full_batch_size) (the reference
+ * asserts this in debug builds, examples/rwkv-lm/src/inferring.rs:224-234).
+ * context_mask ([active_batch_size, context_len] in dtype, NULL = all ones):
+ * a 0 entry gives output 0 and leaves the state untouched. use_dither = 1 adds
+ * the reference's deterministic dither (wkv7_infer/kernel.rs:8-13) seeded with
+ * elapsed_t[slot] + (unmasked steps so far); elapsed_t ([full_batch_size],
+ * read as uint32) may be NULL only when use_dither = 0. The reference turns
+ * the dither on exactly when its element type is not fp32
+ * (wkv7_infer/host.rs:157); here the state is always fp32 and the caller
+ * chooses. */
+int wkv7_infer_forward(const void *weight_decay, const void *receptance,
+                       const void *key, const void *value, const void *removal,
+                       const void *replacement, const int32_t *batch_ids,
+                       float *state, const void *context_mask,
+                       const int32_t *elapsed_t, int64_t active_batch_size,
+                       int64_t context_len, int64_t num_heads,
+                       int64_t head_size, int64_t full_batch_size, int dtype,
+                       int use_dither, void *output, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RWKV_RS_AMD_WKV7_H */

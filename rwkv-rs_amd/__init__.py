@@ -1,0 +1,17 @@
+"""MI355X-native WKV7 time-mix recurrence (forward, backward, decode) behind a
+C ABI (include/wkv7.h) that mirrors rwkv-nn's Burn WKV7 operator traits.
+
+* ``wkv7``      -- the operator API over torch device tensors (imports torch)
+* ``synthetic`` -- seeded operands with the benchmark's value distributions
+* ``build``     -- compiles libwkv7_hip.so for gfx950
+"""
+
+import importlib
+
+from . import synthetic  # noqa: F401
+
+
+def __getattr__(name):
+    if name in ("wkv7", "_native", "build"):
+        return importlib.import_module(f"{__name__}.{name}")
+    raise AttributeError(name)

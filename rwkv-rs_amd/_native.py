@@ -1,0 +1,94 @@
+"""ctypes binding of libwkv7_hip.so, the C ABI declared in include/wkv7.h.
+
+The library is built in-tree by rwkv-rs_amd/build.py. Loading fails loudly when
+it is missing: there is no fallback implementation.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libwkv7_hip.so")
+
+WKV7_OK = 0
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+
+STATUS_NAMES = {
+    0: "WKV7_OK", 1: "WKV7_ERR_NULL_POINTER", 2: "WKV7_ERR_SHAPE",
+    3: "WKV7_ERR_CHUNK_LEN", 4: "WKV7_ERR_HEAD_SIZE", 5: "WKV7_ERR_DTYPE",
+    6: "WKV7_ERR_ALIGNMENT", 7: "WKV7_ERR_OVERLAP", 8: "WKV7_ERR_FLAGS",
+    9: "WKV7_ERR_HIP",
+}
+
+# every symbol include/wkv7.h declares
+EXPORTS = (
+    "wkv7_abi_version", "wkv7_strerror", "wkv7_last_hip_error", "wkv7_checkpoint_numel",
+    "wkv7_forward", "wkv7_backward",
+    "wkv7_pretrain_forward", "wkv7_pretrain_backward",
+    "wkv7_statepass_forward", "wkv7_statepass_backward",
+    "wkv7_statetune_forward", "wkv7_statetune_backward",
+    "wkv7_infer_forward",
+)
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_INT = ctypes.c_int
+
+_SIGNATURES = {
+    "wkv7_abi_version": ([], _INT),
+    "wkv7_strerror": ([_INT], ctypes.c_char_p),
+    "wkv7_last_hip_error": ([], _INT),
+    "wkv7_checkpoint_numel": ([_I64] * 5, _I64),
+    "wkv7_forward": ([_P] * 7 + [_I64] * 5 + [_INT] * 3 + [_P] * 5, _INT),
+    "wkv7_backward": ([_P] * 10 + [_I64] * 5 + [_INT] * 3 + [_P] * 8, _INT),
+    "wkv7_pretrain_forward": ([_P] * 6 + [_I64] * 5 + [_INT] + [_P] * 4, _INT),
+    "wkv7_pretrain_backward": ([_P] * 9 + [_I64] * 5 + [_INT] + [_P] * 7, _INT),
+    "wkv7_statepass_forward": ([_P] * 7 + [_I64] * 5 + [_INT] + [_P] * 5, _INT),
+    "wkv7_statepass_backward": ([_P] * 10 + [_I64] * 5 + [_INT] + [_P] * 8, _INT),
+    "wkv7_statetune_forward": ([_P] * 7 + [_I64] * 5 + [_INT] + [_P] * 4, _INT),
+    "wkv7_statetune_backward": ([_P] * 9 + [_I64] * 5 + [_INT] + [_P] * 8, _INT),
+    "wkv7_infer_forward": ([_P] * 10 + [_I64] * 5 + [_INT] * 2 + [_P] * 2, _INT),
+}
+
+_lib = None
+
+
+class Wkv7Error(RuntimeError):
+    """A non-zero wkv7_status from the C ABI."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(f"{message} ({STATUS_NAMES.get(status, status)})")
+        self.status = status
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(
+            f"WKV7 HIP library not built: {LIB_PATH} is missing "
+            "(run `python rwkv-rs_amd/build.py`)")
+    handle = ctypes.CDLL(LIB_PATH)
+    for name, (args, res) in _SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.argtypes = args
+        fn.restype = res
+    _lib = handle
+    return handle
+
+
+def check(status: int) -> None:
+    if status != WKV7_OK:
+        l = lib()
+        msg = l.wkv7_strerror(status).decode()
+        if status == 9:
+            msg += f": hipError {l.wkv7_last_hip_error()}"
+        raise Wkv7Error(status, msg)
+
+
+def call(name: str, *args) -> None:
+    check(getattr(lib(), name)(*args))

@@ -1,0 +1,56 @@
+"""Build libwkv7_hip.so (the gfx950 kernels and their C ABI) in-tree.
+
+    python rwkv-rs_amd/build.py          # or __graft_entry__.build()
+
+hipcc cross-compiles for gfx950 without a GPU. Packed-FP32 instruction
+generation is switched off (-packed-fp32-ops): the kernels are written for
+scalar v_fmac_f32 with DPP operands, and packed FP32 forms are avoided on this
+hardware pool.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+LIB = os.path.join(HERE, "libwkv7_hip.so")
+SOURCES = ["wkv7_api.cpp", "wkv7_forward.hip", "wkv7_backward.hip", "wkv7_infer.hip"]
+ARCH = "gfx950"
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found (ROCm is required to build the WKV7 kernels)")
+
+
+def flags() -> list[str]:
+    return [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall",
+            "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+
+
+def build(verbose: bool = False) -> str:
+    """Compile every source and link the shared library. Always rebuilds."""
+    tmp = LIB + ".tmp"
+    cmd = [hipcc(), *flags(), "-shared", "-o", tmp,
+           *[os.path.join(CSRC, s) for s in SOURCES]]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "'-packed-fp32-ops' is not a recognized feature for this target"
+    err = "\n".join(l for l in res.stderr.splitlines() if noise not in l and "(ignoring feature)" not in l)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{err}")
+    if err.strip() and verbose:
+        print(err, file=sys.stderr)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

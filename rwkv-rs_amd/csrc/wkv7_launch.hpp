@@ -1,0 +1,57 @@
+// Internal launch interface between the C ABI (wkv7_api.cpp) and the kernels.
+// Shapes are validated by the ABI layer before any of these is called.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace wkv7 {
+
+constexpr int kHeadSize = 64;   // the kernels are specialised for N = 64
+
+enum class Dtype : int { F32 = 0, BF16 = 1 };
+
+// Forward pass, mirrors wkv7_forward_impl (wkv7_common/host.rs:29-183).
+struct ForwardDesc {
+  Dtype dtype;
+  int B, T, H, C;               // batch, context length, heads, chunk_len
+  const void *w, *r, *k, *v, *a, *b;   // [B,T,H,64] in dtype
+  const float* s0;              // [B,H,64,64] or nullptr (zeros)
+  float* ckpt;                  // [B,H,T/C,64,64], key-major (transposed)
+  float* sa;                    // [B,T,H,64] removal_state
+  void* y;                      // [B,T,H,64] in dtype
+  float* sT;                    // [B,H,64,64] or nullptr
+};
+
+// Backward pass, mirrors wkv7_backward_impl (wkv7_common/host.rs:185-369).
+struct BackwardDesc {
+  Dtype dtype;
+  int B, T, H, C;
+  const void *w, *r, *k, *v, *a, *b;   // [B,T,H,64] in dtype
+  const float* ckpt;            // [B,H,T/C,64,64]
+  const float* sa;              // [B,T,H,64]
+  const void* dy;               // [B,T,H,64] in dtype
+  const float* dsT;             // [B,H,64,64] or nullptr (zeros)
+  void *dw, *dr, *dk, *dv, *da, *db;   // [B,T,H,64] in dtype
+  float* ds0;                   // [B,H,64,64] or nullptr
+};
+
+// Slot-mapped inference, mirrors wkv7_infer_forward_impl
+// (wkv7_infer/host.rs:27-187).
+struct InferDesc {
+  Dtype dtype;
+  int Ba, T, H, full_batch;
+  const void *w, *r, *k, *v, *a, *b;   // [Ba,T,H,64] in dtype
+  const int32_t* batch_ids;     // [Ba], values in [0, full_batch)
+  float* state;                 // [full_batch,H,64,64], updated in place
+  const void* context_mask;     // [Ba,T] in dtype, or nullptr (all ones)
+  const int32_t* elapsed_t;     // [full_batch] (read as u32), or nullptr
+  int use_dither;
+  void* y;                      // [Ba,T,H,64] in dtype
+};
+
+hipError_t launch_forward(const ForwardDesc& d, hipStream_t stream);
+hipError_t launch_backward(const BackwardDesc& d, hipStream_t stream);
+hipError_t launch_infer(const InferDesc& d, hipStream_t stream);
+
+}  // namespace wkv7

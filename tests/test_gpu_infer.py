@@ -1,0 +1,104 @@
+"""GPU parity of the slot-mapped decode kernel (wkv7_infer_forward in
+include/wkv7.h) against the oracle restating
+/root/reference/crates/rwkv-nn/src/kernels/wkv7_infer/kernel.rs:15-114."""
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import NAMES, announce, load_pkg, rel_l2, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def wk():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return load_pkg().wkv7
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dither", [False, True])
+def test_decode_step_slot_mapped(wk, oracle, dtype, dither):
+    announce("infer T=1", dtype, dither)
+    pkg = load_pkg()
+    Ba, H, full = 6, 5, 11
+    d = pkg.synthetic.make_inputs(Ba, 1, H, 64, seed=31, bf16=(dtype == torch.bfloat16))
+    rng = np.random.default_rng(32)
+    state = (rng.standard_normal((full, H, 64, 64)) * 0.1).astype(np.float32)
+    ids = np.array([7, 0, 3, 10, 5, 1], np.int32)
+    elapsed = rng.integers(0, 1000, full).astype(np.int32)
+    st_gpu = to_dev(state)
+    out = wk.wkv7_infer_forward(*(to_dev(d[n], dtype) for n in NAMES), torch.from_numpy(ids).cuda(),
+                                st_gpu, None, torch.from_numpy(elapsed).cuda(), use_dither=dither)
+    st_ref = state.copy()
+    y_ref = oracle.infer_f32(*(d[n] for n in NAMES), ids, st_ref, None, elapsed.view(np.uint32),
+                             use_dither=dither)
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    if dtype == torch.bfloat16:
+        y_ref = pkg.synthetic.bf16_round(y_ref)
+    assert rel_l2(to_np(out.output), y_ref) < tol
+    assert out.final_state.data_ptr() == st_gpu.data_ptr()
+    assert rel_l2(to_np(st_gpu), st_ref) < 1e-5
+    untouched = [s for s in range(full) if s not in ids]
+    np.testing.assert_array_equal(to_np(st_gpu)[untouched], state[untouched])
+
+
+def test_prefill_with_mask_matches_oracle(wk, oracle):
+    announce("infer prefill with mask")
+    pkg = load_pkg()
+    Ba, T, H, full = 3, 37, 2, 4
+    d = pkg.synthetic.make_inputs(Ba, T, H, 64, seed=33)
+    rng = np.random.default_rng(34)
+    mask = (rng.random((Ba, T)) < 0.8).astype(np.float32)
+    mask[0, :5] = 0.0   # left padding
+    state = (rng.standard_normal((full, H, 64, 64)) * 0.1).astype(np.float32)
+    ids = np.array([2, 0, 3], np.int32)
+    elapsed = np.array([5, 17, 0, 9], np.int32)
+    st_gpu = to_dev(state)
+    out = wk.wkv7_infer_forward(*(to_dev(d[n]) for n in NAMES), torch.from_numpy(ids).cuda(), st_gpu,
+                                to_dev(mask), torch.from_numpy(elapsed).cuda(), use_dither=True)
+    st_ref = state.copy()
+    y_ref = oracle.infer_f32(*(d[n] for n in NAMES), ids, st_ref, mask, elapsed.view(np.uint32),
+                             use_dither=True)
+    y = to_np(out.output)
+    assert np.all(y[mask == 0] == 0.0)
+    assert rel_l2(y, y_ref) < 1e-5
+    assert rel_l2(to_np(st_gpu), st_ref) < 1e-5
+
+
+def test_masked_padding_is_a_noop(wk):
+    # wkv7_infer/mod.rs:189-230 at N=64: left padding with masked steps gives the
+    # unpadded outputs and state, dither on.
+    announce("infer padding no-op")
+    pkg = load_pkg()
+    H = 3
+    d = pkg.synthetic.make_inputs(1, 6, H, 64, seed=35)
+    pad = pkg.synthetic.make_inputs(1, 2, H, 64, seed=36)
+    padded = {n: np.concatenate([pad[n], d[n]], 1) for n in NAMES}
+    mask_p = np.array([[0, 0, 1, 1, 1, 1, 1, 1]], np.float32)
+    et = torch.tensor([17], dtype=torch.int32, device="cuda")
+    ids = torch.tensor([0], dtype=torch.int32, device="cuda")
+    s_u = torch.zeros(1, H, 64, 64, device="cuda")
+    s_p = torch.zeros(1, H, 64, 64, device="cuda")
+    y_u = wk.wkv7_infer_forward(*(to_dev(d[n]) for n in NAMES), ids, s_u, None, et, use_dither=True).output
+    y_p = wk.wkv7_infer_forward(*(to_dev(padded[n]) for n in NAMES), ids, s_p, to_dev(mask_p), et,
+                                use_dither=True).output
+    assert torch.all(y_p[:, :2] == 0)
+    assert torch.equal(y_p[:, 2:], y_u)
+    assert torch.equal(s_p, s_u)
+
+
+def test_decode_matches_forward_step(wk):
+    # T = 1 infer without dither equals one step of the training forward
+    announce("infer == forward step")
+    d = load_pkg().synthetic.make_inputs(4, 1, 3, 64, seed=37, s0_std=0.1)
+    ins = [to_dev(d[n]) for n in NAMES]
+    s0 = to_dev(d["s0"])
+    fwd = wk.wkv7_statepass_forward(*ins, s0, 1)
+    st = s0.clone()
+    out = wk.wkv7_infer_forward(*ins, torch.arange(4, dtype=torch.int32, device="cuda"), st, None,
+                                torch.zeros(4, dtype=torch.int32, device="cuda"))
+    assert torch.equal(out.output, fwd.output)
+    assert torch.equal(st, fwd.final_state)

@@ -1,0 +1,218 @@
+"""GPU parity of the gfx950 kernels (called through the C ABI in
+include/wkv7.h via the rwkv-rs_amd.wkv7 mirror) against the CPU oracle, which
+restates /root/reference/crates/rwkv-nn/src/kernels/wkv7_common/kernel.rs.
+
+Tolerances: fp32 inputs, relative L2 <= 1e-5 per
+tensor; bf16 inputs with fp32 state, relative L2 <= 1e-2 per tensor for the
+bf16 outputs (the fp32 state-family outputs are held to 1e-5)."""
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import GRAD_NAMES, NAMES, announce, load_pkg, rel_l2, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = 1e-5
+BF16_TOL = 1e-2
+
+
+@pytest.fixture(scope="module")
+def wk():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return load_pkg().wkv7
+
+
+def run_gpu(wk, d, chunk_len, dtype, s0=True, dsT=None):
+    ins = [to_dev(d[n], dtype) for n in NAMES]
+    s0_t = to_dev(d["s0"]) if (s0 and d["s0"] is not None) else None
+    if s0_t is None:
+        s0_t = torch.zeros(ins[0].shape[0], ins[0].shape[2], 64, 64, device="cuda")
+    fwd = wk.wkv7_statepass_forward(*ins, s0_t, chunk_len)
+    dy = to_dev(d["dy"], dtype)
+    dsT_t = to_dev(dsT) if dsT is not None else torch.zeros_like(s0_t)
+    bwd = wk.wkv7_statepass_backward(*ins, fwd.state, fwd.removal_state, dy, dsT_t, chunk_len)
+    torch.cuda.synchronize()
+    return fwd, bwd
+
+
+def run_oracle(oracle, d, chunk_len, dsT=None):
+    ins = [d[n] for n in NAMES]
+    fwd = oracle.forward_f32(*ins, s0=d["s0"], chunk_len=chunk_len)
+    bwd = oracle.backward_f32(*ins, fwd["state"], fwd["removal_state"], d["dy"],
+                              ds_T=dsT, chunk_len=chunk_len)
+    return fwd, bwd
+
+
+def compare(fwd, bwd, ofwd, obwd, tok_tol, label):
+    errs = {
+        "output": rel_l2(to_np(fwd.output), ofwd["output"]),
+        "removal_state": rel_l2(to_np(fwd.removal_state), ofwd["removal_state"]),
+        "state": rel_l2(to_np(fwd.state), ofwd["state"]),
+        "final_state": rel_l2(to_np(fwd.final_state), ofwd["final_state"]),
+        "initial_state_grad": rel_l2(to_np(bwd.initial_state_grad), obwd["initial_state_grad"]),
+    }
+    for gn in GRAD_NAMES:
+        errs[gn] = rel_l2(to_np(getattr(bwd, gn)), obwd[gn])
+    print(label, {k: f"{v:.2e}" for k, v in errs.items()}, flush=True)
+    tok = ("output",) + GRAD_NAMES
+    for key, err in errs.items():
+        assert err <= (tok_tol if key in tok else FP32_TOL), (label, key, err)
+    return errs
+
+
+@pytest.mark.parametrize("case", [
+    # (B, T, H, chunk_len, s0_std, with_dsT, seed)
+    (1, 64, 4, 16, None, False, 0),      # config[0]
+    (1, 64, 4, 16, 0.1, True, 1),
+    (2, 48, 3, 16, 0.1, True, 2),
+    (1, 64, 2, 8, None, True, 3),
+    (1, 32, 2, 1, 0.1, True, 4),
+    (1, 24, 2, 8, 0.1, False, 5),        # T not a multiple of the 16-step tile
+    (1, 20, 1, 4, None, True, 6),
+    (3, 1, 5, 1, 0.1, True, 7),          # single step
+])
+def test_fp32_forward_backward_matches_oracle(wk, oracle, case):
+    B, T, H, C, s0_std, with_dsT, seed = case
+    announce("fp32 fwd+bwd", case)
+    d = load_pkg().synthetic.make_inputs(B, T, H, 64, seed=seed, s0_std=s0_std)
+    dsT = (np.random.default_rng(seed + 50).standard_normal((B, H, 64, 64)).astype(np.float32)
+           if with_dsT else None)
+    if d["s0"] is None:
+        d["s0"] = np.zeros((B, H, 64, 64), np.float32)
+    fwd, bwd = run_gpu(wk, d, C, torch.float32, dsT=dsT)
+    ofwd, obwd = run_oracle(oracle, d, C, dsT=dsT)
+    compare(fwd, bwd, ofwd, obwd, FP32_TOL, f"fp32 {case}")
+
+
+def test_fp32_gradients_match_fp64(wk, oracle):
+    # the kernel against exact (fp64, stored-state) gradients at config[0]
+    announce("fp32 vs fp64 grads, config[0]")
+    d = load_pkg().synthetic.make_inputs(1, 64, 4, 64, seed=0)
+    d["s0"] = np.zeros((1, 4, 64, 64), np.float32)
+    fwd, bwd = run_gpu(wk, d, 16, torch.float32)
+    ref = oracle.grad_f64(*(d[n] for n in NAMES), d["s0"], d["dy"])
+    f64 = oracle.forward_f64(*(d[n] for n in NAMES), s0=d["s0"])
+    assert rel_l2(to_np(fwd.output), f64["output"]) < FP32_TOL
+    for gn in GRAD_NAMES + ("initial_state_grad",):
+        err = rel_l2(to_np(getattr(bwd, gn)), ref[gn])
+        assert err < FP32_TOL, (gn, err)
+
+
+@pytest.mark.parametrize("case", [(2, 128, 4, 16, 0.1, 11), (1, 64, 4, 16, None, 12)])
+def test_bf16_inputs_fp32_state(wk, oracle, case):
+    B, T, H, C, s0_std, seed = case
+    announce("bf16 fwd+bwd", case)
+    pkg = load_pkg()
+    d = pkg.synthetic.make_inputs(B, T, H, 64, seed=seed, s0_std=s0_std, bf16=True)
+    if d["s0"] is None:
+        d["s0"] = np.zeros((B, H, 64, 64), np.float32)
+    fwd, bwd = run_gpu(wk, d, C, torch.bfloat16)
+    assert fwd.output.dtype == torch.bfloat16 and fwd.state.dtype == torch.float32
+    assert bwd.key_grad.dtype == torch.bfloat16 and bwd.initial_state_grad.dtype == torch.float32
+    ofwd, obwd = run_oracle(oracle, d, C)
+    # the reference casts y and the six gradients back to bf16 (host.rs:58-62, 221-228)
+    ofwd["output"] = pkg.synthetic.bf16_round(ofwd["output"])
+    for gn in GRAD_NAMES:
+        obwd[gn] = pkg.synthetic.bf16_round(obwd[gn])
+    compare(fwd, bwd, ofwd, obwd, BF16_TOL, f"bf16 {case}")
+
+
+def test_variants_agree(wk):
+    # pretrain == statepass(s0 = 0) == statetune(s0 = 0) on y and the six gradients
+    announce("variant equivalence")
+    pkg = load_pkg()
+    d = pkg.synthetic.make_inputs(2, 32, 3, 64, seed=21)
+    ins = [to_dev(d[n]) for n in NAMES]
+    dy = to_dev(d["dy"])
+    z = torch.zeros(2, 3, 64, 64, device="cuda")
+    inp = wk.Wkv7ForwardInput(receptance=ins[1], weight_decay=ins[0], replacement_key=ins[2],
+                              value=ins[3], removal_key_normalized=ins[4], replacement=ins[5])
+    pre = wk.wkv7_pretrain_forward(inp, 16)
+    sp = wk.wkv7_statepass_forward(*ins, z, 16)
+    st = wk.wkv7_statetune_forward(*ins, z, 16)
+    for o in (sp, st):
+        assert torch.equal(o.output, pre.output) and torch.equal(o.state, pre.state)
+        assert torch.equal(o.removal_state, pre.removal_state)
+    gp = wk.wkv7_pretrain_backward(*ins, pre.state, pre.removal_state, dy, 16)
+    gs = wk.wkv7_statepass_backward(*ins, sp.state, sp.removal_state, dy, z, 16)
+    gt = wk.wkv7_statetune_backward(*ins, st.state, st.removal_state, dy, 16)
+    for gn in GRAD_NAMES:
+        assert torch.equal(getattr(gs, gn), getattr(gp, gn)), gn
+        assert torch.equal(getattr(gt, gn), getattr(gp, gn)), gn
+    assert torch.equal(gs.initial_state_grad, gt.initial_state_grad)
+
+
+def test_sequence_split_is_exact(wk):
+    # statepass contract (model.rs:368-409): two halves with s_T -> s0 equal one run
+    announce("split invariance")
+    d = load_pkg().synthetic.make_inputs(2, 64, 2, 64, seed=22, s0_std=0.1)
+    ins = [to_dev(d[n]) for n in NAMES]
+    s0 = to_dev(d["s0"])
+    full = wk.wkv7_statepass_forward(*ins, s0, 16)
+    a = wk.wkv7_statepass_forward(*(x[:, :32] for x in ins), s0, 16)
+    b = wk.wkv7_statepass_forward(*(x[:, 32:] for x in ins), a.final_state, 16)
+    assert torch.equal(torch.cat([a.output, b.output], 1), full.output)
+    assert torch.equal(b.final_state, full.final_state)
+
+
+def test_empty_sequence(wk):
+    # T = 0: final state = initial state, initial-state grad = final-state grad
+    announce("T=0")
+    B, H = 2, 3
+    e = torch.empty(B, 0, H, 64, device="cuda")
+    s0 = torch.randn(B, H, 64, 64, device="cuda")
+    out = wk.wkv7_statepass_forward(e, e, e, e, e, e, s0, 16)
+    assert out.output.shape == (B, 0, H, 64) and out.state.shape == (B, H, 0, 64, 64)
+    assert torch.equal(out.final_state, s0)
+    dsT = torch.randn(B, H, 64, 64, device="cuda")
+    g = wk.wkv7_statepass_backward(e, e, e, e, e, e, out.state, out.removal_state, e, dsT, 16)
+    assert torch.equal(g.initial_state_grad, dsT)
+
+
+def test_autograd_matches_direct_backward(wk):
+    announce("autograd")
+    d = load_pkg().synthetic.make_inputs(1, 32, 2, 64, seed=23, s0_std=0.1)
+    ins = [to_dev(d[n]).requires_grad_(True) for n in NAMES]
+    s0 = to_dev(d["s0"]).requires_grad_(True)
+    dy = to_dev(d["dy"])
+    y, sT = wk.Wkv7StatePassFunction.apply(*ins, s0, 16)
+    y.backward(dy)
+    direct_f = wk.wkv7_statepass_forward(*(x.detach() for x in ins), s0.detach(), 16)
+    direct = wk.wkv7_statepass_backward(*(x.detach() for x in ins), direct_f.state,
+                                        direct_f.removal_state, dy, torch.zeros_like(s0), 16)
+    for x, gn in zip(ins, GRAD_NAMES):
+        assert torch.equal(x.grad, getattr(direct, gn)), gn
+    assert torch.equal(s0.grad, direct.initial_state_grad)
+    assert torch.equal(sT, direct_f.final_state)
+
+
+def test_full_size_config1_sampled_heads(wk, oracle):
+    # BASELINE config[1] at full size (B=8, T=4096, H=32, bf16, s0 ~ N(0, 0.1)):
+    # two (b, h) pairs, first and last, checked against the oracle over all 4096
+    # steps, and the checkpoint of the last chunk equals the transposed final state.
+    announce("config[1] full size, sampled heads")
+    pkg = load_pkg()
+    B, T, H = 8, 4096, 32
+    t = pkg.synthetic.make_inputs_torch(B, T, H, seed=0x5EED0001, s0_std=0.1, dtype=torch.bfloat16)
+    ins = [t[n] for n in NAMES]
+    fwd = wk.wkv7_statepass_forward(*ins, t["s0"], 16)
+    bwd = wk.wkv7_statepass_backward(*ins, fwd.state, fwd.removal_state, t["dy"],
+                                     torch.zeros_like(t["s0"]), 16)
+    torch.cuda.synchronize()
+    assert torch.equal(fwd.state[:, :, -1], fwd.final_state.transpose(-1, -2))
+    for bi, h in ((0, 0), (B - 1, H - 1)):
+        sl = lambda x: to_np(x[bi:bi + 1, :, h:h + 1])
+        ins_np = [sl(x) for x in ins]
+        s0 = to_np(t["s0"][bi:bi + 1, h:h + 1])
+        of = oracle.forward_f32(*ins_np, s0=s0, chunk_len=16)
+        ob = oracle.backward_f32(*ins_np, of["state"], of["removal_state"], sl(t["dy"]), chunk_len=16)
+        assert rel_l2(sl(fwd.output), pkg.synthetic.bf16_round(of["output"])) < BF16_TOL
+        assert rel_l2(to_np(fwd.final_state[bi:bi + 1, h:h + 1]), of["final_state"]) < FP32_TOL
+        for gn in GRAD_NAMES:
+            err = rel_l2(sl(getattr(bwd, gn)), pkg.synthetic.bf16_round(ob[gn]))
+            assert err < BF16_TOL, (bi, h, gn, err)
+        err = rel_l2(to_np(bwd.initial_state_grad[bi:bi + 1, h:h + 1]), ob["initial_state_grad"])
+        assert err < FP32_TOL, (bi, h, err)
