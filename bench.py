@@ -1,0 +1,264 @@
+"""WKV7 fwd+bwd benchmark on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg1|cfg2|cfg3|cfg0]
+
+A step is one forward and one backward pass of the WKV7 statepass operator
+(initial state in, final-state gradient zero, 16-step checkpoints) over one
+batch of synthetic operands, called through the C ABI with device-resident
+buffers allocated once. The default workload is BASELINE config[1]:
+B=8, T=4096, H=32, N=64, bf16 operands, fp32 state and arithmetic,
+initial state ~ N(0, 0.1).
+
+Printed JSON line: whole-job Mtokens/s, ms per step, the roofline of the
+dominant kernel (the backward: algorithmic FLOPs per launch / mean launch time
+from HIP events recorded on the launch stream, against the MI355X FP32 vector
+peak), and the CPU baseline (the oracle's reference-order fp32 restatement,
+OpenMP over (batch, head) pairs, timed on a bounded sample of the same
+workload on the host cores). config cfg3 is the batched decode step (T=1),
+which is HBM-bound.
+"""
+
+from __future__ import annotations
+
+import argparse
+import importlib
+import json
+import os
+import sys
+import time
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, HERE)
+
+N_HEAD = 64
+FLOP_FWD = 9 * N_HEAD * N_HEAD      # per head-step: sa 2N^2, update 5N^2, y 2N^2
+FLOP_BWD = 24 * N_HEAD * N_HEAD     # per head-step, non-redundant backward
+PEAK_FP32 = 157.3e12                # MI355X FP32 vector peak (packed issue)
+PEAK_HBM = 8.0e12                   # MI355X HBM3E
+METRIC = "WKV7 fwd+bwd Mtokens/s (B=8,T=4096,C=2048) + % FP32-VALU / HBM roofline"
+
+CONFIGS = {
+    "cfg0": dict(B=1, T=64, H=4, io="f32", s0_std=None),
+    "cfg1": dict(B=8, T=4096, H=32, io="bf16", s0_std=0.1),
+    "cfg2": dict(B=4, T=4096, H=64, io="bf16", s0_std=None),
+    "cfg3": dict(B=256, T=1, H=40, io="bf16", s0_std=0.1),
+}
+
+
+def cpu_cores() -> int:
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))   # the box's CPU share for one GPU is 16
+
+
+def cpu_baseline(cfg, seconds_target=12.0):
+    """Oracle (reference-order fp32 restatement) on a bounded sample of the
+    workload: whole sequences of a few (batch, head) pairs, OpenMP over pairs."""
+    import numpy as np
+
+    import oracle
+    pkg = importlib.import_module("rwkv-rs_amd")
+    B, T, H = cfg["B"], cfg["T"], cfg["H"]
+    cores = cpu_cores()
+    names = ("w", "r", "k", "v", "a", "b")
+
+    d = pkg.synthetic.make_inputs(1, T, cores, N_HEAD, seed=7, s0_std=0.1,
+                                  bf16=cfg["io"] == "bf16")
+    ins = [d[n] for n in names]
+
+    def run():
+        t0 = time.perf_counter()
+        f = oracle.forward_f32(*ins, s0=d["s0"], chunk_len=16, nthreads=cores)
+        oracle.backward_f32(*ins, f["state"], f["removal_state"], d["dy"], chunk_len=16,
+                            nthreads=cores)
+        return time.perf_counter() - t0
+
+    # one (batch, head) pair per core; repeat the pass to ~seconds_target
+    dt1 = run()
+    reps = max(1, int(round(seconds_target / max(dt1, 1e-3))))
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        run()
+    dt = time.perf_counter() - t0
+    nheads = reps * cores
+    tokens = nheads * T / H   # one token covers all H heads
+    return {"value": tokens / dt / 1e6, "unit": "Mtokens/s", "cores": cores,
+            "kind": "port",
+            "sample": f"{nheads} (batch, head) pairs x T={T}, fwd+bwd, chunk 16, "
+                      f"{dt:.1f} s on {cores} threads (oracle/wkv7_oracle.c, reference order)"}
+
+
+def bench_train(cfg, steps, warmup, with_cpu):
+    import torch
+    pkg = importlib.import_module("rwkv-rs_amd")
+    native = importlib.import_module("rwkv-rs_amd._native")
+    lib = native.lib()
+    B, T, H, C = cfg["B"], cfg["T"], cfg["H"], 16
+    io = torch.bfloat16 if cfg["io"] == "bf16" else torch.float32
+    dev = torch.device("cuda:0")
+    d = pkg.synthetic.make_inputs_torch(B, T, H, N_HEAD, seed=0x5EED0001, s0_std=cfg["s0_std"],
+                                        dtype=io, device=dev)
+    s0 = d["s0"] if d["s0"] is not None else torch.zeros(B, H, N_HEAD, N_HEAD, device=dev)
+    names = ("w", "r", "k", "v", "a", "b")
+    ins = [d[n].data_ptr() for n in names]
+    ckpt = torch.empty(B, H, T // C, N_HEAD, N_HEAD, device=dev)
+    sa = torch.empty(B, T, H, N_HEAD, device=dev)
+    y = torch.empty(B, T, H, N_HEAD, device=dev, dtype=io)
+    sT = torch.empty_like(s0)
+    dsT = torch.zeros_like(s0)
+    grads = [torch.empty(B, T, H, N_HEAD, device=dev, dtype=io) for _ in range(6)]
+    ds0 = torch.empty_like(s0)
+    dtype_code = native.DTYPE_BF16 if io == torch.bfloat16 else native.DTYPE_F32
+    stream = torch.cuda.current_stream(dev)
+    sp = stream.cuda_stream
+
+    def fwd():
+        native.check(lib.wkv7_statepass_forward(*ins, s0.data_ptr(), B, T, H, N_HEAD, C,
+                                                dtype_code, ckpt.data_ptr(), sa.data_ptr(),
+                                                y.data_ptr(), sT.data_ptr(), sp))
+
+    def bwd():
+        native.check(lib.wkv7_statepass_backward(*ins, ckpt.data_ptr(), sa.data_ptr(),
+                                                 d["dy"].data_ptr(), dsT.data_ptr(), B, T, H,
+                                                 N_HEAD, C, dtype_code,
+                                                 *(g.data_ptr() for g in grads),
+                                                 ds0.data_ptr(), sp))
+
+    for _ in range(warmup):
+        fwd()
+        bwd()
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
+           torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for e0, e1, e2 in ev:
+        e0.record(stream)
+        fwd()
+        e1.record(stream)
+        bwd()
+        e2.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    fwd_ms = sum(a.elapsed_time(b) for a, b, _ in ev) / steps
+    bwd_ms = sum(b.elapsed_time(c) for _, b, c in ev) / steps
+    ms_per_step = wall * 1e3 / steps
+    head_steps = B * T * H
+    tok = B * T
+    bwd_flops = FLOP_BWD * head_steps
+    fwd_flops = FLOP_FWD * head_steps
+    achieved = bwd_flops / (bwd_ms * 1e-3)
+    # algorithmic HBM bytes per head-step (bf16 io): fwd 7 vectors in/out + sa
+    # out + 1/16 of a checkpoint; bwd 7 vectors + sa in, 6 gradients out,
+    # 1/16 of a checkpoint in
+    e = 2 if io == torch.bfloat16 else 4
+    fwd_bytes = head_steps * (7 * N_HEAD * e + N_HEAD * 4 + N_HEAD * N_HEAD * 4 / C)
+    bwd_bytes = head_steps * (13 * N_HEAD * e + N_HEAD * 4 + N_HEAD * N_HEAD * 4 / C)
+    out = {
+        "metric": METRIC,
+        "value": tok / (ms_per_step * 1e-3) / 1e6,
+        "unit": "Mtokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "wkv7_statepass_fwd_bwd", "batch": B, "context_len": T,
+                   "num_heads": H, "head_size": N_HEAD, "chunk_len": C, "io_dtype": cfg["io"],
+                   "state_dtype": "f32", "initial_state_std": cfg["s0_std"]},
+        "roofline": {"bound": "valu", "kernel": "wkv7_bwd_kernel", "achieved": achieved / 1e12,
+                     "peak": PEAK_FP32 / 1e12, "unit": "TFLOP/s", "frac": achieved / PEAK_FP32,
+                     "traffic": None, "algorithmic_bytes": bwd_bytes,
+                     "flop_per_launch": bwd_flops, "launch_ms": bwd_ms},
+        "fwd_ms": fwd_ms,
+        "bwd_ms": bwd_ms,
+        "fwd_roofline_frac": fwd_flops / (fwd_ms * 1e-3) / PEAK_FP32,
+        "fwd_bwd_roofline_frac": (fwd_flops + bwd_flops) / ((fwd_ms + bwd_ms) * 1e-3) / PEAK_FP32,
+        "fwd_hbm_frac_algorithmic": fwd_bytes / (fwd_ms * 1e-3) / PEAK_HBM,
+        "bwd_hbm_frac_algorithmic": bwd_bytes / (bwd_ms * 1e-3) / PEAK_HBM,
+    }
+    if with_cpu:
+        out["cpu_baseline"] = cpu_baseline(cfg)
+    return out
+
+
+def bench_decode(cfg, steps, warmup):
+    import torch
+    pkg = importlib.import_module("rwkv-rs_amd")
+    native = importlib.import_module("rwkv-rs_amd._native")
+    lib = native.lib()
+    B, T, H = cfg["B"], cfg["T"], cfg["H"]
+    dev = torch.device("cuda:0")
+    d = pkg.synthetic.make_inputs_torch(B, T, H, N_HEAD, seed=0x5EED0003, s0_std=0.1,
+                                        dtype=torch.bfloat16, device=dev)
+    state = d["s0"].contiguous()
+    ids = torch.arange(B, dtype=torch.int32, device=dev)
+    et = torch.zeros(B, dtype=torch.int32, device=dev)
+    y = torch.empty(B, T, H, N_HEAD, device=dev, dtype=torch.bfloat16)
+    names = ("w", "r", "k", "v", "a", "b")
+    stream = torch.cuda.current_stream(dev)
+
+    def step():
+        native.check(lib.wkv7_infer_forward(*(d[n].data_ptr() for n in names), ids.data_ptr(),
+                                            state.data_ptr(), None, et.data_ptr(), B, T, H,
+                                            N_HEAD, B, native.DTYPE_BF16, 0, y.data_ptr(),
+                                            stream.cuda_stream))
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    launch_ms = e0.elapsed_time(e1) / steps
+    nbytes = B * H * (2 * N_HEAD * N_HEAD * 4 + 7 * T * N_HEAD * 2)
+    return {
+        "metric": "WKV7 batched decode Mtokens/s (B=256, T=1, H=40)",
+        "value": B * T / (wall / steps) / 1e6, "unit": "Mtokens/s", "n_gpus": 1,
+        "steps": steps, "warmup": warmup, "ms_per_step": wall * 1e3 / steps,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "wkv7_infer_decode", "batch": B, "context_len": T,
+                   "num_heads": H, "head_size": N_HEAD, "io_dtype": "bf16", "state_dtype": "f32"},
+        "roofline": {"bound": "hbm", "kernel": "wkv7_infer_kernel",
+                     "achieved": nbytes / (launch_ms * 1e-3) / 1e9, "peak": PEAK_HBM / 1e9,
+                     "unit": "GB/s", "frac": nbytes / (launch_ms * 1e-3) / PEAK_HBM,
+                     "traffic": None, "launch_ms": launch_ms},
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="cfg1", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the WKV7 operator needs no collective and "
+              "this build runs on single-GPU boxes (see DESIGN.md for how it shards)",
+              file=sys.stderr)
+        sys.exit(2)
+    cfg = CONFIGS[args.config]
+    if args.config == "cfg3":
+        out = bench_decode(cfg, args.steps, args.warmup)
+    else:
+        out = bench_train(cfg, args.steps, args.warmup,
+                          with_cpu=(not args.no_cpu and args.config == "cfg1"))
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -14,207 +14,46 @@
 //   dS     = dS diag(w~) + dsa a^T                                  (:289-296)
 //   ds0    = dS after t = 0                                         (:299-307)
 //
-// Design. One 256-thread workgroup per (b, h). Every thread has an own index
-// e = 16*wave + 4*g + lo and a segment hi (see wkv7_device.hpp) and plays two
-// roles at once:
-//   row role:    dSr[m] = dS[e][16*hi+m]   -> row sums dv_e and dsa_e
-//   column role: Sc[m]  = S[16*hi+m][e], dSc[m] = dS[16*hi+m][e]
-//                -> column sums dr_e, dw~_e, dk_e, db_e, da_e
-// so every sum is 16 in-lane products plus a 2-step DPP reduction over the
-// four segments, and the operand that varies along the summed index always
-// arrives as a DPP quad broadcast. Keeping dS twice (row and column layout)
-// costs 3 instructions per element per step; the alternative, cross-wave
-// reductions of the five column sums, costs more. The only data exchanged
-// between waves is dsa (64 floats, needed by the column role): one LDS vector
-// and one barrier per step, whose latency is covered by the column-role work
-// scheduled between the write and the barrier.
+// Design. One 512-thread workgroup per (b, h). Thread tid = 16*q + L plays two
+// roles on two transposed 2x4 blocks (layout in wkv7_device.hpp):
+//   row role:    dSr[d][c] = dS[2q+d][4L+c]   -> row sums dv, dsa of rows 2q, 2q+1
+//   column role: Sc[c][d]  = S[4L+c][2q+d],
+//                dSc[c][d] = dS[4L+c][2q+d]   -> column sums dr, dw~, dk, db, da
+//                                                of columns 2q, 2q+1
+// The sixteen lanes of a DPP row (same q) span all 64 columns in the row role
+// and all 64 rows in the column role, so every sum is in-lane products plus a
+// DPP reduction over the row; sums that are only written out use a
+// reduce-scatter (one lane per value) instead of a full reduction. Keeping dS
+// twice costs 3 instructions per element per step; reducing the five column
+// sums across waves instead would cost more. Every operand arrives as one
+// ds_read_b128 of an LDS vector (the thread's four columns for the row role,
+// its four rows for the column role) or of a packed per-column-pair record,
+// consumed by plain full-rate FMAs. The only data exchanged between waves is
+// dsa (64 floats, needed by the column role): one LDS vector and one barrier
+// per step, with the column-role work scheduled between write and barrier.
 #include "wkv7_device.hpp"
 #include "wkv7_launch.hpp"
 
 namespace wkv7 {
 namespace {
 
-constexpr int kTile = 16;   // timesteps per LDS tile
+constexpr int kTile = 8;   // timesteps per LDS tile
 
-// LDS vectors per timestep (fp32)
+// LDS vectors per timestep (fp32, 64 entries)
 enum {
-  V_R = 0, V_K, V_B, V_W, V_A,   // key-indexed (row role broadcasts these)
-  V_DY, V_V, V_SA,               // value-indexed (column role broadcasts these)
-  V_IW,                          // 1 / w~
-  V_DWF,                         // W_SCALE * w~ * sig * (1 - sig)
+  V_R = 0, V_K, V_B, V_W, V_A,   // key-indexed: row role
+  V_DY, V_V, V_SA,               // value-indexed: column role (dy also row role)
+  V_DWF,                         // W_SCALE * w~ * sig * (1 - sig), used at the flush
   V_COUNT
 };
-// staged outputs per timestep
-enum { O_DW = 0, O_DR, O_DK, O_DV, O_DA, O_DB, O_COUNT };
+// per-column-pair records for the column role, float4 {x[2p], x[2p+1], y[2p], y[2p+1]}
+enum { P_RK = 0, P_BW, P_AI, P_COUNT };   // {r, k}, {b, w~}, {a, 1/w~}
+// staged outputs per timestep, in the order the reduce-scatters deliver them
+enum { O_DV = 0, O_DR, O_DW, O_DK, O_DB, O_DA, O_COUNT };
 
-// Row role, 8 columns m = 4*S0 .. 4*S0+7 (quad lanes S0, S0+1):
-//   dSr[m] += dy_e * r[m];  dv += dSr[m] * k[m];  dsa += dSr[m] * b[m]
-#define WKV7_DEF_ROW1(S0, S1)                                                        \
-  __device__ __forceinline__ void row1_q##S0(float* d, float& v0, float& v1,         \
-                                             float& s0, float& s1, float4 r,          \
-                                             float4 k, float4 b, float dye) {         \
-    asm("s_nop 1\n\t"                                                                 \
-        "v_fmac_f32_dpp %0, %12, %24" WKV7_QP(S0)                                     \
-        "v_fmac_f32_dpp %1, %13, %24" WKV7_QP(S0)                                     \
-        "v_fmac_f32_dpp %2, %14, %24" WKV7_QP(S0)                                     \
-        "v_fmac_f32_dpp %3, %15, %24" WKV7_QP(S0)                                     \
-        "v_fmac_f32_dpp %4, %12, %24" WKV7_QP(S1)                                     \
-        "v_fmac_f32_dpp %5, %13, %24" WKV7_QP(S1)                                     \
-        "v_fmac_f32_dpp %6, %14, %24" WKV7_QP(S1)                                     \
-        "v_fmac_f32_dpp %7, %15, %24" WKV7_QP(S1)                                     \
-        "v_fmac_f32_dpp %8, %16, %0" WKV7_QP(S0)                                      \
-        "v_fmac_f32_dpp %9, %17, %1" WKV7_QP(S0)                                      \
-        "v_fmac_f32_dpp %8, %18, %2" WKV7_QP(S0)                                      \
-        "v_fmac_f32_dpp %9, %19, %3" WKV7_QP(S0)                                      \
-        "v_fmac_f32_dpp %8, %16, %4" WKV7_QP(S1)                                      \
-        "v_fmac_f32_dpp %9, %17, %5" WKV7_QP(S1)                                      \
-        "v_fmac_f32_dpp %8, %18, %6" WKV7_QP(S1)                                      \
-        "v_fmac_f32_dpp %9, %19, %7" WKV7_QP(S1)                                      \
-        "v_fmac_f32_dpp %10, %20, %0" WKV7_QP(S0)                                     \
-        "v_fmac_f32_dpp %11, %21, %1" WKV7_QP(S0)                                     \
-        "v_fmac_f32_dpp %10, %22, %2" WKV7_QP(S0)                                     \
-        "v_fmac_f32_dpp %11, %23, %3" WKV7_QP(S0)                                     \
-        "v_fmac_f32_dpp %10, %20, %4" WKV7_QP(S1)                                     \
-        "v_fmac_f32_dpp %11, %21, %5" WKV7_QP(S1)                                     \
-        "v_fmac_f32_dpp %10, %22, %6" WKV7_QP(S1)                                     \
-        "v_fmac_f32_dpp %11, %23, %7" WKV7_QP(S1)                                     \
-        : "+v"(d[0]), "+v"(d[1]), "+v"(d[2]), "+v"(d[3]), "+v"(d[4]), "+v"(d[5]),    \
-          "+v"(d[6]), "+v"(d[7]), "+v"(v0), "+v"(v1), "+v"(s0), "+v"(s1)              \
-        : "v"(r.x), "v"(r.y), "v"(r.z), "v"(r.w), "v"(k.x), "v"(k.y), "v"(k.z),       \
-          "v"(k.w), "v"(b.x), "v"(b.y), "v"(b.z), "v"(b.w), "v"(dye));                \
-  }
-WKV7_DEF_ROW1(0, 1)
-WKV7_DEF_ROW1(2, 3)
-
-// Row role after dsa is known: dSr[m] = dSr[m] * w~[m] + dsa_e * a[m]
-#define WKV7_DEF_ROW2(S0, S1)                                                        \
-  __device__ __forceinline__ void row2_q##S0(float* d, float4 w, float4 a,           \
-                                             float dsae) {                            \
-    asm("s_nop 1\n\t"                                                                 \
-        "v_mul_f32_dpp %0, %8, %0" WKV7_QP(S0)                                        \
-        "v_mul_f32_dpp %1, %9, %1" WKV7_QP(S0)                                        \
-        "v_mul_f32_dpp %2, %10, %2" WKV7_QP(S0)                                       \
-        "v_mul_f32_dpp %3, %11, %3" WKV7_QP(S0)                                       \
-        "v_mul_f32_dpp %4, %8, %4" WKV7_QP(S1)                                        \
-        "v_mul_f32_dpp %5, %9, %5" WKV7_QP(S1)                                        \
-        "v_mul_f32_dpp %6, %10, %6" WKV7_QP(S1)                                       \
-        "v_mul_f32_dpp %7, %11, %7" WKV7_QP(S1)                                       \
-        "v_fmac_f32_dpp %0, %12, %16" WKV7_QP(S0)                                     \
-        "v_fmac_f32_dpp %1, %13, %16" WKV7_QP(S0)                                     \
-        "v_fmac_f32_dpp %2, %14, %16" WKV7_QP(S0)                                     \
-        "v_fmac_f32_dpp %3, %15, %16" WKV7_QP(S0)                                     \
-        "v_fmac_f32_dpp %4, %12, %16" WKV7_QP(S1)                                     \
-        "v_fmac_f32_dpp %5, %13, %16" WKV7_QP(S1)                                     \
-        "v_fmac_f32_dpp %6, %14, %16" WKV7_QP(S1)                                     \
-        "v_fmac_f32_dpp %7, %15, %16" WKV7_QP(S1)                                     \
-        : "+v"(d[0]), "+v"(d[1]), "+v"(d[2]), "+v"(d[3]), "+v"(d[4]), "+v"(d[5]),    \
-          "+v"(d[6]), "+v"(d[7])                                                      \
-        : "v"(w.x), "v"(w.y), "v"(w.z), "v"(w.w), "v"(a.x), "v"(a.y), "v"(a.z),       \
-          "v"(a.w), "v"(dsae));                                                       \
-  }
-WKV7_DEF_ROW2(0, 1)
-WKV7_DEF_ROW2(2, 3)
-
-// Column role, first half, 4 rows m = 4*S .. 4*S+3 (quad lane S):
-//   dr  += S_t[m] * dy[m]
-//   S[m] = ((S[m] - v[m] * k_e) - sa[m] * b_e) * (1/w~_e)   -> S_{t-1}
-//   dSc[m] += dy[m] * r_e
-//   dw~ += dSc[m] * S[m];  dk += dSc[m] * v[m];  db += dSc[m] * sa[m]
-#define WKV7_DEF_COL1(S)                                                             \
-  __device__ __forceinline__ void col1_q##S(float* c, float* d, float* acc,          \
-                                            float4 dy, float4 v, float4 sa,           \
-                                            float ke, float be, float iwe,            \
-                                            float re) {                               \
-    asm("s_nop 1\n\t"                                                                 \
-        "v_fmac_f32_dpp %8, %16, %0" WKV7_QP(S)                                       \
-        "v_fmac_f32_dpp %9, %17, %1" WKV7_QP(S)                                       \
-        "v_fmac_f32_dpp %8, %18, %2" WKV7_QP(S)                                       \
-        "v_fmac_f32_dpp %9, %19, %3" WKV7_QP(S)                                       \
-        "v_fmac_f32_dpp %0, -%20, %28" WKV7_QP(S)                                     \
-        "v_fmac_f32_dpp %1, -%21, %28" WKV7_QP(S)                                     \
-        "v_fmac_f32_dpp %2, -%22, %28" WKV7_QP(S)                                     \
-        "v_fmac_f32_dpp %3, -%23, %28" WKV7_QP(S)                                     \
-        "v_fmac_f32_dpp %0, -%24, %29" WKV7_QP(S)                                     \
-        "v_fmac_f32_dpp %1, -%25, %29" WKV7_QP(S)                                     \
-        "v_fmac_f32_dpp %2, -%26, %29" WKV7_QP(S)                                     \
-        "v_fmac_f32_dpp %3, -%27, %29" WKV7_QP(S)                                     \
-        "v_mul_f32_e32 %0, %30, %0\n\t"                                               \
-        "v_mul_f32_e32 %1, %30, %1\n\t"                                               \
-        "v_mul_f32_e32 %2, %30, %2\n\t"                                               \
-        "v_mul_f32_e32 %3, %30, %3\n\t"                                               \
-        "v_fmac_f32_dpp %4, %16, %31" WKV7_QP(S)                                      \
-        "v_fmac_f32_dpp %5, %17, %31" WKV7_QP(S)                                      \
-        "v_fmac_f32_dpp %6, %18, %31" WKV7_QP(S)                                      \
-        "v_fmac_f32_dpp %7, %19, %31" WKV7_QP(S)                                      \
-        "v_fmac_f32_e32 %10, %4, %0\n\t"                                              \
-        "v_fmac_f32_e32 %11, %5, %1\n\t"                                              \
-        "v_fmac_f32_e32 %10, %6, %2\n\t"                                              \
-        "v_fmac_f32_e32 %11, %7, %3\n\t"                                              \
-        "v_fmac_f32_dpp %12, %20, %4" WKV7_QP(S)                                      \
-        "v_fmac_f32_dpp %13, %21, %5" WKV7_QP(S)                                      \
-        "v_fmac_f32_dpp %12, %22, %6" WKV7_QP(S)                                      \
-        "v_fmac_f32_dpp %13, %23, %7" WKV7_QP(S)                                      \
-        "v_fmac_f32_dpp %14, %24, %4" WKV7_QP(S)                                      \
-        "v_fmac_f32_dpp %15, %25, %5" WKV7_QP(S)                                      \
-        "v_fmac_f32_dpp %14, %26, %6" WKV7_QP(S)                                      \
-        "v_fmac_f32_dpp %15, %27, %7" WKV7_QP(S)                                      \
-        : "+v"(c[0]), "+v"(c[1]), "+v"(c[2]), "+v"(c[3]), "+v"(d[0]), "+v"(d[1]),    \
-          "+v"(d[2]), "+v"(d[3]), "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]),           \
-          "+v"(acc[3]), "+v"(acc[4]), "+v"(acc[5]), "+v"(acc[6]), "+v"(acc[7])        \
-        : "v"(dy.x), "v"(dy.y), "v"(dy.z), "v"(dy.w), "v"(v.x), "v"(v.y), "v"(v.z),   \
-          "v"(v.w), "v"(sa.x), "v"(sa.y), "v"(sa.z), "v"(sa.w), "v"(ke), "v"(be),     \
-          "v"(iwe), "v"(re));                                                         \
-  }
-WKV7_DEF_COL1(0)
-WKV7_DEF_COL1(1)
-WKV7_DEF_COL1(2)
-WKV7_DEF_COL1(3)
-
-// Column role, second half, 8 rows m = 4*S0 .. 4*S0+7:
-//   da += S_{t-1}[m] * dsa[m];   dSc[m] = dSc[m] * w~_e + dsa[m] * a_e
-#define WKV7_DEF_COL2(S0, S1)                                                        \
-  __device__ __forceinline__ void col2_q##S0(const float* c, float* d, float& a0,    \
-                                             float& a1, float4 dsa, float we,         \
-                                             float ae) {                              \
-    asm("s_nop 1\n\t"                                                                 \
-        "v_fmac_f32_dpp %8, %10, %16" WKV7_QP(S0)                                     \
-        "v_fmac_f32_dpp %9, %11, %17" WKV7_QP(S0)                                     \
-        "v_fmac_f32_dpp %8, %12, %18" WKV7_QP(S0)                                     \
-        "v_fmac_f32_dpp %9, %13, %19" WKV7_QP(S0)                                     \
-        "v_fmac_f32_dpp %8, %10, %20" WKV7_QP(S1)                                     \
-        "v_fmac_f32_dpp %9, %11, %21" WKV7_QP(S1)                                     \
-        "v_fmac_f32_dpp %8, %12, %22" WKV7_QP(S1)                                     \
-        "v_fmac_f32_dpp %9, %13, %23" WKV7_QP(S1)                                     \
-        "v_mul_f32_e32 %0, %14, %0\n\t"                                               \
-        "v_mul_f32_e32 %1, %14, %1\n\t"                                               \
-        "v_mul_f32_e32 %2, %14, %2\n\t"                                               \
-        "v_mul_f32_e32 %3, %14, %3\n\t"                                               \
-        "v_mul_f32_e32 %4, %14, %4\n\t"                                               \
-        "v_mul_f32_e32 %5, %14, %5\n\t"                                               \
-        "v_mul_f32_e32 %6, %14, %6\n\t"                                               \
-        "v_mul_f32_e32 %7, %14, %7\n\t"                                               \
-        "v_fmac_f32_dpp %0, %10, %15" WKV7_QP(S0)                                     \
-        "v_fmac_f32_dpp %1, %11, %15" WKV7_QP(S0)                                     \
-        "v_fmac_f32_dpp %2, %12, %15" WKV7_QP(S0)                                     \
-        "v_fmac_f32_dpp %3, %13, %15" WKV7_QP(S0)                                     \
-        "v_fmac_f32_dpp %4, %10, %15" WKV7_QP(S1)                                     \
-        "v_fmac_f32_dpp %5, %11, %15" WKV7_QP(S1)                                     \
-        "v_fmac_f32_dpp %6, %12, %15" WKV7_QP(S1)                                     \
-        "v_fmac_f32_dpp %7, %13, %15" WKV7_QP(S1)                                     \
-        : "+v"(d[0]), "+v"(d[1]), "+v"(d[2]), "+v"(d[3]), "+v"(d[4]), "+v"(d[5]),    \
-          "+v"(d[6]), "+v"(d[7]), "+v"(a0), "+v"(a1)                                  \
-        : "v"(dsa.x), "v"(dsa.y), "v"(dsa.z), "v"(dsa.w), "v"(we), "v"(ae),           \
-          "v"(c[0]), "v"(c[1]), "v"(c[2]), "v"(c[3]), "v"(c[4]), "v"(c[5]),           \
-          "v"(c[6]), "v"(c[7]));                                                      \
-  }
-WKV7_DEF_COL2(0, 1)
-WKV7_DEF_COL2(2, 3)
-
-struct StepOps {
-  float4 r, k, b, w, a;      // key-indexed, quad-distributed
-  float4 dy, v, sa;          // value-indexed, quad-distributed
-  float re, ke, be, we, ae, dye, iwe;   // own index e
-};
+__device__ __forceinline__ void unpack4(float* d, float4 x) {
+  d[0] = x.x; d[1] = x.y; d[2] = x.z; d[3] = x.w;
+}
 
 template <typename Tin>
 struct BwdParams {
@@ -229,50 +68,52 @@ struct BwdParams {
 
 template <typename Tin>
 __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
-  __shared__ float4 tile[2][V_COUNT][kTile][16];   // 80 KiB
-  __shared__ float ost[2][O_COUNT][kTile][kHead];  // 48 KiB
+  __shared__ float4 tile[2][V_COUNT][kTile][16];   // 36 KiB
+  __shared__ float4 pairs[2][P_COUNT][kTile][32];  // 24 KiB
+  __shared__ float ost[2][O_COUNT][kTile][kHead];  // 24 KiB
   __shared__ float4 dsab[2][16];                   // dsa of the step, by parity
 
   const int h = blockIdx.x, bi = blockIdx.y;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int L = lane & 15, g = lane >> 4, lo = L & 3, hi = L >> 2;
-  const int e = 16 * wave + 4 * g + lo;
-  const int sl = tid >> 4, pp = tid & 15;
+  const int tid = threadIdx.x;
+  const int L = tid & 15, q = tid >> 4;
+  const int sl = (tid >> 4) & 7, pp = tid & 15;   // staging (threads 0..127)
+  const bool stager = tid < 16 * kTile;
 
   const int T = p.T, C = p.C;
   const int64_t bh = (int64_t)bi * p.H + h;
   const int64_t tstride = (int64_t)p.H * kHead;
   const int64_t tok0 = ((int64_t)bi * T * p.H + h) * kHead;
 
-  float dSr[16], Sc[16], dSc[16], Pf[16];
+  float dSr[2][4], Sc[4][2], dSc[4][2], Pf[4][2];
 #pragma unroll
-  for (int m = 0; m < 16; ++m) Sc[m] = 0.0f;
+  for (int c = 0; c < 4; ++c) { Sc[c][0] = 0.0f; Sc[c][1] = 0.0f; }
   if (p.dsT) {
     const float* g0 = p.dsT + bh * (kHead * kHead);
-    const float4* row = reinterpret_cast<const float4*>(g0 + e * kHead + 16 * hi);
+    unpack4(dSr[0], *reinterpret_cast<const float4*>(g0 + (2 * q) * kHead + 4 * L));
+    unpack4(dSr[1], *reinterpret_cast<const float4*>(g0 + (2 * q + 1) * kHead + 4 * L));
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float4 x = row[q];
-      dSr[4 * q] = x.x; dSr[4 * q + 1] = x.y; dSr[4 * q + 2] = x.z; dSr[4 * q + 3] = x.w;
+    for (int c = 0; c < 4; ++c) {
+      const float2 x = *reinterpret_cast<const float2*>(g0 + (4 * L + c) * kHead + 2 * q);
+      dSc[c][0] = x.x;
+      dSc[c][1] = x.y;
     }
-#pragma unroll
-    for (int m = 0; m < 16; ++m) dSc[m] = g0[(16 * hi + m) * kHead + e];
   } else {
 #pragma unroll
-    for (int m = 0; m < 16; ++m) { dSr[m] = 0.0f; dSc[m] = 0.0f; }
+    for (int c = 0; c < 4; ++c) {
+      dSr[0][c] = 0.0f; dSr[1][c] = 0.0f; dSc[c][0] = 0.0f; dSc[c][1] = 0.0f;
+    }
   }
 
-  // checkpoint c holds S after step c*C + C - 1, key-major: row e of the
-  // checkpoint is column e of S.
+  // checkpoint c holds S after step c*C + C - 1, key-major ([i][j]): its row
+  // 2q+d, entries 4L .. 4L+3, is Sc[0..3][d].
   const int64_t nchunks = T / C;
-  const float* ckpt_bh = p.ckpt + bh * nchunks * (kHead * kHead) + e * kHead + 16 * hi;
+  const float* ckpt_bh = p.ckpt + (bh * nchunks * kHead + 2 * q) * kHead + 4 * L;
   auto ckload = [&](int64_t c) {
-    const float4* src = reinterpret_cast<const float4*>(ckpt_bh + c * (kHead * kHead));
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float4 x = src[q];
-      Pf[4 * q] = x.x; Pf[4 * q + 1] = x.y; Pf[4 * q + 2] = x.z; Pf[4 * q + 3] = x.w;
-    }
+    const float* src = ckpt_bh + c * (kHead * kHead);
+    const float4 x0 = *reinterpret_cast<const float4*>(src);
+    const float4 x1 = *reinterpret_cast<const float4*>(src + kHead);
+    Pf[0][0] = x0.x; Pf[1][0] = x0.y; Pf[2][0] = x0.z; Pf[3][0] = x0.w;
+    Pf[0][1] = x1.x; Pf[1][1] = x1.y; Pf[2][1] = x1.z; Pf[3][1] = x1.w;
   };
   int64_t next_chunk = nchunks - 1;
   if (next_chunk >= 0) ckload(next_chunk);
@@ -281,7 +122,7 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
   typename io::raw pre[7];
   float4 pre_sa;
   auto gload = [&](int t0) {
-    if (t0 + sl < T) {
+    if (stager && t0 + sl < T) {
       const int64_t off = tok0 + (int64_t)(t0 + sl) * tstride + 4 * pp;
       pre[0] = io::load(p.w + off);
       pre[1] = io::load(p.r + off);
@@ -294,9 +135,8 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
     }
   };
   auto lstore = [&](int buf, int t0) {
-    if (t0 + sl < T) {
+    if (stager && t0 + sl < T) {
       const float4 x = io::widen(pre[0]);
-      float4 w, iw, dwf;
       const float xs[4] = {x.x, x.y, x.z, x.w};
       float ws[4], iws[4], dws[4];
 #pragma unroll
@@ -306,84 +146,122 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
         iws[c] = 1.0f / ws[c];
         dws[c] = kWScale * ws[c] * sig * (1.0f - sig);
       }
-      w = make_float4(ws[0], ws[1], ws[2], ws[3]);
-      iw = make_float4(iws[0], iws[1], iws[2], iws[3]);
-      dwf = make_float4(dws[0], dws[1], dws[2], dws[3]);
+      const float4 r = io::widen(pre[1]), k = io::widen(pre[2]), a = io::widen(pre[4]);
+      const float4 b = io::widen(pre[5]);
+      const float4 w = make_float4(ws[0], ws[1], ws[2], ws[3]);
+      const float4 iw = make_float4(iws[0], iws[1], iws[2], iws[3]);
+      tile[buf][V_R][sl][pp] = r;
+      tile[buf][V_K][sl][pp] = k;
+      tile[buf][V_B][sl][pp] = b;
       tile[buf][V_W][sl][pp] = w;
-      tile[buf][V_IW][sl][pp] = iw;
-      tile[buf][V_DWF][sl][pp] = dwf;
-      tile[buf][V_R][sl][pp] = io::widen(pre[1]);
-      tile[buf][V_K][sl][pp] = io::widen(pre[2]);
-      tile[buf][V_V][sl][pp] = io::widen(pre[3]);
-      tile[buf][V_A][sl][pp] = io::widen(pre[4]);
-      tile[buf][V_B][sl][pp] = io::widen(pre[5]);
+      tile[buf][V_A][sl][pp] = a;
       tile[buf][V_DY][sl][pp] = io::widen(pre[6]);
+      tile[buf][V_V][sl][pp] = io::widen(pre[3]);
       tile[buf][V_SA][sl][pp] = pre_sa;
+      tile[buf][V_DWF][sl][pp] = make_float4(dws[0], dws[1], dws[2], dws[3]);
+      // columns 4pp .. 4pp+3 are column pairs 2pp and 2pp+1
+      pairs[buf][P_RK][sl][2 * pp] = make_float4(r.x, r.y, k.x, k.y);
+      pairs[buf][P_RK][sl][2 * pp + 1] = make_float4(r.z, r.w, k.z, k.w);
+      pairs[buf][P_BW][sl][2 * pp] = make_float4(b.x, b.y, w.x, w.y);
+      pairs[buf][P_BW][sl][2 * pp + 1] = make_float4(b.z, b.w, w.z, w.w);
+      pairs[buf][P_AI][sl][2 * pp] = make_float4(a.x, a.y, iw.x, iw.y);
+      pairs[buf][P_AI][sl][2 * pp + 1] = make_float4(a.z, a.w, iw.z, iw.w);
     }
-  };
-  auto lread = [&](int buf, int s) {
-    StepOps o;
-    o.r = tile[buf][V_R][s][L];
-    o.k = tile[buf][V_K][s][L];
-    o.b = tile[buf][V_B][s][L];
-    o.w = tile[buf][V_W][s][L];
-    o.a = tile[buf][V_A][s][L];
-    o.dy = tile[buf][V_DY][s][L];
-    o.v = tile[buf][V_V][s][L];
-    o.sa = tile[buf][V_SA][s][L];
-    o.re = reinterpret_cast<const float*>(tile[buf][V_R][s])[e];
-    o.ke = reinterpret_cast<const float*>(tile[buf][V_K][s])[e];
-    o.be = reinterpret_cast<const float*>(tile[buf][V_B][s])[e];
-    o.we = reinterpret_cast<const float*>(tile[buf][V_W][s])[e];
-    o.ae = reinterpret_cast<const float*>(tile[buf][V_A][s])[e];
-    o.dye = reinterpret_cast<const float*>(tile[buf][V_DY][s])[e];
-    o.iwe = reinterpret_cast<const float*>(tile[buf][V_IW][s])[e];
-    return o;
   };
 
   int until_reload = 0;   // steps until the next checkpoint reload
   int parity = 0;
 
-  auto step = [&](const StepOps& o, int buf, int s) {
-    if (until_reload == 0) {   // (t + 1) % C == 0
+  auto step = [&](int buf, int s) {
+    if (until_reload == 0) {   // (t + 1) % C == 0, kernel.rs:210-228
       until_reload = C;
 #pragma unroll
-      for (int m = 0; m < 16; ++m) Sc[m] = Pf[m];
+      for (int c = 0; c < 4; ++c) { Sc[c][0] = Pf[c][0]; Sc[c][1] = Pf[c][1]; }
       --next_chunk;
       if (next_chunk >= 0) ckload(next_chunk);
     }
     --until_reload;
 
-    // row role: dS row += dy_e r^T; dv_e, dsa_e
-    float v0 = 0.0f, v1 = 0.0f, s0 = 0.0f, s1 = 0.0f;
-    row1_q0(dSr, v0, v1, s0, s1, o.r, o.k, o.b, o.dye);
-    row1_q2(dSr + 8, v0, v1, s0, s1, o.r, o.k, o.b, o.dye);
-    const float dv = seg_sum(v0 + v1);
-    const float dsa = seg_sum(s0 + s1);
-    reinterpret_cast<float*>(dsab[parity])[e] = dsa;
-    ost[buf][O_DV][s][e] = dv;
+    // row role operands: columns 4L..4L+3, rows 2q, 2q+1
+    float rr[4], kk[4], bb[4];
+    unpack4(rr, tile[buf][V_R][s][L]);
+    unpack4(kk, tile[buf][V_K][s][L]);
+    unpack4(bb, tile[buf][V_B][s][L]);
+    const float2 dyr = reinterpret_cast<const float2*>(tile[buf][V_DY][s])[q];
+    // column role operands: rows 4L..4L+3, columns 2q, 2q+1
+    float dy[4], v[4], sa[4];
+    unpack4(dy, tile[buf][V_DY][s][L]);
+    unpack4(v, tile[buf][V_V][s][L]);
+    unpack4(sa, tile[buf][V_SA][s][L]);
+    const float4 prk = pairs[buf][P_RK][s][q], pbw = pairs[buf][P_BW][s][q];
+    const float4 pai = pairs[buf][P_AI][s][q];
+    const float rc[2] = {prk.x, prk.y}, kc[2] = {prk.z, prk.w};
+    const float bc[2] = {pbw.x, pbw.y}, wc[2] = {pbw.z, pbw.w};
+    const float ac[2] = {pai.x, pai.y}, iwc[2] = {pai.z, pai.w};
 
-    // column role: dr (from S_t), rebuild S_{t-1}, dS col += dy r_e; dw~, dk, db
-    float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-    col1_q0(Sc, dSc, acc, o.dy, o.v, o.sa, o.ke, o.be, o.iwe, o.re);
-    col1_q1(Sc + 4, dSc + 4, acc, o.dy, o.v, o.sa, o.ke, o.be, o.iwe, o.re);
-    col1_q2(Sc + 8, dSc + 8, acc, o.dy, o.v, o.sa, o.ke, o.be, o.iwe, o.re);
-    col1_q3(Sc + 12, dSc + 12, acc, o.dy, o.v, o.sa, o.ke, o.be, o.iwe, o.re);
-    ost[buf][O_DR][s][e] = seg_sum(acc[0] + acc[1]);
-    ost[buf][O_DW][s][e] = seg_sum(acc[2] + acc[3]);
-    ost[buf][O_DK][s][e] = seg_sum(acc[4] + acc[5]);
-    ost[buf][O_DB][s][e] = seg_sum(acc[6] + acc[7]);
+    // row role: dS row += dy r^T (kernel.rs:248); dv, dsa (kernel.rs:261-262)
+    const float dyd[2] = {dyr.x, dyr.y};
+    float dvp[2] = {0.0f, 0.0f};
+    float dsa0 = 0.0f, dsa1 = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      dSr[0][c] = __builtin_fmaf(dyd[0], rr[c], dSr[0][c]);
+      dSr[1][c] = __builtin_fmaf(dyd[1], rr[c], dSr[1][c]);
+      dvp[0] = __builtin_fmaf(dSr[0][c], kk[c], dvp[0]);
+      dvp[1] = __builtin_fmaf(dSr[1][c], kk[c], dvp[1]);
+      dsa0 = __builtin_fmaf(dSr[0][c], bb[c], dsa0);
+      dsa1 = __builtin_fmaf(dSr[1][c], bb[c], dsa1);
+    }
+    row16_sum2(dsa0, dsa1, L);
+    if (L == 0) reinterpret_cast<float2*>(dsab[parity])[q] = make_float2(dsa0, dsa1);
+
+    // column role: dr from S_t; rebuild S_{t-1}; dS col += dy r; dw~, dk, db
+    float drp[2] = {0.0f, 0.0f}, dwp[2] = {0.0f, 0.0f}, dkp[2] = {0.0f, 0.0f};
+    float dbp[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int d = 0; d < 2; ++d) {
+        drp[d] = __builtin_fmaf(Sc[c][d], dy[c], drp[d]);   // kernel.rs:230-237
+        // ((S - k v) - b sa) / w~, kernel.rs:239-246
+        Sc[c][d] = __builtin_fmaf(-bc[d], sa[c], __builtin_fmaf(-kc[d], v[c], Sc[c][d])) * iwc[d];
+        dSc[c][d] = __builtin_fmaf(rc[d], dy[c], dSc[c][d]);   // kernel.rs:249
+        dwp[d] = __builtin_fmaf(dSc[c][d], Sc[c][d], dwp[d]);   // kernel.rs:258-264
+        dkp[d] = __builtin_fmaf(dSc[c][d], v[c], dkp[d]);
+        dbp[d] = __builtin_fmaf(dSc[c][d], sa[c], dbp[d]);
+      }
+    // dv (rows 2q, 2q+1) and dr, dw~, dk (columns 2q, 2q+1): one lane pair each
+    float early[8] = {dvp[0], dvp[1], drp[0], drp[1], dwp[0], dwp[1], dkp[0], dkp[1]};
+    row16_scatter<8>(early, L);
+    if ((L & 1) == 0) ost[buf][O_DV + (L >> 2)][s][2 * q + ((L >> 1) & 1)] = early[0];
 
     __syncthreads();   // dsa of every row visible
-    const float4 dsa4 = dsab[parity][L];
+    float ds[4];
+    unpack4(ds, dsab[parity][L]);
     parity ^= 1;
 
-    row2_q0(dSr, o.w, o.a, dsa);
-    row2_q2(dSr + 8, o.w, o.a, dsa);
-    float a0 = 0.0f, a1 = 0.0f;
-    col2_q0(Sc, dSc, a0, a1, dsa4, o.we, o.ae);
-    col2_q2(Sc + 8, dSc + 8, a0, a1, dsa4, o.we, o.ae);
-    ost[buf][O_DA][s][e] = seg_sum(a0 + a1);
+    // row role: dS row = dS row * w~ + dsa a^T (kernel.rs:290-291)
+    float ww[4], aa[4];
+    unpack4(ww, tile[buf][V_W][s][L]);
+    unpack4(aa, tile[buf][V_A][s][L]);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      dSr[0][c] = __builtin_fmaf(dsa0, aa[c], dSr[0][c] * ww[c]);
+      dSr[1][c] = __builtin_fmaf(dsa1, aa[c], dSr[1][c] * ww[c]);
+    }
+    // column role: da = S_{t-1}^T dsa (kernel.rs:280-287); dS col = dS col * w~ + a dsa
+    float dap[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int d = 0; d < 2; ++d) {
+        dap[d] = __builtin_fmaf(Sc[c][d], ds[c], dap[d]);
+        dSc[c][d] = __builtin_fmaf(ac[d], ds[c], dSc[c][d] * wc[d]);   // kernel.rs:293-294
+      }
+    // db, da (columns 2q, 2q+1): four lanes each
+    float late[4] = {dbp[0], dbp[1], dap[0], dap[1]};
+    row16_scatter<4>(late, L);
+    if ((L & 3) == 0) ost[buf][O_DB + (L >> 3)][s][2 * q + ((L >> 2) & 1)] = late[0];
   };
 
   const int ntiles = (T + kTile - 1) / kTile;
@@ -398,24 +276,14 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
     const int t0 = ti * kTile;
     const int nst = min(kTile, T - t0);
     if (ti > 0) gload(t0 - kTile);
-
-    StepOps A = lread(buf, nst - 1);
-    int s = nst - 1;
-    for (; s >= 1; s -= 2) {
-      const StepOps Bo = lread(buf, s - 1);
-      step(A, buf, s);
-      A = lread(buf, max(s - 2, 0));
-      step(Bo, buf, s - 1);
-    }
-    if (s == 0) step(A, buf, 0);
-
+    for (int s = nst - 1; s >= 0; --s) step(buf, s);
     if (ti > 0) lstore(buf ^ 1, t0 - kTile);
     __syncthreads();
-    if (sl < nst) {
+    if (stager && sl < nst) {
       const int64_t off = tok0 + (int64_t)(t0 + sl) * tstride + 4 * pp;
       float4 dw = reinterpret_cast<const float4*>(ost[buf][O_DW][sl])[pp];
       const float4 f = tile[buf][V_DWF][sl][pp];
-      dw.x *= f.x; dw.y *= f.y; dw.z *= f.z; dw.w *= f.w;
+      dw.x *= f.x; dw.y *= f.y; dw.z *= f.z; dw.w *= f.w;   // kernel.rs:267-271
       io::store(p.dw + off, dw);
       io::store(p.dr + off, reinterpret_cast<const float4*>(ost[buf][O_DR][sl])[pp]);
       io::store(p.dk + off, reinterpret_cast<const float4*>(ost[buf][O_DK][sl])[pp]);
@@ -425,11 +293,11 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
     }
   }
 
-  if (p.ds0) {
-    float4* dst = reinterpret_cast<float4*>(p.ds0 + (bh * kHead + e) * kHead + 16 * hi);
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      dst[q] = make_float4(dSr[4 * q], dSr[4 * q + 1], dSr[4 * q + 2], dSr[4 * q + 3]);
+  if (p.ds0) {   // kernel.rs:299-307
+    float* base = p.ds0 + (bh * kHead + 2 * q) * kHead + 4 * L;
+    *reinterpret_cast<float4*>(base) = make_float4(dSr[0][0], dSr[0][1], dSr[0][2], dSr[0][3]);
+    *reinterpret_cast<float4*>(base + kHead) =
+        make_float4(dSr[1][0], dSr[1][1], dSr[1][2], dSr[1][3]);
   }
 }
 

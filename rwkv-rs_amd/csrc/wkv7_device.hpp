@@ -1,29 +1,22 @@
 // Device-side building blocks shared by the WKV7 kernels (gfx950 / CDNA4).
 //
-// Work layout (all three kernels). One workgroup of 256 threads (4 wave64)
-// owns one (batch, head) pair and its 64x64 fp32 state. Inside a wave the
-// lanes form four 16-lane DPP rows. A DPP row is four quads. With
-//   wave = tid / 64, g = (tid % 64) / 16, L = tid % 16, lo = L % 4, hi = L / 4
-// a thread's "own index" is e = 16*wave + 4*g + lo (0..63) and its "segment"
-// is hi (0..3, covering indices 16*hi .. 16*hi+15). The forward kernel keeps
-// state row e, columns 16*hi+m (m = 0..15) in 16 VGPRs.
+// Work layout. One workgroup (512 threads, 8 waves) owns one (batch, head)
+// pair and its 64x64 fp32 state S (row j = value index, column i = key index).
 //
-// Per-timestep vectors (one value per index 0..63) are stored in LDS as fp32
-// and read with one ds_read_b128 per lane: lane L of every DPP row reads
-// elements 4L..4L+3. Element 16*hi+m of a vector then sits in quad hi, quad
-// lane m/4, component m%4, so a quad_perm:[s,s,s,s] DPP source operand hands
-// element 16*hi+4s+c to all four lanes of the quad in the same instruction
-// that consumes it. That turns the "broadcast a column value to every row"
-// of the recurrence into a free operand modifier instead of an LDS read per
-// element. The compiler does not fold DPP moves into v_fmac_f32, so the
-// element loops are short inline-asm blocks of v_fmac_f32_dpp/v_mul_f32_dpp.
+// Why eight waves per head: on gfx950 a wave issues at most one VALU
+// instruction about every 4 cycles, while a SIMD retires a plain wave64 FP32
+// FMA every ~2 cycles when two waves feed it; DPP-modified instructions retire
+// at half that rate. With 256 heads (the benchmark shape) only 512 threads per
+// head give every SIMD two waves.
 //
-// DPP hazard: on gfx9 a DPP instruction that reads a VGPR written by a VALU
-// instruction less than two instructions earlier reads a stale value. Every
-// asm block starts with `s_nop 1`, and inside a block no DPP source operand is
-// ever written, so the blocks are safe whatever the compiler schedules before
-// them. The cross-lane reductions use the __builtin_amdgcn_update_dpp path,
-// for which the compiler inserts the wait states itself.
+// Thread tile. Thread tid owns a 2x4 block: column group L = tid % 16
+// (columns 4L .. 4L+3) and row pair q = tid / 16 (rows 2q, 2q+1). The sixteen
+// lanes of one DPP row therefore cover all 64 columns of two rows, so a sum
+// over a row is 4 in-lane products plus a 4-step DPP rotation reduction, and
+// every per-column operand the thread needs is one ds_read_b128 of a 64-entry
+// LDS vector (entries 4L .. 4L+3), consumed by plain full-rate FMAs.
+// LDS bandwidth (~250 B/clk/CU on gfx950, broadcast or not) is the other
+// limit, which is why the block is 2x4 rather than 1x8.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -32,7 +25,7 @@
 namespace wkv7 {
 
 constexpr int kHead = 64;        // head size N (the kernels are specialised)
-constexpr int kThreads = 256;    // 4 waves per (batch, head)
+constexpr int kThreads = 512;    // 8 waves per (batch, head)
 constexpr float kWScale = -0.6065306597f;   // -exp(-1/2), kernel.rs:4
 
 typedef uint16_t bf16_t;
@@ -86,95 +79,97 @@ __device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf
 __device__ __forceinline__ float decay_f(float sig) { return expf(kWScale * sig); }
 
 // ------------------------------------------------------- cross-lane reduction
-// Sum over the four lanes L, L+4, L+8, L+12 of a DPP row (the four segments
-// of one index). The result is bit-identical in all four lanes: the first
-// step pairs segments {0,2} and {1,3}, the second adds the two pair sums, and
-// IEEE addition is commutative.
-__device__ __forceinline__ float seg_sum(float x) {
-  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-           0, __builtin_bit_cast(int, x), 0x128 /* row_ror:8 */, 0xf, 0xf, false));
-  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-           0, __builtin_bit_cast(int, x), 0x124 /* row_ror:4 */, 0xf, 0xf, false));
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+      0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+
+// Sum within each 8-lane half of a DPP row (pairs L/7-L, then L/L^2, then
+// L/L^1). All eight lanes get the same bits: every step adds two partial sums
+// that the lanes of the orbit form from the same operands, and IEEE addition
+// is commutative.
+__device__ __forceinline__ float half8_sum(float x) {
+  x += dpp_mov<0x141>(x);   // row_half_mirror
+  x += dpp_mov<0x4E>(x);    // quad_perm:[2,3,0,1]
+  x += dpp_mov<0xB1>(x);    // quad_perm:[1,0,3,2]
   return x;
 }
 
-// ------------------------------------------------------------ asm helpers
-#define WKV7_QP(s) " quad_perm:[" #s "," #s "," #s "," #s "] row_mask:0xf bank_mask:0xf\n\t"
-
-// ------------------------------------------- forward step (rows independent)
-// sa0/sa1 += a[m] * S[m] over the 16 columns m of this thread's segment
-// (a quad-broadcast: column 16*hi+4s+c is component c of quad lane s)
-__device__ __forceinline__ void fwd_sa16(float& sa0, float& sa1, float4 a, const float* S) {
-  asm("s_nop 1\n\t"
-      "v_fmac_f32_dpp %0, %2, %6" WKV7_QP(0)
-      "v_fmac_f32_dpp %1, %3, %7" WKV7_QP(0)
-      "v_fmac_f32_dpp %0, %4, %8" WKV7_QP(0)
-      "v_fmac_f32_dpp %1, %5, %9" WKV7_QP(0)
-      "v_fmac_f32_dpp %0, %2, %10" WKV7_QP(1)
-      "v_fmac_f32_dpp %1, %3, %11" WKV7_QP(1)
-      "v_fmac_f32_dpp %0, %4, %12" WKV7_QP(1)
-      "v_fmac_f32_dpp %1, %5, %13" WKV7_QP(1)
-      "v_fmac_f32_dpp %0, %2, %14" WKV7_QP(2)
-      "v_fmac_f32_dpp %1, %3, %15" WKV7_QP(2)
-      "v_fmac_f32_dpp %0, %4, %16" WKV7_QP(2)
-      "v_fmac_f32_dpp %1, %5, %17" WKV7_QP(2)
-      "v_fmac_f32_dpp %0, %2, %18" WKV7_QP(3)
-      "v_fmac_f32_dpp %1, %3, %19" WKV7_QP(3)
-      "v_fmac_f32_dpp %0, %4, %20" WKV7_QP(3)
-      "v_fmac_f32_dpp %1, %5, %21" WKV7_QP(3)
-      : "+v"(sa0), "+v"(sa1)
-      : "v"(a.x), "v"(a.y), "v"(a.z), "v"(a.w), "v"(S[0]), "v"(S[1]), "v"(S[2]),
-        "v"(S[3]), "v"(S[4]), "v"(S[5]), "v"(S[6]), "v"(S[7]), "v"(S[8]), "v"(S[9]),
-        "v"(S[10]), "v"(S[11]), "v"(S[12]), "v"(S[13]), "v"(S[14]), "v"(S[15]));
+// One recursive-halving step of a reduce-scatter over a DPP row: the lane
+// keeps half of its N values (the upper half when `upper`) and adds the
+// partner's copy of that half; the partner lane (the DPP source) has the
+// opposite `upper`.
+template <int CTRL, int N>
+__device__ __forceinline__ void rs_step(float* x, bool upper) {
+#pragma unroll
+  for (int j = 0; j < N / 2; ++j) {
+    const float keep = upper ? x[N / 2 + j] : x[j];
+    const float send = upper ? x[j] : x[N / 2 + j];
+    x[j] = keep + dpp_mov<CTRL>(send);
+  }
 }
 
-// For the 8 columns m = 4*S0 .. 4*S0+7 (quad lanes S0 and S0+1):
-//   S[m] = S[m] * w~ + sa * b + k * v_e ;  y0/y1 += r * S[m]
-// in the reference's operation order ((S*w + sa*b) + k*v, kernel.rs:79-83).
-#define WKV7_DEF_FWD_UPD8(S0, S1)                                                   \
-  __device__ __forceinline__ void fwd_upd8_q##S0(float* s, float& y0, float& y1,     \
-                                                 float4 w, float4 b, float4 k,       \
-                                                 float4 r, float sa, float ve) {     \
-    asm("s_nop 1\n\t"                                                                \
-        "v_mul_f32_dpp %0, %10, %0" WKV7_QP(S0)                                      \
-        "v_mul_f32_dpp %1, %11, %1" WKV7_QP(S0)                                      \
-        "v_mul_f32_dpp %2, %12, %2" WKV7_QP(S0)                                      \
-        "v_mul_f32_dpp %3, %13, %3" WKV7_QP(S0)                                      \
-        "v_mul_f32_dpp %4, %10, %4" WKV7_QP(S1)                                      \
-        "v_mul_f32_dpp %5, %11, %5" WKV7_QP(S1)                                      \
-        "v_mul_f32_dpp %6, %12, %6" WKV7_QP(S1)                                      \
-        "v_mul_f32_dpp %7, %13, %7" WKV7_QP(S1)                                      \
-        "v_fmac_f32_dpp %0, %14, %26" WKV7_QP(S0)                                    \
-        "v_fmac_f32_dpp %1, %15, %26" WKV7_QP(S0)                                    \
-        "v_fmac_f32_dpp %2, %16, %26" WKV7_QP(S0)                                    \
-        "v_fmac_f32_dpp %3, %17, %26" WKV7_QP(S0)                                    \
-        "v_fmac_f32_dpp %4, %14, %26" WKV7_QP(S1)                                    \
-        "v_fmac_f32_dpp %5, %15, %26" WKV7_QP(S1)                                    \
-        "v_fmac_f32_dpp %6, %16, %26" WKV7_QP(S1)                                    \
-        "v_fmac_f32_dpp %7, %17, %26" WKV7_QP(S1)                                    \
-        "v_fmac_f32_dpp %0, %18, %27" WKV7_QP(S0)                                    \
-        "v_fmac_f32_dpp %1, %19, %27" WKV7_QP(S0)                                    \
-        "v_fmac_f32_dpp %2, %20, %27" WKV7_QP(S0)                                    \
-        "v_fmac_f32_dpp %3, %21, %27" WKV7_QP(S0)                                    \
-        "v_fmac_f32_dpp %4, %18, %27" WKV7_QP(S1)                                    \
-        "v_fmac_f32_dpp %5, %19, %27" WKV7_QP(S1)                                    \
-        "v_fmac_f32_dpp %6, %20, %27" WKV7_QP(S1)                                    \
-        "v_fmac_f32_dpp %7, %21, %27" WKV7_QP(S1)                                    \
-        "v_fmac_f32_dpp %8, %22, %0" WKV7_QP(S0)                                     \
-        "v_fmac_f32_dpp %9, %23, %1" WKV7_QP(S0)                                     \
-        "v_fmac_f32_dpp %8, %24, %2" WKV7_QP(S0)                                     \
-        "v_fmac_f32_dpp %9, %25, %3" WKV7_QP(S0)                                     \
-        "v_fmac_f32_dpp %8, %22, %4" WKV7_QP(S1)                                     \
-        "v_fmac_f32_dpp %9, %23, %5" WKV7_QP(S1)                                     \
-        "v_fmac_f32_dpp %8, %24, %6" WKV7_QP(S1)                                     \
-        "v_fmac_f32_dpp %9, %25, %7" WKV7_QP(S1)                                     \
-        : "+v"(s[0]), "+v"(s[1]), "+v"(s[2]), "+v"(s[3]), "+v"(s[4]), "+v"(s[5]),   \
-          "+v"(s[6]), "+v"(s[7]), "+v"(y0), "+v"(y1)                                 \
-        : "v"(w.x), "v"(w.y), "v"(w.z), "v"(w.w), "v"(b.x), "v"(b.y), "v"(b.z),      \
-          "v"(b.w), "v"(k.x), "v"(k.y), "v"(k.z), "v"(k.w), "v"(r.x), "v"(r.y),      \
-          "v"(r.z), "v"(r.w), "v"(sa), "v"(ve));                                     \
+// Sums of N values (N = 2, 4, 8, 16) over the 16 lanes of a DPP row, spread
+// over the lanes: afterwards x[0] of lane L holds the full sum of value
+// index L / (16/N), i.e. lanes (16/N)*m .. (16/N)*m + 16/N - 1 hold value m. Partners: L^8 (row_ror:8), the mirror inside an 8-lane half, L^2,
+// L^1; a level with one value left is a plain pairwise sum.
+template <int N>
+__device__ __forceinline__ void row16_scatter(float* x, int L) {
+  static_assert(N == 2 || N == 4 || N == 8 || N == 16, "N must be 2, 4, 8 or 16");
+  rs_step<0x128, N>(x, (L & 8) != 0);
+  if constexpr (N >= 4) rs_step<0x141, N / 2>(x, (L & 4) != 0);
+  else x[0] += dpp_mov<0x141>(x[0]);
+  if constexpr (N >= 8) rs_step<0x4E, N / 4>(x, (L & 2) != 0);
+  else x[0] += dpp_mov<0x4E>(x[0]);
+  if constexpr (N >= 16) rs_step<0xB1, N / 8>(x, (L & 1) != 0);
+  else x[0] += dpp_mov<0xB1>(x[0]);
+}
+
+// Both row sums of a lane pair (x0, x1), available in every lane of the DPP
+// row: a reduce-scatter to one value per half, then one exchange.
+__device__ __forceinline__ void row16_sum2(float& x0, float& x1, int L) {
+  float x[2] = {x0, x1};
+  row16_scatter<2>(x, L);   // lanes 0-7: sum of x0, lanes 8-15: sum of x1
+  const float other = dpp_mov<0x128>(x[0]);
+  const bool up = (L & 8) != 0;
+  x0 = up ? other : x[0];
+  x1 = up ? x[0] : other;
+}
+
+// ------------------------------------------------------------- forward step
+// One timestep of the recurrence on a thread's 2x4 block: S0/S1 are rows 2q
+// and 2q+1, columns 4L .. 4L+3; w4, a4, b4, k4, r4 hold those columns of w~,
+// a, b, k, r and v the two rows of v (wkv7_common/kernel.rs:66-87):
+//   sa_j = sum_i a_i S[j,i];  S[j,i] = (S[j,i] w~_i + sa_j b_i) + k_i v_j;
+//   y_j = sum_i S[j,i] r_i.
+// On return sa0/sa1 hold sa of both rows in every lane and y holds y of row
+// 2q in lanes 0-7 and of row 2q+1 in lanes 8-15 of the DPP row.
+__device__ __forceinline__ void fwd_step(float* S0, float* S1, float4 w4, float4 a4,
+                                         float4 b4, float4 k4, float4 r4, float2 v, int L,
+                                         float& sa0, float& sa1, float& y) {
+  const float w[4] = {w4.x, w4.y, w4.z, w4.w}, a[4] = {a4.x, a4.y, a4.z, a4.w};
+  const float b[4] = {b4.x, b4.y, b4.z, b4.w}, k[4] = {k4.x, k4.y, k4.z, k4.w};
+  const float r[4] = {r4.x, r4.y, r4.z, r4.w};
+  float p0 = 0.0f, p1 = 0.0f;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    p0 = __builtin_fmaf(a[c], S0[c], p0);
+    p1 = __builtin_fmaf(a[c], S1[c], p1);
   }
-WKV7_DEF_FWD_UPD8(0, 1)
-WKV7_DEF_FWD_UPD8(2, 3)
+  row16_sum2(p0, p1, L);
+  sa0 = p0;
+  sa1 = p1;
+  float yy[2] = {0.0f, 0.0f};
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    S0[c] = __builtin_fmaf(k[c], v.x, __builtin_fmaf(b[c], sa0, S0[c] * w[c]));
+    S1[c] = __builtin_fmaf(k[c], v.y, __builtin_fmaf(b[c], sa1, S1[c] * w[c]));
+    yy[0] = __builtin_fmaf(r[c], S0[c], yy[0]);
+    yy[1] = __builtin_fmaf(r[c], S1[c], yy[1]);
+  }
+  row16_scatter<2>(yy, L);
+  y = yy[0];
+}
 
 }  // namespace wkv7

@@ -8,19 +8,18 @@
 //   y_j   = sum_i S[j,i] r_i
 //   every C steps: checkpoint S^T (key-major), at the end: s_T = S
 //
-// Design. One 256-thread workgroup per (b, h); thread (e, hi) keeps state row
-// e, columns 16*hi..16*hi+15 in VGPRs (16 fp32), so the four waves of the
-// workgroup cover the 64x64 state with no cross-wave traffic at all: rows are
-// independent in the forward. Operands are staged through LDS in tiles of 16
-// timesteps: all 256 threads load one tile with coalesced 8/16-byte loads
-// (one timestep of one operand is a 128/256-byte row), widen bf16 to fp32 and
+// Design. One 512-thread workgroup per (b, h); each thread keeps a 2x4 block
+// of the state in VGPRs (layout in wkv7_device.hpp). Rows are independent in
+// the forward, so the only cross-lane work is the two row sums (sa and y),
+// four DPP steps each. Operands are staged through LDS in tiles of 16
+// timesteps: threads load one tile with coalesced 8/16-byte loads (one
+// timestep of one operand is a 128/256-byte row), widen bf16 to fp32 and
 // compute the decay once per element, and the next tile's global loads are in
 // flight while the current tile is consumed (double-buffered LDS). Per step a
-// thread reads five quad-distributed operand vectors (ds_read_b128 each) and
-// its own v_e, then does 5 VALU instructions per state element, all with a
-// DPP quad broadcast for the column operand, plus two 2-step DPP reductions
-// (sa and y over the four segments of a row). y and sa are staged in LDS and
-// written once per tile with full-row stores.
+// thread reads its four columns of w~, a, b, k, r (five ds_read_b128) and its
+// two rows of v. y and sa are staged in LDS and written once per tile with
+// full-row stores; a checkpoint taken inside a tile is stored at the tile end,
+// after the tile's loads have been consumed, so no wait ever covers it.
 #include "wkv7_device.hpp"
 #include "wkv7_launch.hpp"
 
@@ -33,8 +32,8 @@ constexpr int kTile = 16;   // timesteps per LDS tile
 enum { V_W = 0, V_R, V_K, V_V, V_A, V_B, V_COUNT };
 
 struct StepOps {
-  float4 w, r, k, a, b;
-  float ve;
+  float4 w, a, b, k, r;   // columns 4L .. 4L+3
+  float2 v;               // rows 2q, 2q+1
 };
 
 template <typename Tin>
@@ -54,66 +53,97 @@ __global__ __launch_bounds__(kThreads) void wkv7_fwd_kernel(FwdParams<Tin> p) {
   __shared__ float ost[2][2][kTile][kHead];        // 16 KiB: y, sa
 
   const int h = blockIdx.x, bi = blockIdx.y;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int L = lane & 15, g = lane >> 4, lo = L & 3, hi = L >> 2;
-  const int e = 16 * wave + 4 * g + lo;   // state row owned by this thread
-  const int sl = tid >> 4, pp = tid & 15; // staging: timestep, 4-element part
+  const int tid = threadIdx.x;
+  const int L = tid & 15, q = tid >> 4;   // columns 4L.., rows 2q, 2q+1
+  // staging: threads 0..255 stage w, r, k; threads 256..511 stage v, a, b
+  const int st_half = tid >> 8, sl = (tid >> 4) & 15, pp = tid & 15;
 
   const int T = p.T;
   const int64_t bh = (int64_t)bi * p.H + h;
   const int64_t tstride = (int64_t)p.H * kHead;
   const int64_t tok0 = ((int64_t)bi * T * p.H + h) * kHead;
 
-  float S[16];
+  float S0[4], S1[4];   // rows 2q and 2q+1, columns 4L .. 4L+3
   if (p.s0) {
-    const float4* src = reinterpret_cast<const float4*>(p.s0 + (bh * kHead + e) * kHead + 16 * hi);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      float4 x = src[q];
-      S[4 * q] = x.x; S[4 * q + 1] = x.y; S[4 * q + 2] = x.z; S[4 * q + 3] = x.w;
-    }
+    const float* base = p.s0 + (bh * kHead + 2 * q) * kHead + 4 * L;
+    const float4 x0 = *reinterpret_cast<const float4*>(base);
+    const float4 x1 = *reinterpret_cast<const float4*>(base + kHead);
+    S0[0] = x0.x; S0[1] = x0.y; S0[2] = x0.z; S0[3] = x0.w;
+    S1[0] = x1.x; S1[1] = x1.y; S1[2] = x1.z; S1[3] = x1.w;
   } else {
 #pragma unroll
-    for (int m = 0; m < 16; ++m) S[m] = 0.0f;
+    for (int c = 0; c < 4; ++c) { S0[c] = 0.0f; S1[c] = 0.0f; }
   }
 
   typedef Io<Tin> io;
-  typename io::raw pre[V_COUNT];
+  typename io::raw pre[3];
+  const Tin* src0 = st_half ? p.v : p.w;
+  const Tin* src1 = st_half ? p.a : p.r;
+  const Tin* src2 = st_half ? p.b : p.k;
   auto gload = [&](int t0) {
     if (t0 + sl < T) {
       const int64_t off = tok0 + (int64_t)(t0 + sl) * tstride + 4 * pp;
-      pre[V_W] = io::load(p.w + off);
-      pre[V_R] = io::load(p.r + off);
-      pre[V_K] = io::load(p.k + off);
-      pre[V_V] = io::load(p.v + off);
-      pre[V_A] = io::load(p.a + off);
-      pre[V_B] = io::load(p.b + off);
+      pre[0] = io::load(src0 + off);
+      pre[1] = io::load(src1 + off);
+      pre[2] = io::load(src2 + off);
     }
   };
   auto lstore = [&](int buf, int t0) {
     if (t0 + sl < T) {
-      float4 x = io::widen(pre[V_W]);
-      x.x = decay_f(sigmoid_f(x.x));
-      x.y = decay_f(sigmoid_f(x.y));
-      x.z = decay_f(sigmoid_f(x.z));
-      x.w = decay_f(sigmoid_f(x.w));
-      tile[buf][V_W][sl][pp] = x;
-      tile[buf][V_R][sl][pp] = io::widen(pre[V_R]);
-      tile[buf][V_K][sl][pp] = io::widen(pre[V_K]);
-      tile[buf][V_V][sl][pp] = io::widen(pre[V_V]);
-      tile[buf][V_A][sl][pp] = io::widen(pre[V_A]);
-      tile[buf][V_B][sl][pp] = io::widen(pre[V_B]);
+      float4 x0 = io::widen(pre[0]);
+      if (!st_half) {
+        x0.x = decay_f(sigmoid_f(x0.x));
+        x0.y = decay_f(sigmoid_f(x0.y));
+        x0.z = decay_f(sigmoid_f(x0.z));
+        x0.w = decay_f(sigmoid_f(x0.w));
+      }
+      tile[buf][st_half ? V_V : V_W][sl][pp] = x0;
+      tile[buf][st_half ? V_A : V_R][sl][pp] = io::widen(pre[1]);
+      tile[buf][st_half ? V_B : V_K][sl][pp] = io::widen(pre[2]);
     }
   };
   auto lread = [&](int buf, int s) {
     StepOps o;
     o.w = tile[buf][V_W][s][L];
-    o.r = tile[buf][V_R][s][L];
-    o.k = tile[buf][V_K][s][L];
     o.a = tile[buf][V_A][s][L];
     o.b = tile[buf][V_B][s][L];
-    o.ve = reinterpret_cast<const float*>(tile[buf][V_V][s])[e];
+    o.k = tile[buf][V_K][s][L];
+    o.r = tile[buf][V_R][s][L];
+    o.v = reinterpret_cast<const float2*>(tile[buf][V_V][s])[q];
     return o;
+  };
+
+  // checkpoint c: S after step c*C + C - 1, stored key-major ([i][j])
+  const int C = p.C;
+  const int64_t nchunks = T / C;
+  float* ckpt_bh = p.ckpt + (bh * nchunks * kHead + 4 * L) * kHead + 2 * q;
+  const bool defer_ckpt = C >= kTile;   // at most one checkpoint per tile
+  int until_ckpt = C;
+  int64_t chunk = 0;
+  bool ck_pending = false;
+  float Ck0[4], Ck1[4];
+  auto ck_store = [&](int64_t c, const float* a0, const float* a1) {
+    float* dst = ckpt_bh + c * (kHead * kHead);
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+      *reinterpret_cast<float2*>(dst + m * kHead) = make_float2(a0[m], a1[m]);
+  };
+
+  auto step = [&](const StepOps& o, int buf, int s) {
+    float sa0, sa1, y;
+    fwd_step(S0, S1, o.w, o.a, o.b, o.k, o.r, o.v, L, sa0, sa1, y);
+    if ((L & 7) == 0) ost[buf][0][s][2 * q + (L >> 3)] = y;
+    if (L == 0) reinterpret_cast<float2*>(ost[buf][1][s])[q] = make_float2(sa0, sa1);
+    if (--until_ckpt == 0) {   // (t + 1) % C == 0, kernel.rs:89-102
+      until_ckpt = C;
+      if (defer_ckpt) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) { Ck0[m] = S0[m]; Ck1[m] = S1[m]; }
+        ck_pending = true;
+      } else {
+        ck_store(chunk++, S0, S1);
+      }
+    }
   };
 
   const int ntiles = (T + kTile - 1) / kTile;
@@ -122,30 +152,6 @@ __global__ __launch_bounds__(kThreads) void wkv7_fwd_kernel(FwdParams<Tin> p) {
     lstore(0, 0);
   }
   __syncthreads();
-
-  int until_ckpt = p.C;
-  int64_t chunk = 0;
-  const int64_t nchunks = T / p.C;
-  float* ckpt_bh = p.ckpt + bh * nchunks * (kHead * kHead) + (16 * hi) * kHead + e;
-
-  auto step = [&](const StepOps& o, int buf, int s) {
-    float sa0 = 0.0f, sa1 = 0.0f;
-    fwd_sa16(sa0, sa1, o.a, S);
-    const float sa = seg_sum(sa0 + sa1);
-    float y0 = 0.0f, y1 = 0.0f;
-    fwd_upd8_q0(S, y0, y1, o.w, o.b, o.k, o.r, sa, o.ve);
-    fwd_upd8_q2(S + 8, y0, y1, o.w, o.b, o.k, o.r, sa, o.ve);
-    const float y = seg_sum(y0 + y1);
-    ost[buf][0][s][e] = y;
-    ost[buf][1][s][e] = sa;
-    if (--until_ckpt == 0) {   // (t + 1) % C == 0, kernel.rs:89-102
-      until_ckpt = p.C;
-      float* dst = ckpt_bh + chunk * (kHead * kHead);
-#pragma unroll
-      for (int m = 0; m < 16; ++m) dst[m * kHead] = S[m];
-      ++chunk;
-    }
-  };
 
   for (int ti = 0; ti < ntiles; ++ti) {
     const int buf = ti & 1;
@@ -166,8 +172,12 @@ __global__ __launch_bounds__(kThreads) void wkv7_fwd_kernel(FwdParams<Tin> p) {
     if (s < nst) step(A, buf, s);
 
     if (ti + 1 < ntiles) lstore(buf ^ 1, t0 + kTile);
+    if (ck_pending) {
+      ck_store(chunk++, Ck0, Ck1);
+      ck_pending = false;
+    }
     __syncthreads();
-    if (sl < nst) {
+    if (tid < 256 && sl < nst) {
       const int64_t off = tok0 + (int64_t)(t0 + sl) * tstride + 4 * pp;
       io::store(p.y + off, reinterpret_cast<const float4*>(ost[buf][0][sl])[pp]);
       *reinterpret_cast<float4*>(p.sa + off) = reinterpret_cast<const float4*>(ost[buf][1][sl])[pp];
@@ -175,10 +185,9 @@ __global__ __launch_bounds__(kThreads) void wkv7_fwd_kernel(FwdParams<Tin> p) {
   }
 
   if (p.sT) {
-    float4* dst = reinterpret_cast<float4*>(p.sT + (bh * kHead + e) * kHead + 16 * hi);
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      dst[q] = make_float4(S[4 * q], S[4 * q + 1], S[4 * q + 2], S[4 * q + 3]);
+    float* base = p.sT + (bh * kHead + 2 * q) * kHead + 4 * L;
+    *reinterpret_cast<float4*>(base) = make_float4(S0[0], S0[1], S0[2], S0[3]);
+    *reinterpret_cast<float4*>(base + kHead) = make_float4(S1[0], S1[1], S1[2], S1[3]);
   }
 }
 

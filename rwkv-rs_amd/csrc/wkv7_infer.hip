@@ -12,10 +12,10 @@
 // want its arithmetic pass use_dither explicitly.
 //
 // Design: the forward kernel's thread layout and per-step arithmetic (one
-// workgroup per (active row, head), state row e / segment hi in VGPRs, DPP
-// quad-broadcast operands from LDS). At T = 1 the kernel is bound by the
-// 16 KiB state read and 16 KiB state write per (row, head): every thread moves
-// 64 contiguous bytes each way, and the grid has Ba*H workgroups.
+// workgroup per (active row, head), a 2x4 state block per thread in VGPRs,
+// operands from LDS). At T = 1 the kernel is bound by the 16 KiB state read
+// and 16 KiB state write per (row, head): every thread moves two 16-byte rows
+// each way, and the grid has Ba*H workgroups.
 #include "wkv7_device.hpp"
 #include "wkv7_launch.hpp"
 
@@ -25,10 +25,6 @@ namespace {
 constexpr int kTile = 16;
 enum { V_W = 0, V_R, V_K, V_V, V_A, V_B, V_COUNT };
 
-struct StepOps {
-  float4 w, r, k, a, b;
-  float ve;
-};
 
 __device__ __forceinline__ float dither_f(uint32_t seed) {
   const uint32_t mixed = seed * 2654435769u;          // wrapping u32 product
@@ -62,10 +58,10 @@ __global__ __launch_bounds__(kThreads) void wkv7_infer_kernel(InferParams<Tin> p
   __shared__ int live[2][kTile];                   // step not masked
 
   const int h = blockIdx.x, bi = blockIdx.y;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int L = lane & 15, g = lane >> 4, lo = L & 3, hi = L >> 2;
-  const int e = 16 * wave + 4 * g + lo;
-  const int sl = tid >> 4, pp = tid & 15;
+  const int tid = threadIdx.x;
+  const int L = tid & 15, q = tid >> 4;   // columns 4L.., rows 2q, 2q+1
+  const int sl = (tid >> 4) & 15, pp = tid & 15;   // staging (threads 0..255)
+  const bool stager = tid < 16 * kTile;
 
   const int T = p.T;
   const int64_t slot = p.batch_ids[bi];
@@ -83,12 +79,13 @@ __global__ __launch_bounds__(kThreads) void wkv7_infer_kernel(InferParams<Tin> p
   const int64_t tstride = (int64_t)p.H * kHead;
   const int64_t tok0 = ((int64_t)bi * T * p.H + h) * kHead;
 
-  float* st = p.state + ((slot * p.H + h) * kHead + e) * kHead + 16 * hi;
-  float S[16];
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const float4 x = reinterpret_cast<const float4*>(st)[q];
-    S[4 * q] = x.x; S[4 * q + 1] = x.y; S[4 * q + 2] = x.z; S[4 * q + 3] = x.w;
+  float* st = p.state + ((slot * p.H + h) * kHead + 2 * q) * kHead + 4 * L;
+  float S0[4], S1[4];
+  {
+    const float4 x0 = *reinterpret_cast<const float4*>(st);
+    const float4 x1 = *reinterpret_cast<const float4*>(st + kHead);
+    S0[0] = x0.x; S0[1] = x0.y; S0[2] = x0.z; S0[3] = x0.w;
+    S1[0] = x1.x; S1[1] = x1.y; S1[2] = x1.z; S1[3] = x1.w;
   }
 
   typedef Io<Tin> io;
@@ -99,7 +96,7 @@ __global__ __launch_bounds__(kThreads) void wkv7_infer_kernel(InferParams<Tin> p
 
   auto gload = [&](int t0) {
     const int t = t0 + sl;
-    if (t < T) {
+    if (stager && t < T) {
       pre_live = !p.mask || mask_on<Tin>(p.mask, (int64_t)bi * T + t);
       uint32_t vt = valid_before_tile;
       if (p.mask) {
@@ -118,7 +115,7 @@ __global__ __launch_bounds__(kThreads) void wkv7_infer_kernel(InferParams<Tin> p
     }
   };
   auto lstore = [&](int buf, int t0) {
-    if (t0 + sl < T) {
+    if (stager && t0 + sl < T) {
       float4 x = io::widen(pre[V_W]);
       const float dith = p.use_dither ? dither_f(elapsed + pre_vt) : 0.0f;
       x.x = decay_f(sigmoid_f(x.x)) + dith;
@@ -158,35 +155,24 @@ __global__ __launch_bounds__(kThreads) void wkv7_infer_kernel(InferParams<Tin> p
     for (int s = 0; s < nst; ++s) {
       float y = 0.0f;
       if (live[buf][s]) {   // uniform across the workgroup
-        StepOps o;
-        o.w = tile[buf][V_W][s][L];
-        o.r = tile[buf][V_R][s][L];
-        o.k = tile[buf][V_K][s][L];
-        o.a = tile[buf][V_A][s][L];
-        o.b = tile[buf][V_B][s][L];
-        o.ve = reinterpret_cast<const float*>(tile[buf][V_V][s])[e];
-        float sa0 = 0.0f, sa1 = 0.0f;
-        fwd_sa16(sa0, sa1, o.a, S);
-        const float sa = seg_sum(sa0 + sa1);
-        float y0 = 0.0f, y1 = 0.0f;
-        fwd_upd8_q0(S, y0, y1, o.w, o.b, o.k, o.r, sa, o.ve);
-        fwd_upd8_q2(S + 8, y0, y1, o.w, o.b, o.k, o.r, sa, o.ve);
-        y = seg_sum(y0 + y1);
+        float sa0, sa1;
+        fwd_step(S0, S1, tile[buf][V_W][s][L], tile[buf][V_A][s][L], tile[buf][V_B][s][L],
+                 tile[buf][V_K][s][L], tile[buf][V_R][s][L],
+                 reinterpret_cast<const float2*>(tile[buf][V_V][s])[q], L, sa0, sa1, y);
       }
-      ost[buf][s][e] = y;
+      if ((L & 7) == 0) ost[buf][s][2 * q + (L >> 3)] = y;
     }
 
     if (ti + 1 < ntiles) lstore(buf ^ 1, t0 + kTile);
     __syncthreads();
-    if (sl < nst) {
+    if (stager && sl < nst) {
       const int64_t off = tok0 + (int64_t)(t0 + sl) * tstride + 4 * pp;
       io::store(p.y + off, reinterpret_cast<const float4*>(ost[buf][sl])[pp]);
     }
   }
 
-#pragma unroll
-  for (int q = 0; q < 4; ++q)
-    reinterpret_cast<float4*>(st)[q] = make_float4(S[4 * q], S[4 * q + 1], S[4 * q + 2], S[4 * q + 3]);
+  *reinterpret_cast<float4*>(st) = make_float4(S0[0], S0[1], S0[2], S0[3]);
+  *reinterpret_cast<float4*>(st + kHead) = make_float4(S1[0], S1[1], S1[2], S1[3]);
 }
 
 template <typename Tin>
