@@ -43,13 +43,15 @@ constexpr int kTile = 8;   // timesteps per LDS tile
 enum {
   V_R = 0, V_K, V_B, V_W, V_A,   // key-indexed: row role
   V_DY, V_V, V_SA,               // value-indexed: column role (dy also row role)
-  V_DWF,                         // W_SCALE * w~ * sig * (1 - sig), used at the flush
+  V_DWF,                         // W_SCALE * w~ * sig * (1 - sig)
   V_COUNT
 };
 // per-column-pair records for the column role, float4 {x[2p], x[2p+1], y[2p], y[2p+1]}
-enum { P_RK = 0, P_BW, P_AI, P_COUNT };   // {r, k}, {b, w~}, {a, 1/w~}
+enum { P_RK = 0, P_BA, P_WI, P_COUNT };   // {r, k}, {b, a}, {w~, 1/w~}
 // staged outputs per timestep, in the order the reduce-scatters deliver them
 enum { O_DV = 0, O_DR, O_DW, O_DK, O_DB, O_DA, O_COUNT };
+// raw (input dtype) operand rows as loaded from global memory
+enum { R_W = 0, R_R, R_K, R_V, R_A, R_B, R_DY, R_COUNT };
 
 __device__ __forceinline__ void unpack4(float* d, float4 x) {
   d[0] = x.x; d[1] = x.y; d[2] = x.z; d[3] = x.w;
@@ -57,7 +59,7 @@ __device__ __forceinline__ void unpack4(float* d, float4 x) {
 
 template <typename Tin>
 struct BwdParams {
-  const Tin *w, *r, *k, *v, *a, *b, *dy;
+  const Tin* in[R_COUNT];   // w, r, k, v, a, b, dy (R_* order)
   const float* ckpt;
   const float* sa;
   const float* dsT;
@@ -66,25 +68,110 @@ struct BwdParams {
   int T, H, C;
 };
 
-template <typename Tin>
+// kCkTiled: C is a multiple of the tile length, so every checkpoint reload
+// happens at the last step of a tile and the checkpoint travels with that
+// tile (loaded into LDS one tile ahead). Otherwise reloads read global memory
+// directly. The two are separate instantiations so that the compiler never
+// merges the LDS and global reads into one generic (flat) access.
+template <typename Tin, bool kCkTiled>
 __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
-  __shared__ float4 tile[2][V_COUNT][kTile][16];   // 36 KiB
-  __shared__ float4 pairs[2][P_COUNT][kTile][32];  // 24 KiB
-  __shared__ float ost[2][O_COUNT][kTile][kHead];  // 24 KiB
-  __shared__ float4 dsab[2][16];                   // dsa of the step, by parity
+  constexpr int kRow = kHead * sizeof(Tin);                // bytes of one raw row
+  constexpr int kRawBytes = R_COUNT * kTile * kRow + kTile * kHead * 4;
+  __shared__ float4 tile[V_COUNT][kTile][16];              // 18 KiB
+  __shared__ float4 pairs[P_COUNT][kTile][32];             // 12 KiB
+  __shared__ float ost[O_COUNT][kTile][kHead];             // 12 KiB
+  __shared__ float4 ckbuf[2][kHead * kHead / 4];           // 32 KiB, by tile parity
+  __shared__ float4 raw[kRawBytes / 16];                   // 9 or 16 KiB
+  __shared__ float4 dsab[2][16];                           // dsa of the step, by parity
 
   const int h = blockIdx.x, bi = blockIdx.y;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63;
   const int L = tid & 15, q = tid >> 4;
-  const int sl = (tid >> 4) & 7, pp = tid & 15;   // staging (threads 0..127)
-  const bool stager = tid < 16 * kTile;
+  // conversion: group sg = tid / 128 (0: w; 1: r, k; 2: b, a; 3: dy, v, sa),
+  // timestep sl, elements 4pp .. 4pp+3
+  const int sg = tid >> 7, sl = (tid >> 4) & 7, pp = tid & 15;
 
   const int T = p.T, C = p.C;
   const int64_t bh = (int64_t)bi * p.H + h;
   const int64_t tstride = (int64_t)p.H * kHead;
   const int64_t tok0 = ((int64_t)bi * T * p.H + h) * kHead;
+  const int64_t nchunks = T / C;
+  const float* ckpt_bh = p.ckpt + bh * nchunks * (kHead * kHead);
+  auto ck_needed = [&](int t0, int nst) { return kCkTiled && ((t0 + nst) % C) == 0; };
 
-  float dSr[2][4], Sc[4][2], dSc[4][2], Pf[4][2];
+  // Issue the loads of tile [t0, t0+nst) into `raw` (and its checkpoint into
+  // ckbuf[par]); they complete while another tile is computed.
+  auto issue = [&](int t0, int nst, int par) {
+    constexpr int kChunksTok = R_COUNT * kTile * kRow / 16;
+    constexpr int kChunks = kRawBytes / 16;
+    for (int c0 = tid - lane; c0 < kChunks; c0 += kThreads) {   // wave-uniform loop
+      const int c = c0 + lane;
+      const int wrow = __builtin_amdgcn_readfirstlane(c0 < kChunksTok ? c0 / (kRow / 16) : 0);
+      const char* src;
+      int step;
+      if (c0 < kChunksTok) {
+        const int row = c / (kRow / 16), col = c % (kRow / 16);
+        step = row % kTile;
+        const Tin* base = p.in[wrow / kTile];   // one operand per wave-load (uniform)
+        src = reinterpret_cast<const char*>(base + tok0 + (int64_t)(t0 + step) * tstride) + 16 * col;
+      } else {
+        const int cc = c - kChunksTok;
+        step = cc / 16;
+        src = reinterpret_cast<const char*>(p.sa + tok0 + (int64_t)(t0 + step) * tstride) + 16 * (cc % 16);
+      }
+      if (step < nst) load_lds16(src, &raw[c0]);
+    }
+    if (ck_needed(t0, nst)) {
+      const float4* src = reinterpret_cast<const float4*>(
+          ckpt_bh + (int64_t)((t0 + nst) / C - 1) * (kHead * kHead));
+      load_lds16(src + tid, &ckbuf[par][tid - lane]);
+      load_lds16(src + kThreads + tid, &ckbuf[par][kThreads + tid - lane]);
+    }
+  };
+  // raw tile -> fp32 operand vectors and column-pair records
+  auto convert = [&](int nst) {
+    if (sl >= nst) return;
+    const char* rb = reinterpret_cast<const char*>(raw);
+    auto rawv = [&](int vec) {
+      return Io<Tin>::widen(*reinterpret_cast<const typename Io<Tin>::raw*>(
+          rb + (vec * kTile + sl) * kRow + 4 * pp * sizeof(Tin)));
+    };
+    if (sg == 0) {
+      const float4 x = rawv(R_W);
+      const float xs[4] = {x.x, x.y, x.z, x.w};
+      float ws[4], iws[4], dws[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float sig = sigmoid_f(xs[c]);
+        ws[c] = decay_f(sig);
+        iws[c] = 1.0f / ws[c];
+        dws[c] = kWScale * ws[c] * sig * (1.0f - sig);
+      }
+      tile[V_W][sl][pp] = make_float4(ws[0], ws[1], ws[2], ws[3]);
+      tile[V_DWF][sl][pp] = make_float4(dws[0], dws[1], dws[2], dws[3]);
+      pairs[P_WI][sl][2 * pp] = make_float4(ws[0], ws[1], iws[0], iws[1]);
+      pairs[P_WI][sl][2 * pp + 1] = make_float4(ws[2], ws[3], iws[2], iws[3]);
+    } else if (sg == 1) {
+      const float4 r = rawv(R_R), k = rawv(R_K);
+      tile[V_R][sl][pp] = r;
+      tile[V_K][sl][pp] = k;
+      pairs[P_RK][sl][2 * pp] = make_float4(r.x, r.y, k.x, k.y);
+      pairs[P_RK][sl][2 * pp + 1] = make_float4(r.z, r.w, k.z, k.w);
+    } else if (sg == 2) {
+      const float4 b = rawv(R_B), a = rawv(R_A);
+      tile[V_B][sl][pp] = b;
+      tile[V_A][sl][pp] = a;
+      pairs[P_BA][sl][2 * pp] = make_float4(b.x, b.y, a.x, a.y);
+      pairs[P_BA][sl][2 * pp + 1] = make_float4(b.z, b.w, a.z, a.w);
+    } else {
+      tile[V_DY][sl][pp] = rawv(R_DY);
+      tile[V_V][sl][pp] = rawv(R_V);
+      tile[V_SA][sl][pp] = *reinterpret_cast<const float4*>(
+          rb + R_COUNT * kTile * kRow + (sl * kHead + 4 * pp) * 4);
+    }
+  };
+
+  float dSr[2][4], Sc[4][2], dSc[4][2];
 #pragma unroll
   for (int c = 0; c < 4; ++c) { Sc[c][0] = 0.0f; Sc[c][1] = 0.0f; }
   if (p.dsT) {
@@ -104,100 +191,46 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
     }
   }
 
-  // checkpoint c holds S after step c*C + C - 1, key-major ([i][j]): its row
-  // 2q+d, entries 4L .. 4L+3, is Sc[0..3][d].
-  const int64_t nchunks = T / C;
-  const float* ckpt_bh = p.ckpt + (bh * nchunks * kHead + 2 * q) * kHead + 4 * L;
-  auto ckload = [&](int64_t c) {
-    const float* src = ckpt_bh + c * (kHead * kHead);
-    const float4 x0 = *reinterpret_cast<const float4*>(src);
-    const float4 x1 = *reinterpret_cast<const float4*>(src + kHead);
-    Pf[0][0] = x0.x; Pf[1][0] = x0.y; Pf[2][0] = x0.z; Pf[3][0] = x0.w;
-    Pf[0][1] = x1.x; Pf[1][1] = x1.y; Pf[2][1] = x1.z; Pf[3][1] = x1.w;
-  };
-  int64_t next_chunk = nchunks - 1;
-  if (next_chunk >= 0) ckload(next_chunk);
-
-  typedef Io<Tin> io;
-  typename io::raw pre[7];
-  float4 pre_sa;
-  auto gload = [&](int t0) {
-    if (stager && t0 + sl < T) {
-      const int64_t off = tok0 + (int64_t)(t0 + sl) * tstride + 4 * pp;
-      pre[0] = io::load(p.w + off);
-      pre[1] = io::load(p.r + off);
-      pre[2] = io::load(p.k + off);
-      pre[3] = io::load(p.v + off);
-      pre[4] = io::load(p.a + off);
-      pre[5] = io::load(p.b + off);
-      pre[6] = io::load(p.dy + off);
-      pre_sa = *reinterpret_cast<const float4*>(p.sa + off);
-    }
-  };
-  auto lstore = [&](int buf, int t0) {
-    if (stager && t0 + sl < T) {
-      const float4 x = io::widen(pre[0]);
-      const float xs[4] = {x.x, x.y, x.z, x.w};
-      float ws[4], iws[4], dws[4];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const float sig = sigmoid_f(xs[c]);
-        ws[c] = decay_f(sig);
-        iws[c] = 1.0f / ws[c];
-        dws[c] = kWScale * ws[c] * sig * (1.0f - sig);
-      }
-      const float4 r = io::widen(pre[1]), k = io::widen(pre[2]), a = io::widen(pre[4]);
-      const float4 b = io::widen(pre[5]);
-      const float4 w = make_float4(ws[0], ws[1], ws[2], ws[3]);
-      const float4 iw = make_float4(iws[0], iws[1], iws[2], iws[3]);
-      tile[buf][V_R][sl][pp] = r;
-      tile[buf][V_K][sl][pp] = k;
-      tile[buf][V_B][sl][pp] = b;
-      tile[buf][V_W][sl][pp] = w;
-      tile[buf][V_A][sl][pp] = a;
-      tile[buf][V_DY][sl][pp] = io::widen(pre[6]);
-      tile[buf][V_V][sl][pp] = io::widen(pre[3]);
-      tile[buf][V_SA][sl][pp] = pre_sa;
-      tile[buf][V_DWF][sl][pp] = make_float4(dws[0], dws[1], dws[2], dws[3]);
-      // columns 4pp .. 4pp+3 are column pairs 2pp and 2pp+1
-      pairs[buf][P_RK][sl][2 * pp] = make_float4(r.x, r.y, k.x, k.y);
-      pairs[buf][P_RK][sl][2 * pp + 1] = make_float4(r.z, r.w, k.z, k.w);
-      pairs[buf][P_BW][sl][2 * pp] = make_float4(b.x, b.y, w.x, w.y);
-      pairs[buf][P_BW][sl][2 * pp + 1] = make_float4(b.z, b.w, w.z, w.w);
-      pairs[buf][P_AI][sl][2 * pp] = make_float4(a.x, a.y, iw.x, iw.y);
-      pairs[buf][P_AI][sl][2 * pp + 1] = make_float4(a.z, a.w, iw.z, iw.w);
-    }
-  };
-
   int until_reload = 0;   // steps until the next checkpoint reload
+  int64_t reload_chunk = nchunks - 1;
   int parity = 0;
 
-  auto step = [&](int buf, int s) {
+  // One timestep (kernel.rs:177-297); `par` selects this tile's checkpoint.
+  auto step = [&](int s, int par) {
     if (until_reload == 0) {   // (t + 1) % C == 0, kernel.rs:210-228
       until_reload = C;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) { Sc[c][0] = Pf[c][0]; Sc[c][1] = Pf[c][1]; }
-      --next_chunk;
-      if (next_chunk >= 0) ckload(next_chunk);
+      // checkpoint row 2q+d, entries 4L .. 4L+3, is Sc[0..3][d]
+      float4 x0, x1;
+      if constexpr (kCkTiled) {
+        x0 = ckbuf[par][((2 * q) * kHead + 4 * L) / 4];
+        x1 = ckbuf[par][((2 * q + 1) * kHead + 4 * L) / 4];
+      } else {
+        const float* src = ckpt_bh + reload_chunk * (kHead * kHead) + (2 * q) * kHead + 4 * L;
+        x0 = *reinterpret_cast<const float4*>(src);
+        x1 = *reinterpret_cast<const float4*>(src + kHead);
+      }
+      Sc[0][0] = x0.x; Sc[1][0] = x0.y; Sc[2][0] = x0.z; Sc[3][0] = x0.w;
+      Sc[0][1] = x1.x; Sc[1][1] = x1.y; Sc[2][1] = x1.z; Sc[3][1] = x1.w;
+      --reload_chunk;
     }
     --until_reload;
 
     // row role operands: columns 4L..4L+3, rows 2q, 2q+1
     float rr[4], kk[4], bb[4];
-    unpack4(rr, tile[buf][V_R][s][L]);
-    unpack4(kk, tile[buf][V_K][s][L]);
-    unpack4(bb, tile[buf][V_B][s][L]);
-    const float2 dyr = reinterpret_cast<const float2*>(tile[buf][V_DY][s])[q];
+    unpack4(rr, tile[V_R][s][L]);
+    unpack4(kk, tile[V_K][s][L]);
+    unpack4(bb, tile[V_B][s][L]);
+    const float2 dyr = reinterpret_cast<const float2*>(tile[V_DY][s])[q];
     // column role operands: rows 4L..4L+3, columns 2q, 2q+1
     float dy[4], v[4], sa[4];
-    unpack4(dy, tile[buf][V_DY][s][L]);
-    unpack4(v, tile[buf][V_V][s][L]);
-    unpack4(sa, tile[buf][V_SA][s][L]);
-    const float4 prk = pairs[buf][P_RK][s][q], pbw = pairs[buf][P_BW][s][q];
-    const float4 pai = pairs[buf][P_AI][s][q];
+    unpack4(dy, tile[V_DY][s][L]);
+    unpack4(v, tile[V_V][s][L]);
+    unpack4(sa, tile[V_SA][s][L]);
+    const float4 prk = pairs[P_RK][s][q], pba = pairs[P_BA][s][q];
+    const float4 pwi = pairs[P_WI][s][q];
     const float rc[2] = {prk.x, prk.y}, kc[2] = {prk.z, prk.w};
-    const float bc[2] = {pbw.x, pbw.y}, wc[2] = {pbw.z, pbw.w};
-    const float ac[2] = {pai.x, pai.y}, iwc[2] = {pai.z, pai.w};
+    const float bc[2] = {pba.x, pba.y}, ac[2] = {pba.z, pba.w};
+    const float wc[2] = {pwi.x, pwi.y}, iwc[2] = {pwi.z, pwi.w};
 
     // row role: dS row += dy r^T (kernel.rs:248); dv, dsa (kernel.rs:261-262)
     const float dyd[2] = {dyr.x, dyr.y};
@@ -233,17 +266,23 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
     // dv (rows 2q, 2q+1) and dr, dw~, dk (columns 2q, 2q+1): one lane pair each
     float early[8] = {dvp[0], dvp[1], drp[0], drp[1], dwp[0], dwp[1], dkp[0], dkp[1]};
     row16_scatter<8>(early, L);
-    if ((L & 1) == 0) ost[buf][O_DV + (L >> 2)][s][2 * q + ((L >> 1) & 1)] = early[0];
+    if ((L & 1) == 0) {
+      const int o = O_DV + (L >> 2), idx = 2 * q + ((L >> 1) & 1);
+      float val = early[0];
+      // dw = W_SCALE * dw~ * w~ * sig * (1 - sig), kernel.rs:267-271
+      if (o == O_DW) val *= reinterpret_cast<const float*>(tile[V_DWF][s])[idx];
+      ost[o][s][idx] = val;
+    }
 
-    __syncthreads();   // dsa of every row visible
+    lds_barrier();   // dsa of every row visible
     float ds[4];
     unpack4(ds, dsab[parity][L]);
     parity ^= 1;
 
     // row role: dS row = dS row * w~ + dsa a^T (kernel.rs:290-291)
     float ww[4], aa[4];
-    unpack4(ww, tile[buf][V_W][s][L]);
-    unpack4(aa, tile[buf][V_A][s][L]);
+    unpack4(ww, tile[V_W][s][L]);
+    unpack4(aa, tile[V_A][s][L]);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       dSr[0][c] = __builtin_fmaf(dsa0, aa[c], dSr[0][c] * ww[c]);
@@ -261,36 +300,46 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
     // db, da (columns 2q, 2q+1): four lanes each
     float late[4] = {dbp[0], dbp[1], dap[0], dap[1]};
     row16_scatter<4>(late, L);
-    if ((L & 3) == 0) ost[buf][O_DB + (L >> 3)][s][2 * q + ((L >> 2) & 1)] = late[0];
+    if ((L & 3) == 0) ost[O_DB + (L >> 3)][s][2 * q + ((L >> 2) & 1)] = late[0];
   };
 
+  // Tile pipeline (tiles run backwards in time). While tile ti is computed,
+  // the raw operands of tile ti-1 stream into LDS. At the tile end one wait +
+  // barrier makes them visible; the outputs of tile ti are flushed and tile
+  // ti-1 is converted to fp32 (a different LDS region), a barrier, and the
+  // loads for tile ti-2 are issued.
   const int ntiles = (T + kTile - 1) / kTile;
+  auto tile_t0 = [&](int ti) { return ti * kTile; };
+  auto tile_n = [&](int ti) { return min(kTile, T - ti * kTile); };
   if (ntiles > 0) {
-    gload((ntiles - 1) * kTile);
-    lstore((ntiles - 1) & 1, (ntiles - 1) * kTile);
-  }
-  __syncthreads();
-
-  for (int ti = ntiles - 1; ti >= 0; --ti) {
-    const int buf = ti & 1;
-    const int t0 = ti * kTile;
-    const int nst = min(kTile, T - t0);
-    if (ti > 0) gload(t0 - kTile);
-    for (int s = nst - 1; s >= 0; --s) step(buf, s);
-    if (ti > 0) lstore(buf ^ 1, t0 - kTile);
+    issue(tile_t0(ntiles - 1), tile_n(ntiles - 1), (ntiles - 1) & 1);
+    __builtin_amdgcn_s_waitcnt(0);   // vmcnt/lgkmcnt 0
     __syncthreads();
-    if (stager && sl < nst) {
+    convert(tile_n(ntiles - 1));
+    __syncthreads();
+    if (ntiles > 1) issue(tile_t0(ntiles - 2), tile_n(ntiles - 2), (ntiles - 2) & 1);
+  }
+
+  // flush: threads 0..383, group fg = tid / 128 writes outputs 2fg and 2fg+1
+  const int fg = tid >> 7;
+  typedef Io<Tin> io;
+  for (int ti = ntiles - 1; ti >= 0; --ti) {
+    const int t0 = tile_t0(ti), nst = tile_n(ti);
+    for (int s = nst - 1; s >= 0; --s) step(s, ti & 1);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (fg < 3 && sl < nst) {
       const int64_t off = tok0 + (int64_t)(t0 + sl) * tstride + 4 * pp;
-      float4 dw = reinterpret_cast<const float4*>(ost[buf][O_DW][sl])[pp];
-      const float4 f = tile[buf][V_DWF][sl][pp];
-      dw.x *= f.x; dw.y *= f.y; dw.z *= f.z; dw.w *= f.w;   // kernel.rs:267-271
-      io::store(p.dw + off, dw);
-      io::store(p.dr + off, reinterpret_cast<const float4*>(ost[buf][O_DR][sl])[pp]);
-      io::store(p.dk + off, reinterpret_cast<const float4*>(ost[buf][O_DK][sl])[pp]);
-      io::store(p.dv + off, reinterpret_cast<const float4*>(ost[buf][O_DV][sl])[pp]);
-      io::store(p.da + off, reinterpret_cast<const float4*>(ost[buf][O_DA][sl])[pp]);
-      io::store(p.db + off, reinterpret_cast<const float4*>(ost[buf][O_DB][sl])[pp]);
+      const float4 x0 = reinterpret_cast<const float4*>(ost[2 * fg][sl])[pp];
+      const float4 x1 = reinterpret_cast<const float4*>(ost[2 * fg + 1][sl])[pp];
+      Tin* d0 = fg == 0 ? p.dv : fg == 1 ? p.dw : p.db;
+      Tin* d1 = fg == 0 ? p.dr : fg == 1 ? p.dk : p.da;
+      io::store(d0 + off, x0);
+      io::store(d1 + off, x1);
     }
+    if (ti > 0) convert(tile_n(ti - 1));
+    __syncthreads();
+    if (ti > 1) issue(tile_t0(ti - 2), tile_n(ti - 2), (ti - 2) & 1);
   }
 
   if (p.ds0) {   // kernel.rs:299-307
@@ -304,13 +353,13 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
 template <typename Tin>
 hipError_t launch_bwd_t(const BackwardDesc& d, hipStream_t stream) {
   BwdParams<Tin> p;
-  p.w = static_cast<const Tin*>(d.w);
-  p.r = static_cast<const Tin*>(d.r);
-  p.k = static_cast<const Tin*>(d.k);
-  p.v = static_cast<const Tin*>(d.v);
-  p.a = static_cast<const Tin*>(d.a);
-  p.b = static_cast<const Tin*>(d.b);
-  p.dy = static_cast<const Tin*>(d.dy);
+  p.in[R_W] = static_cast<const Tin*>(d.w);
+  p.in[R_R] = static_cast<const Tin*>(d.r);
+  p.in[R_K] = static_cast<const Tin*>(d.k);
+  p.in[R_V] = static_cast<const Tin*>(d.v);
+  p.in[R_A] = static_cast<const Tin*>(d.a);
+  p.in[R_B] = static_cast<const Tin*>(d.b);
+  p.in[R_DY] = static_cast<const Tin*>(d.dy);
   p.ckpt = d.ckpt;
   p.sa = d.sa;
   p.dsT = d.dsT;
@@ -324,7 +373,12 @@ hipError_t launch_bwd_t(const BackwardDesc& d, hipStream_t stream) {
   p.T = d.T;
   p.H = d.H;
   p.C = d.C;
-  hipLaunchKernelGGL(wkv7_bwd_kernel<Tin>, dim3(d.H, d.B, 1), dim3(kThreads, 1, 1), 0, stream, p);
+  if (d.C % kTile == 0)
+    hipLaunchKernelGGL((wkv7_bwd_kernel<Tin, true>), dim3(d.H, d.B, 1), dim3(kThreads, 1, 1), 0,
+                       stream, p);
+  else
+    hipLaunchKernelGGL((wkv7_bwd_kernel<Tin, false>), dim3(d.H, d.B, 1), dim3(kThreads, 1, 1), 0,
+                       stream, p);
   return hipGetLastError();
 }
 

@@ -137,6 +137,42 @@ __device__ __forceinline__ void row16_sum2(float& x0, float& x1, int L) {
   x1 = up ? x[0] : other;
 }
 
+// ---------------------------------------------------------- direct LDS loads
+// 16 bytes from global memory to LDS without passing through VGPRs
+// (global_load_lds_dwordx4, new in gfx950). `lds_wave_base` must be the same
+// for the whole wave: lane i writes lds_wave_base + 16 * i. Completion is
+// tracked by vmcnt; the caller waits for vmcnt 0 and barriers before reading
+// the data.
+//
+// Issued from inline asm on purpose: when the compiler sees an LDS DMA in
+// flight it cannot tell which LDS bytes it writes, so it makes every later
+// LDS read of the wave wait for vmcnt 0 first, which turns a prefetch one tile
+// ahead into a synchronous load at the next step. The compiler does not count
+// these loads in its own vmcnt bookkeeping; as vector memory operations
+// complete in issue order that only makes its own waits stricter.
+// M0 holds the LDS address (bound as an operand, so the compiler writes it);
+// an SALU write of M0 needs one wait state before an LDS DMA reads it.
+__device__ __forceinline__ void load_lds16(const void* src, void* lds_wave_base) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds_wave_base);
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(src), "{m0}"(m0)
+               : "memory");
+}
+
+// Workgroup barrier that orders LDS accesses only. __syncthreads() fences
+// every address space, which makes each wave wait for all of its global loads
+// (vmcnt 0) first; prefetches in flight then stall every step that has a
+// barrier. This one waits for the wave's LDS accesses alone, so loads issued
+// earlier (global_load_lds included, which the caller waits for explicitly
+// before reading what they wrote) keep flying across it.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // ------------------------------------------------------------- forward step
 // One timestep of the recurrence on a thread's 2x4 block: S0/S1 are rows 2q
 // and 2q+1, columns 4L .. 4L+3; w4, a4, b4, k4, r4 hold those columns of w~,

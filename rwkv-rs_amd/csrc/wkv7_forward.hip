@@ -12,14 +12,13 @@
 // of the state in VGPRs (layout in wkv7_device.hpp). Rows are independent in
 // the forward, so the only cross-lane work is the two row sums (sa and y),
 // four DPP steps each. Operands are staged through LDS in tiles of 16
-// timesteps: threads load one tile with coalesced 8/16-byte loads (one
-// timestep of one operand is a 128/256-byte row), widen bf16 to fp32 and
-// compute the decay once per element, and the next tile's global loads are in
-// flight while the current tile is consumed (double-buffered LDS). Per step a
-// thread reads its four columns of w~, a, b, k, r (five ds_read_b128) and its
-// two rows of v. y and sa are staged in LDS and written once per tile with
-// full-row stores; a checkpoint taken inside a tile is stored at the tile end,
-// after the tile's loads have been consumed, so no wait ever covers it.
+// timesteps: the raw rows of the next tile (one timestep of one operand is a
+// 128/256-byte row) stream from global memory straight into LDS
+// (global_load_lds_dwordx4, no VGPRs involved); at the tile end they are
+// widened to fp32 with the decay formed once per element. The loads are in
+// flight while the current tile is consumed. Per step a thread reads its four
+// columns of w~, a, b, k, r (five ds_read_b128) and its two rows of v. y and
+// sa are staged in LDS and written once per tile with full-row stores.
 #include "wkv7_device.hpp"
 #include "wkv7_launch.hpp"
 
@@ -28,7 +27,7 @@ namespace {
 
 constexpr int kTile = 16;   // timesteps per LDS tile
 
-// LDS operand vectors per timestep
+// LDS operand vectors per timestep (fp32), and raw rows as loaded
 enum { V_W = 0, V_R, V_K, V_V, V_A, V_B, V_COUNT };
 
 struct StepOps {
@@ -38,7 +37,7 @@ struct StepOps {
 
 template <typename Tin>
 struct FwdParams {
-  const Tin *w, *r, *k, *v, *a, *b;
+  const Tin* in[V_COUNT];   // w, r, k, v, a, b (V_* order)
   const float* s0;
   float* ckpt;
   float* sa;
@@ -47,16 +46,21 @@ struct FwdParams {
   int T, H, C;
 };
 
-template <typename Tin>
+// kDefer: C >= kTile, so a tile holds at most one checkpoint, which is kept in
+// registers and stored at the tile end instead of in the middle of the steps.
+template <typename Tin, bool kDefer>
 __global__ __launch_bounds__(kThreads) void wkv7_fwd_kernel(FwdParams<Tin> p) {
-  __shared__ float4 tile[2][V_COUNT][kTile][16];   // 48 KiB
-  __shared__ float ost[2][2][kTile][kHead];        // 16 KiB: y, sa
+  constexpr int kRow = kHead * sizeof(Tin);   // bytes of one raw row
+  constexpr int kRawBytes = V_COUNT * kTile * kRow;
+  __shared__ float4 tile[V_COUNT][kTile][16];   // 24 KiB
+  __shared__ float ost[2][kTile][kHead];        // 8 KiB: y, sa
+  __shared__ float4 raw[kRawBytes / 16];        // 12 or 24 KiB
 
   const int h = blockIdx.x, bi = blockIdx.y;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63;
   const int L = tid & 15, q = tid >> 4;   // columns 4L.., rows 2q, 2q+1
-  // staging: threads 0..255 stage w, r, k; threads 256..511 stage v, a, b
-  const int st_half = tid >> 8, sl = (tid >> 4) & 15, pp = tid & 15;
+  // conversion and flush: timestep sl, elements 4pp .. 4pp+3, half cg
+  const int cg = tid >> 8, sl = (tid >> 4) & 15, pp = tid & 15;
 
   const int T = p.T;
   const int64_t bh = (int64_t)bi * p.H + h;
@@ -76,40 +80,51 @@ __global__ __launch_bounds__(kThreads) void wkv7_fwd_kernel(FwdParams<Tin> p) {
   }
 
   typedef Io<Tin> io;
-  typename io::raw pre[3];
-  const Tin* src0 = st_half ? p.v : p.w;
-  const Tin* src1 = st_half ? p.a : p.r;
-  const Tin* src2 = st_half ? p.b : p.k;
-  auto gload = [&](int t0) {
-    if (t0 + sl < T) {
-      const int64_t off = tok0 + (int64_t)(t0 + sl) * tstride + 4 * pp;
-      pre[0] = io::load(src0 + off);
-      pre[1] = io::load(src1 + off);
-      pre[2] = io::load(src2 + off);
+  // Issue the loads of tile [t0, t0+nst) into `raw` (row vec*kTile + step).
+  auto issue = [&](int t0, int nst) {
+    constexpr int kChunks = kRawBytes / 16;
+    for (int c0 = tid - lane; c0 < kChunks; c0 += kThreads) {   // wave-uniform loop
+      const int c = c0 + lane;
+      const int row = c / (kRow / 16), col = c % (kRow / 16);
+      const int step = row % kTile;
+      const int vec = __builtin_amdgcn_readfirstlane(c0 / (kRow / 16)) / kTile;
+      const Tin* base = p.in[vec];   // kernel-argument array, uniform index
+      const char* src =
+          reinterpret_cast<const char*>(base + tok0 + (int64_t)(t0 + step) * tstride) + 16 * col;
+      if (step < nst) load_lds16(src, &raw[c0]);
     }
   };
-  auto lstore = [&](int buf, int t0) {
-    if (t0 + sl < T) {
-      float4 x0 = io::widen(pre[0]);
-      if (!st_half) {
-        x0.x = decay_f(sigmoid_f(x0.x));
-        x0.y = decay_f(sigmoid_f(x0.y));
-        x0.z = decay_f(sigmoid_f(x0.z));
-        x0.w = decay_f(sigmoid_f(x0.w));
-      }
-      tile[buf][st_half ? V_V : V_W][sl][pp] = x0;
-      tile[buf][st_half ? V_A : V_R][sl][pp] = io::widen(pre[1]);
-      tile[buf][st_half ? V_B : V_K][sl][pp] = io::widen(pre[2]);
+  // raw tile -> fp32 vectors; the decay w~ is formed here, once per element
+  auto convert = [&](int nst) {
+    if (sl >= nst) return;
+    const char* rb = reinterpret_cast<const char*>(raw);
+    auto rawv = [&](int vec) {
+      return io::widen(*reinterpret_cast<const typename io::raw*>(
+          rb + (vec * kTile + sl) * kRow + 4 * pp * sizeof(Tin)));
+    };
+    if (cg == 0) {
+      float4 x = rawv(V_W);
+      x.x = decay_f(sigmoid_f(x.x));
+      x.y = decay_f(sigmoid_f(x.y));
+      x.z = decay_f(sigmoid_f(x.z));
+      x.w = decay_f(sigmoid_f(x.w));
+      tile[V_W][sl][pp] = x;
+      tile[V_R][sl][pp] = rawv(V_R);
+      tile[V_K][sl][pp] = rawv(V_K);
+    } else {
+      tile[V_V][sl][pp] = rawv(V_V);
+      tile[V_A][sl][pp] = rawv(V_A);
+      tile[V_B][sl][pp] = rawv(V_B);
     }
   };
-  auto lread = [&](int buf, int s) {
+  auto lread = [&](int s) {
     StepOps o;
-    o.w = tile[buf][V_W][s][L];
-    o.a = tile[buf][V_A][s][L];
-    o.b = tile[buf][V_B][s][L];
-    o.k = tile[buf][V_K][s][L];
-    o.r = tile[buf][V_R][s][L];
-    o.v = reinterpret_cast<const float2*>(tile[buf][V_V][s])[q];
+    o.w = tile[V_W][s][L];
+    o.a = tile[V_A][s][L];
+    o.b = tile[V_B][s][L];
+    o.k = tile[V_K][s][L];
+    o.r = tile[V_R][s][L];
+    o.v = reinterpret_cast<const float2*>(tile[V_V][s])[q];
     return o;
   };
 
@@ -117,7 +132,6 @@ __global__ __launch_bounds__(kThreads) void wkv7_fwd_kernel(FwdParams<Tin> p) {
   const int C = p.C;
   const int64_t nchunks = T / C;
   float* ckpt_bh = p.ckpt + (bh * nchunks * kHead + 4 * L) * kHead + 2 * q;
-  const bool defer_ckpt = C >= kTile;   // at most one checkpoint per tile
   int until_ckpt = C;
   int64_t chunk = 0;
   bool ck_pending = false;
@@ -129,14 +143,14 @@ __global__ __launch_bounds__(kThreads) void wkv7_fwd_kernel(FwdParams<Tin> p) {
       *reinterpret_cast<float2*>(dst + m * kHead) = make_float2(a0[m], a1[m]);
   };
 
-  auto step = [&](const StepOps& o, int buf, int s) {
+  auto step = [&](const StepOps& o, int s) {
     float sa0, sa1, y;
     fwd_step(S0, S1, o.w, o.a, o.b, o.k, o.r, o.v, L, sa0, sa1, y);
-    if ((L & 7) == 0) ost[buf][0][s][2 * q + (L >> 3)] = y;
-    if (L == 0) reinterpret_cast<float2*>(ost[buf][1][s])[q] = make_float2(sa0, sa1);
+    if ((L & 7) == 0) ost[0][s][2 * q + (L >> 3)] = y;
+    if (L == 0) reinterpret_cast<float2*>(ost[1][s])[q] = make_float2(sa0, sa1);
     if (--until_ckpt == 0) {   // (t + 1) % C == 0, kernel.rs:89-102
       until_ckpt = C;
-      if (defer_ckpt) {
+      if constexpr (kDefer) {
 #pragma unroll
         for (int m = 0; m < 4; ++m) { Ck0[m] = S0[m]; Ck1[m] = S1[m]; }
         ck_pending = true;
@@ -146,42 +160,51 @@ __global__ __launch_bounds__(kThreads) void wkv7_fwd_kernel(FwdParams<Tin> p) {
     }
   };
 
+  // Tile pipeline. While tile ti is computed, the raw operands of tile ti+1
+  // stream into LDS. At the tile end one wait + barrier makes them visible;
+  // the outputs of tile ti are flushed and tile ti+1 is converted to fp32, a
+  // barrier, and the loads for tile ti+2 are issued.
   const int ntiles = (T + kTile - 1) / kTile;
+  auto tile_n = [&](int ti) { return min(kTile, T - ti * kTile); };
   if (ntiles > 0) {
-    gload(0);
-    lstore(0, 0);
+    issue(0, tile_n(0));
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    convert(tile_n(0));
+    __syncthreads();
+    if (ntiles > 1) issue(kTile, tile_n(1));
   }
-  __syncthreads();
 
   for (int ti = 0; ti < ntiles; ++ti) {
-    const int buf = ti & 1;
-    const int t0 = ti * kTile;
-    const int nst = min(kTile, T - t0);
-    if (ti + 1 < ntiles) gload(t0 + kTile);
+    const int t0 = ti * kTile, nst = tile_n(ti);
 
     // Two operand sets alternate so that the reads for step s+1 are in flight
     // while step s computes, without register copies between iterations.
-    StepOps A = lread(buf, 0);
+    StepOps A = lread(0);
     int s = 0;
     for (; s + 1 < nst; s += 2) {
-      const StepOps Bo = lread(buf, s + 1);
-      step(A, buf, s);
-      A = lread(buf, min(s + 2, nst - 1));
-      step(Bo, buf, s + 1);
+      const StepOps Bo = lread(s + 1);
+      step(A, s);
+      A = lread(min(s + 2, nst - 1));
+      step(Bo, s + 1);
     }
-    if (s < nst) step(A, buf, s);
+    if (s < nst) step(A, s);
 
-    if (ti + 1 < ntiles) lstore(buf ^ 1, t0 + kTile);
     if (ck_pending) {
       ck_store(chunk++, Ck0, Ck1);
       ck_pending = false;
     }
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (tid < 256 && sl < nst) {
+    if (sl < nst) {   // cg 0 writes y, cg 1 writes sa
       const int64_t off = tok0 + (int64_t)(t0 + sl) * tstride + 4 * pp;
-      io::store(p.y + off, reinterpret_cast<const float4*>(ost[buf][0][sl])[pp]);
-      *reinterpret_cast<float4*>(p.sa + off) = reinterpret_cast<const float4*>(ost[buf][1][sl])[pp];
+      const float4 x = reinterpret_cast<const float4*>(ost[cg][sl])[pp];
+      if (cg == 0) io::store(p.y + off, x);
+      else *reinterpret_cast<float4*>(p.sa + off) = x;
     }
+    if (ti + 1 < ntiles) convert(tile_n(ti + 1));
+    __syncthreads();
+    if (ti + 2 < ntiles) issue((ti + 2) * kTile, tile_n(ti + 2));
   }
 
   if (p.sT) {
@@ -194,12 +217,12 @@ __global__ __launch_bounds__(kThreads) void wkv7_fwd_kernel(FwdParams<Tin> p) {
 template <typename Tin>
 hipError_t launch_fwd_t(const ForwardDesc& d, hipStream_t stream) {
   FwdParams<Tin> p;
-  p.w = static_cast<const Tin*>(d.w);
-  p.r = static_cast<const Tin*>(d.r);
-  p.k = static_cast<const Tin*>(d.k);
-  p.v = static_cast<const Tin*>(d.v);
-  p.a = static_cast<const Tin*>(d.a);
-  p.b = static_cast<const Tin*>(d.b);
+  p.in[V_W] = static_cast<const Tin*>(d.w);
+  p.in[V_R] = static_cast<const Tin*>(d.r);
+  p.in[V_K] = static_cast<const Tin*>(d.k);
+  p.in[V_V] = static_cast<const Tin*>(d.v);
+  p.in[V_A] = static_cast<const Tin*>(d.a);
+  p.in[V_B] = static_cast<const Tin*>(d.b);
   p.s0 = d.s0;
   p.ckpt = d.ckpt;
   p.sa = d.sa;
@@ -208,7 +231,12 @@ hipError_t launch_fwd_t(const ForwardDesc& d, hipStream_t stream) {
   p.T = d.T;
   p.H = d.H;
   p.C = d.C;
-  hipLaunchKernelGGL(wkv7_fwd_kernel<Tin>, dim3(d.H, d.B, 1), dim3(kThreads, 1, 1), 0, stream, p);
+  if (d.C >= kTile)
+    hipLaunchKernelGGL((wkv7_fwd_kernel<Tin, true>), dim3(d.H, d.B, 1), dim3(kThreads, 1, 1), 0,
+                       stream, p);
+  else
+    hipLaunchKernelGGL((wkv7_fwd_kernel<Tin, false>), dim3(d.H, d.B, 1), dim3(kThreads, 1, 1), 0,
+                       stream, p);
   return hipGetLastError();
 }
 
