@@ -35,6 +35,10 @@ FLOP_FWD = 9 * N_HEAD * N_HEAD      # per head-step: sa 2N^2, update 5N^2, y 2N^
 FLOP_BWD = 24 * N_HEAD * N_HEAD     # per head-step, non-redundant backward
 PEAK_FP32 = 157.3e12                # MI355X FP32 vector peak (packed issue)
 PEAK_HBM = 8.0e12                   # MI355X HBM3E
+COPY_PROBE_BYTES = 512 << 20        # fp32 stream (read once, write once) of --copy-probe
+# HBM traffic of the dominant kernel per launch, from rocprofv3 FETCH_SIZE /
+# WRITE_SIZE passes scaled by the copy probe; written by --pmc-summary
+TRAFFIC_FILE = os.path.join(HERE, "profiles", "wkv7_bwd_cfg1_traffic.md")
 METRIC = "WKV7 fwd+bwd Mtokens/s (B=8,T=4096,C=2048) + % FP32-VALU / HBM roofline"
 
 CONFIGS = {
@@ -90,7 +94,78 @@ def cpu_baseline(cfg, seconds_target=12.0):
                       f"{dt:.1f} s on {cores} threads (oracle/wkv7_oracle.c, reference order)"}
 
 
-def bench_train(cfg, steps, warmup, with_cpu):
+def recorded_traffic(kernel: str):
+    """Bytes per launch of `kernel` recorded in TRAFFIC_FILE ("traffic_bytes
+    <kernel>: <int>" lines), or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith(f"traffic_bytes {kernel}:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
+def copy_probe():
+    """One streaming kernel over COPY_PROBE_BYTES (each byte read once and
+    written once; an elementwise absolute value, since a same-dtype copy_ may
+    become a DMA transfer instead of a kernel, and nothing else here launches
+    that kernel): the scale for rocprofv3's FETCH_SIZE and WRITE_SIZE
+    counters."""
+    import torch
+    n = COPY_PROBE_BYTES // 4
+    src = torch.ones(n, device="cuda:0")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    torch.abs(src, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
+
+
+def pmc_summary(dirs):
+    """Mean counter value per dispatch for each WKV7 kernel and the copy probe
+    in rocprofv3 --pmc CSV output, and the traffic scaled by the probe."""
+    import csv
+    import glob
+    from collections import defaultdict
+    keys = ("wkv7_fwd_kernel", "wkv7_bwd_kernel", "wkv7_infer_kernel", "abs_kernel")
+    per = defaultdict(lambda: defaultdict(lambda: defaultdict(float)))
+    for d in dirs:
+        for path in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            with open(path) as f:
+                for row in csv.DictReader(f):
+                    name = row["Kernel_Name"]
+                    key = next((k for k in keys if k in name), None)
+                    if key is None:
+                        continue
+                    # rows of one dispatch (one per XCD / shader engine) add up
+                    per[key][row["Counter_Name"]][row["Dispatch_Id"]] += float(row["Counter_Value"])
+    # the probe is the last dispatch of its kernel
+    for c, v in per.get("abs_kernel", {}).items():
+        last = max(v, key=int)
+        per["abs_kernel"][c] = {last: v[last]}
+    mean = {k: {c: sum(v.values()) / len(v) for c, v in cs.items()} for k, cs in per.items()}
+    probe_kib = COPY_PROBE_BYTES / 1024
+    scale = {c: probe_kib / mean["abs_kernel"][c] for c in ("FETCH_SIZE", "WRITE_SIZE")
+             if "abs_kernel" in mean and c in mean["abs_kernel"]}
+    print("| kernel | counter | KiB per dispatch | scale | bytes per dispatch |")
+    print("|---|---|---|---|---|")
+    totals = {}
+    for k in keys:
+        for c, v in sorted(mean.get(k, {}).items()):
+            sc = scale.get(c)
+            b = v * 1024 * sc if sc else None
+            if b is not None and k != "abs_kernel":
+                totals[k] = totals.get(k, 0) + b
+            print(f"| {k} | {c} | {v:.0f} | {sc if sc else '-'} | "
+                  f"{'-' if b is None else f'{b:.0f}'} |")
+    print()
+    for k, b in totals.items():
+        print(f"traffic_bytes {k}: {int(round(b))}")
+
+
+def bench_train(cfg, steps, warmup, with_cpu, probe=False):
     import torch
     pkg = importlib.import_module("rwkv-rs_amd")
     native = importlib.import_module("rwkv-rs_amd._native")
@@ -130,6 +205,8 @@ def bench_train(cfg, steps, warmup, with_cpu):
         fwd()
         bwd()
     torch.cuda.synchronize()
+    if probe:
+        copy_probe()
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
            torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     torch.cuda.synchronize()
@@ -174,7 +251,8 @@ def bench_train(cfg, steps, warmup, with_cpu):
                    "state_dtype": "f32", "initial_state_std": cfg["s0_std"]},
         "roofline": {"bound": "valu", "kernel": "wkv7_bwd_kernel", "achieved": achieved / 1e12,
                      "peak": PEAK_FP32 / 1e12, "unit": "TFLOP/s", "frac": achieved / PEAK_FP32,
-                     "traffic": None, "algorithmic_bytes": bwd_bytes,
+                     "traffic": recorded_traffic("wkv7_bwd_kernel"),
+                     "algorithmic_bytes": bwd_bytes,
                      "flop_per_launch": bwd_flops, "launch_ms": bwd_ms},
         "fwd_ms": fwd_ms,
         "bwd_ms": bwd_ms,
@@ -245,7 +323,14 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="cfg1", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also launch one plain copy of known size (counter calibration)")
+    ap.add_argument("--pmc-summary", nargs="+", metavar="DIR",
+                    help="summarise rocprofv3 --pmc CSV output directories and exit")
     args = ap.parse_args()
+    if args.pmc_summary:
+        pmc_summary(args.pmc_summary)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the WKV7 operator needs no collective and "
               "this build runs on single-GPU boxes (see DESIGN.md for how it shards)",
@@ -256,7 +341,8 @@ def main():
         out = bench_decode(cfg, args.steps, args.warmup)
     else:
         out = bench_train(cfg, args.steps, args.warmup,
-                          with_cpu=(not args.no_cpu and args.config == "cfg1"))
+                          with_cpu=(not args.no_cpu and args.config == "cfg1"),
+                          probe=args.copy_probe)
     print(json.dumps(out), flush=True)
 
 

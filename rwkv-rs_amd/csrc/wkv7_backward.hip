@@ -15,22 +15,25 @@
 //   ds0    = dS after t = 0                                         (:299-307)
 //
 // Design. One 512-thread workgroup per (b, h). Thread tid = 16*q + L plays two
-// roles on two transposed 2x4 blocks (layout in wkv7_device.hpp):
-//   row role:    dSr[d][c] = dS[2q+d][4L+c]   -> row sums dv, dsa of rows 2q, 2q+1
-//   column role: Sc[c][d]  = S[4L+c][2q+d],
-//                dSc[c][d] = dS[4L+c][2q+d]   -> column sums dr, dw~, dk, db, da
-//                                                of columns 2q, 2q+1
+// roles on two transposed 2x4 blocks (layout and lane-relative order in
+// wkv7_device.hpp; d = 0 is the thread's own row/column 2q + up, d = 1 the
+// other one):
+//   row role:    dSo/dSt[c] = dS[own/other row][4L+c] -> row sums dv, dsa
+//   column role: Sc[c][d]  = S[4L+c][column d],
+//                dSc[c][d] = dS[4L+c][column d]      -> column sums dr, dw~,
+//                                                       dk, db, da
 // The sixteen lanes of a DPP row (same q) span all 64 columns in the row role
 // and all 64 rows in the column role, so every sum is in-lane products plus a
-// DPP reduction over the row; sums that are only written out use a
-// reduce-scatter (one lane per value) instead of a full reduction. Keeping dS
-// twice costs 3 instructions per element per step; reducing the five column
-// sums across waves instead would cost more. Every operand arrives as one
-// ds_read_b128 of an LDS vector (the thread's four columns for the row role,
-// its four rows for the column role) or of a packed per-column-pair record,
-// consumed by plain full-rate FMAs. The only data exchanged between waves is
-// dsa (64 floats, needed by the column role): one LDS vector and one barrier
-// per step, with the column-role work scheduled between write and barrier.
+// DPP reduction over the row. Keeping dS twice costs 3 instructions per
+// element per step; reducing the five column sums across waves instead would
+// cost more. Every operand arrives as one ds_read_b128 of an LDS vector (the
+// thread's four columns for the row role, its four rows for the column role)
+// or of a packed per-column-pair record, consumed by plain full-rate FMAs.
+// The only data exchanged between waves is dsa (64 floats, needed by the
+// column role): one LDS vector and one barrier per step. dsa is the only sum
+// on the step-to-step dependency chain; the twelve per-step partial sums of
+// the six gradients stay in registers for the 8 steps of a tile and are
+// reduced in one batch at the tile end.
 #include "wkv7_device.hpp"
 #include "wkv7_launch.hpp"
 
@@ -39,16 +42,19 @@ namespace {
 
 constexpr int kTile = 8;   // timesteps per LDS tile
 
-// LDS vectors per timestep (fp32, 64 entries)
+// fp32 LDS vectors per timestep (64 entries)
 enum {
   V_R = 0, V_K, V_B, V_W, V_A,   // key-indexed: row role
-  V_DY, V_V, V_SA,               // value-indexed: column role (dy also row role)
+  V_DY, V_V, V_SA,               // value-indexed: column role
+  V_DYS,                         // dy with each row pair swapped (row role, upper half)
   V_DWF,                         // W_SCALE * w~ * sig * (1 - sig)
   V_COUNT
 };
-// per-column-pair records for the column role, float4 {x[2p], x[2p+1], y[2p], y[2p+1]}
+// per-column-pair records for the column role, float4 {x[2p], x[2p+1],
+// y[2p], y[2p+1]}; a second copy with each pair swapped serves the upper
+// half-rows
 enum { P_RK = 0, P_BA, P_WI, P_COUNT };   // {r, k}, {b, a}, {w~, 1/w~}
-// staged outputs per timestep, in the order the reduce-scatters deliver them
+// gradient outputs, in the order of the per-step partials
 enum { O_DV = 0, O_DR, O_DW, O_DK, O_DB, O_DA, O_COUNT };
 // raw (input dtype) operand rows as loaded from global memory
 enum { R_W = 0, R_R, R_K, R_V, R_A, R_B, R_DY, R_COUNT };
@@ -68,25 +74,30 @@ struct BwdParams {
   int T, H, C;
 };
 
-// kCkTiled: C is a multiple of the tile length, so every checkpoint reload
-// happens at the last step of a tile and the checkpoint travels with that
-// tile (loaded into LDS one tile ahead). Otherwise reloads read global memory
-// directly. The two are separate instantiations so that the compiler never
-// merges the LDS and global reads into one generic (flat) access.
+// kCkTiled: C is a multiple of the tile length, so every tile is full (T is a
+// multiple of C), every checkpoint reload happens at the first step processed
+// in a tile, and the checkpoint travels with that tile (loaded into LDS one
+// tile ahead); the steps of a tile then form one branch-free block.
+// Otherwise the last tile may be partial and reloads read global memory at
+// any step.
 template <typename Tin, bool kCkTiled>
 __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
   constexpr int kRow = kHead * sizeof(Tin);                // bytes of one raw row
   constexpr int kRawBytes = R_COUNT * kTile * kRow + kTile * kHead * 4;
-  __shared__ float4 tile[V_COUNT][kTile][16];              // 18 KiB
-  __shared__ float4 pairs[P_COUNT][kTile][32];             // 12 KiB
+  constexpr int kParts = 2 * O_COUNT * kTile;              // partial sums per tile
+  __shared__ float4 tile[V_COUNT][kTile][16];              // 20 KiB
+  __shared__ float4 pairs[2][P_COUNT][kTile][32];          // 24 KiB: plain, swapped
   __shared__ float ost[O_COUNT][kTile][kHead];             // 12 KiB
   __shared__ float4 ckbuf[2][kHead * kHead / 4];           // 32 KiB, by tile parity
   __shared__ float4 raw[kRawBytes / 16];                   // 9 or 16 KiB
-  __shared__ float4 dsab[2][16];                           // dsa of the step, by parity
+  __shared__ float dsab[2][kHead];                         // dsa of the step, by parity
+  __shared__ float dump[kThreads];                         // sink of unselected lanes
 
   const int h = blockIdx.x, bi = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63;
   const int L = tid & 15, q = tid >> 4;
+  const int up = (L >> 3) & 1;
+  const int ro = 2 * q + up, rt = 2 * q + 1 - up;   // own and other row / column
   // conversion: group sg = tid / 128 (0: w; 1: r, k; 2: b, a; 3: dy, v, sa),
   // timestep sl, elements 4pp .. 4pp+3
   const int sg = tid >> 7, sl = (tid >> 4) & 7, pp = tid & 15;
@@ -128,13 +139,19 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
       load_lds16(src + kThreads + tid, &ckbuf[par][kThreads + tid - lane]);
     }
   };
-  // raw tile -> fp32 operand vectors and column-pair records
+  // raw tile -> fp32 operand vectors and column-pair records (plain, swapped)
   auto convert = [&](int nst) {
     if (sl >= nst) return;
     const char* rb = reinterpret_cast<const char*>(raw);
     auto rawv = [&](int vec) {
       return Io<Tin>::widen(*reinterpret_cast<const typename Io<Tin>::raw*>(
           rb + (vec * kTile + sl) * kRow + 4 * pp * sizeof(Tin)));
+    };
+    auto put_pairs = [&](int rec, float4 x, float4 y) {
+      pairs[0][rec][sl][2 * pp] = make_float4(x.x, x.y, y.x, y.y);
+      pairs[0][rec][sl][2 * pp + 1] = make_float4(x.z, x.w, y.z, y.w);
+      pairs[1][rec][sl][2 * pp] = make_float4(x.y, x.x, y.y, y.x);
+      pairs[1][rec][sl][2 * pp + 1] = make_float4(x.w, x.z, y.w, y.z);
     };
     if (sg == 0) {
       const float4 x = rawv(R_W);
@@ -147,108 +164,93 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
         iws[c] = 1.0f / ws[c];
         dws[c] = kWScale * ws[c] * sig * (1.0f - sig);
       }
-      tile[V_W][sl][pp] = make_float4(ws[0], ws[1], ws[2], ws[3]);
+      const float4 w4 = make_float4(ws[0], ws[1], ws[2], ws[3]);
+      tile[V_W][sl][pp] = w4;
       tile[V_DWF][sl][pp] = make_float4(dws[0], dws[1], dws[2], dws[3]);
-      pairs[P_WI][sl][2 * pp] = make_float4(ws[0], ws[1], iws[0], iws[1]);
-      pairs[P_WI][sl][2 * pp + 1] = make_float4(ws[2], ws[3], iws[2], iws[3]);
+      put_pairs(P_WI, w4, make_float4(iws[0], iws[1], iws[2], iws[3]));
     } else if (sg == 1) {
       const float4 r = rawv(R_R), k = rawv(R_K);
       tile[V_R][sl][pp] = r;
       tile[V_K][sl][pp] = k;
-      pairs[P_RK][sl][2 * pp] = make_float4(r.x, r.y, k.x, k.y);
-      pairs[P_RK][sl][2 * pp + 1] = make_float4(r.z, r.w, k.z, k.w);
+      put_pairs(P_RK, r, k);
     } else if (sg == 2) {
       const float4 b = rawv(R_B), a = rawv(R_A);
       tile[V_B][sl][pp] = b;
       tile[V_A][sl][pp] = a;
-      pairs[P_BA][sl][2 * pp] = make_float4(b.x, b.y, a.x, a.y);
-      pairs[P_BA][sl][2 * pp + 1] = make_float4(b.z, b.w, a.z, a.w);
+      put_pairs(P_BA, b, a);
     } else {
-      tile[V_DY][sl][pp] = rawv(R_DY);
+      const float4 dy = rawv(R_DY);
+      tile[V_DY][sl][pp] = dy;
+      tile[V_DYS][sl][pp] = make_float4(dy.y, dy.x, dy.w, dy.z);
       tile[V_V][sl][pp] = rawv(R_V);
       tile[V_SA][sl][pp] = *reinterpret_cast<const float4*>(
           rb + R_COUNT * kTile * kRow + (sl * kHead + 4 * pp) * 4);
     }
   };
+  // (own, other) rows of dy for the row role: 32 float2 per step row
+  const float2* dyrow = reinterpret_cast<const float2*>(&tile[up ? V_DYS : V_DY][0][0]) + q;
+  const float4(*prec)[kTile][32] = pairs[up];   // this half-row's pair records
 
-  float dSr[2][4], Sc[4][2], dSc[4][2];
+  float dSo[4], dSt[4], Sc[4][2], dSc[4][2];
 #pragma unroll
   for (int c = 0; c < 4; ++c) { Sc[c][0] = 0.0f; Sc[c][1] = 0.0f; }
   if (p.dsT) {
     const float* g0 = p.dsT + bh * (kHead * kHead);
-    unpack4(dSr[0], *reinterpret_cast<const float4*>(g0 + (2 * q) * kHead + 4 * L));
-    unpack4(dSr[1], *reinterpret_cast<const float4*>(g0 + (2 * q + 1) * kHead + 4 * L));
+    unpack4(dSo, *reinterpret_cast<const float4*>(g0 + ro * kHead + 4 * L));
+    unpack4(dSt, *reinterpret_cast<const float4*>(g0 + rt * kHead + 4 * L));
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const float2 x = *reinterpret_cast<const float2*>(g0 + (4 * L + c) * kHead + 2 * q);
-      dSc[c][0] = x.x;
-      dSc[c][1] = x.y;
+      dSc[c][0] = g0[(4 * L + c) * kHead + ro];
+      dSc[c][1] = g0[(4 * L + c) * kHead + rt];
     }
   } else {
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      dSr[0][c] = 0.0f; dSr[1][c] = 0.0f; dSc[c][0] = 0.0f; dSc[c][1] = 0.0f;
+      dSo[c] = 0.0f; dSt[c] = 0.0f; dSc[c][0] = 0.0f; dSc[c][1] = 0.0f;
     }
   }
 
-  int until_reload = 0;   // steps until the next checkpoint reload
+  // checkpoint key-rows own/other, entries 4L .. 4L+3, are Sc[0..3][0/1]
+  auto reload = [&](float4 x0, float4 x1) {   // kernel.rs:210-228
+    Sc[0][0] = x0.x; Sc[1][0] = x0.y; Sc[2][0] = x0.z; Sc[3][0] = x0.w;
+    Sc[0][1] = x1.x; Sc[1][1] = x1.y; Sc[2][1] = x1.z; Sc[3][1] = x1.w;
+  };
+  int until_reload = 0;   // steps until the next checkpoint reload (unaligned C)
   int64_t reload_chunk = nchunks - 1;
-  int parity = 0;
 
-  // One timestep (kernel.rs:177-297); `par` selects this tile's checkpoint.
-  auto step = [&](int s, int par) {
-    if (until_reload == 0) {   // (t + 1) % C == 0, kernel.rs:210-228
-      until_reload = C;
-      // checkpoint row 2q+d, entries 4L .. 4L+3, is Sc[0..3][d]
-      float4 x0, x1;
-      if constexpr (kCkTiled) {
-        x0 = ckbuf[par][((2 * q) * kHead + 4 * L) / 4];
-        x1 = ckbuf[par][((2 * q + 1) * kHead + 4 * L) / 4];
-      } else {
-        const float* src = ckpt_bh + reload_chunk * (kHead * kHead) + (2 * q) * kHead + 4 * L;
-        x0 = *reinterpret_cast<const float4*>(src);
-        x1 = *reinterpret_cast<const float4*>(src + kHead);
-      }
-      Sc[0][0] = x0.x; Sc[1][0] = x0.y; Sc[2][0] = x0.z; Sc[3][0] = x0.w;
-      Sc[0][1] = x1.x; Sc[1][1] = x1.y; Sc[2][1] = x1.z; Sc[3][1] = x1.w;
-      --reload_chunk;
-    }
-    --until_reload;
-
-    // row role operands: columns 4L..4L+3, rows 2q, 2q+1
+  // One timestep (kernel.rs:177-297) of tile row s; its twelve partial sums
+  // go to part[] as [own block | other block], six per step each.
+  auto step = [&](int s, int par, float* part) {
+    // row role: dS row += dy r^T (kernel.rs:248); dv, dsa (kernel.rs:261-262)
     float rr[4], kk[4], bb[4];
     unpack4(rr, tile[V_R][s][L]);
     unpack4(kk, tile[V_K][s][L]);
     unpack4(bb, tile[V_B][s][L]);
-    const float2 dyr = reinterpret_cast<const float2*>(tile[V_DY][s])[q];
-    // column role operands: rows 4L..4L+3, columns 2q, 2q+1
+    const float2 dyr = dyrow[s * 32];
+    float dvo = 0.0f, dvt = 0.0f, dsa_o = 0.0f, dsa_t = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      dSo[c] = __builtin_fmaf(dyr.x, rr[c], dSo[c]);
+      dSt[c] = __builtin_fmaf(dyr.y, rr[c], dSt[c]);
+      dvo = __builtin_fmaf(dSo[c], kk[c], dvo);
+      dvt = __builtin_fmaf(dSt[c], kk[c], dvt);
+      dsa_o = __builtin_fmaf(dSo[c], bb[c], dsa_o);
+      dsa_t = __builtin_fmaf(dSt[c], bb[c], dsa_t);
+    }
+    row_pair_sum(dsa_o, dsa_t);
+    // one lane per half-row publishes dsa of its own row; the others write a
+    // private sink, which keeps the step free of branches
+    *((L & 7) == 0 ? &dsab[par][ro] : &dump[tid]) = dsa_o;
+
+    // column role: dr from S_t; rebuild S_{t-1}; dS col += dy r; dw~, dk, db
     float dy[4], v[4], sa[4];
     unpack4(dy, tile[V_DY][s][L]);
     unpack4(v, tile[V_V][s][L]);
     unpack4(sa, tile[V_SA][s][L]);
-    const float4 prk = pairs[P_RK][s][q], pba = pairs[P_BA][s][q];
-    const float4 pwi = pairs[P_WI][s][q];
+    const float4 prk = prec[P_RK][s][q], pba = prec[P_BA][s][q], pwi = prec[P_WI][s][q];
     const float rc[2] = {prk.x, prk.y}, kc[2] = {prk.z, prk.w};
     const float bc[2] = {pba.x, pba.y}, ac[2] = {pba.z, pba.w};
     const float wc[2] = {pwi.x, pwi.y}, iwc[2] = {pwi.z, pwi.w};
-
-    // row role: dS row += dy r^T (kernel.rs:248); dv, dsa (kernel.rs:261-262)
-    const float dyd[2] = {dyr.x, dyr.y};
-    float dvp[2] = {0.0f, 0.0f};
-    float dsa0 = 0.0f, dsa1 = 0.0f;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      dSr[0][c] = __builtin_fmaf(dyd[0], rr[c], dSr[0][c]);
-      dSr[1][c] = __builtin_fmaf(dyd[1], rr[c], dSr[1][c]);
-      dvp[0] = __builtin_fmaf(dSr[0][c], kk[c], dvp[0]);
-      dvp[1] = __builtin_fmaf(dSr[1][c], kk[c], dvp[1]);
-      dsa0 = __builtin_fmaf(dSr[0][c], bb[c], dsa0);
-      dsa1 = __builtin_fmaf(dSr[1][c], bb[c], dsa1);
-    }
-    row16_sum2(dsa0, dsa1, L);
-    if (L == 0) reinterpret_cast<float2*>(dsab[parity])[q] = make_float2(dsa0, dsa1);
-
-    // column role: dr from S_t; rebuild S_{t-1}; dS col += dy r; dw~, dk, db
     float drp[2] = {0.0f, 0.0f}, dwp[2] = {0.0f, 0.0f}, dkp[2] = {0.0f, 0.0f};
     float dbp[2] = {0.0f, 0.0f};
 #pragma unroll
@@ -263,21 +265,10 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
         dkp[d] = __builtin_fmaf(dSc[c][d], v[c], dkp[d]);
         dbp[d] = __builtin_fmaf(dSc[c][d], sa[c], dbp[d]);
       }
-    // dv (rows 2q, 2q+1) and dr, dw~, dk (columns 2q, 2q+1): one lane pair each
-    float early[8] = {dvp[0], dvp[1], drp[0], drp[1], dwp[0], dwp[1], dkp[0], dkp[1]};
-    row16_scatter<8>(early, L);
-    if ((L & 1) == 0) {
-      const int o = O_DV + (L >> 2), idx = 2 * q + ((L >> 1) & 1);
-      float val = early[0];
-      // dw = W_SCALE * dw~ * w~ * sig * (1 - sig), kernel.rs:267-271
-      if (o == O_DW) val *= reinterpret_cast<const float*>(tile[V_DWF][s])[idx];
-      ost[o][s][idx] = val;
-    }
 
     lds_barrier();   // dsa of every row visible
     float ds[4];
-    unpack4(ds, dsab[parity][L]);
-    parity ^= 1;
+    unpack4(ds, reinterpret_cast<const float4*>(dsab[par])[L]);
 
     // row role: dS row = dS row * w~ + dsa a^T (kernel.rs:290-291)
     float ww[4], aa[4];
@@ -285,8 +276,8 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
     unpack4(aa, tile[V_A][s][L]);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      dSr[0][c] = __builtin_fmaf(dsa0, aa[c], dSr[0][c] * ww[c]);
-      dSr[1][c] = __builtin_fmaf(dsa1, aa[c], dSr[1][c] * ww[c]);
+      dSo[c] = __builtin_fmaf(dsa_o, aa[c], dSo[c] * ww[c]);
+      dSt[c] = __builtin_fmaf(dsa_t, aa[c], dSt[c] * ww[c]);
     }
     // column role: da = S_{t-1}^T dsa (kernel.rs:280-287); dS col = dS col * w~ + a dsa
     float dap[2] = {0.0f, 0.0f};
@@ -297,26 +288,31 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
         dap[d] = __builtin_fmaf(Sc[c][d], ds[c], dap[d]);
         dSc[c][d] = __builtin_fmaf(ac[d], ds[c], dSc[c][d] * wc[d]);   // kernel.rs:293-294
       }
-    // db, da (columns 2q, 2q+1): four lanes each
-    float late[4] = {dbp[0], dbp[1], dap[0], dap[1]};
-    row16_scatter<4>(late, L);
-    if ((L & 3) == 0) ost[O_DB + (L >> 3)][s][2 * q + ((L >> 2) & 1)] = late[0];
+    float* po = part + O_COUNT * s;
+    float* pt = part + O_COUNT * (kTile + s);
+    po[O_DV] = dvo;     pt[O_DV] = dvt;
+    po[O_DR] = drp[0];  pt[O_DR] = drp[1];
+    po[O_DW] = dwp[0];  pt[O_DW] = dwp[1];
+    po[O_DK] = dkp[0];  pt[O_DK] = dkp[1];
+    po[O_DB] = dbp[0];  pt[O_DB] = dbp[1];
+    po[O_DA] = dap[0];  pt[O_DA] = dap[1];
   };
 
   // Tile pipeline (tiles run backwards in time). While tile ti is computed,
-  // the raw operands of tile ti-1 stream into LDS. At the tile end one wait +
-  // barrier makes them visible; the outputs of tile ti are flushed and tile
-  // ti-1 is converted to fp32 (a different LDS region), a barrier, and the
-  // loads for tile ti-2 are issued.
+  // the raw operands of tile ti-1 stream into LDS. At the tile end the
+  // gradient partials are reduced and staged, one wait + barrier makes the
+  // loads visible; the outputs of tile ti are flushed and tile ti-1 is
+  // converted to fp32 (a different LDS region), a barrier, and the loads for
+  // tile ti-2 are issued.
   const int ntiles = (T + kTile - 1) / kTile;
   auto tile_t0 = [&](int ti) { return ti * kTile; };
   auto tile_n = [&](int ti) { return min(kTile, T - ti * kTile); };
   if (ntiles > 0) {
     issue(tile_t0(ntiles - 1), tile_n(ntiles - 1), (ntiles - 1) & 1);
     __builtin_amdgcn_s_waitcnt(0);   // vmcnt/lgkmcnt 0
-    __syncthreads();
+    lds_barrier();
     convert(tile_n(ntiles - 1));
-    __syncthreads();
+    lds_barrier();
     if (ntiles > 1) issue(tile_t0(ntiles - 2), tile_n(ntiles - 2), (ntiles - 2) & 1);
   }
 
@@ -325,9 +321,46 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
   typedef Io<Tin> io;
   for (int ti = ntiles - 1; ti >= 0; --ti) {
     const int t0 = tile_t0(ti), nst = tile_n(ti);
-    for (int s = nst - 1; s >= 0; --s) step(s, ti & 1);
+    if constexpr (kCkTiled) {
+      if (ck_needed(t0, nst)) {   // the reload of step t0 + kTile - 1
+        const float4* ck = ckbuf[ti & 1];
+        reload(ck[(ro * kHead + 4 * L) / 4], ck[(rt * kHead + 4 * L) / 4]);
+      }
+    }
+    float part[kParts];
+#pragma unroll
+    for (int s = kTile - 1; s >= 0; --s) {
+      if constexpr (!kCkTiled) {
+        if (s >= nst) {   // uniform: the first tile processed may be partial
+#pragma unroll
+          for (int m = 0; m < O_COUNT; ++m) part[O_COUNT * s + m] = part[O_COUNT * (kTile + s) + m] = 0.0f;
+          continue;
+        }
+        if (until_reload == 0) {   // (t + 1) % C == 0, kernel.rs:210-228
+          until_reload = C;
+          const float* src = ckpt_bh + reload_chunk * (kHead * kHead) + 4 * L;
+          reload(*reinterpret_cast<const float4*>(src + ro * kHead),
+                 *reinterpret_cast<const float4*>(src + rt * kHead));
+          --reload_chunk;
+        }
+        --until_reload;
+      }
+      step(s, (kTile - 1 - s) & 1, part);
+    }
+    // the six gradients of own row/column 2q+up at step L&7 of the tile
+    row16_reduce_scatter<kParts>(part, L);
+    const int so = L & 7;
+    // dw = W_SCALE * dw~ * w~ * sig * (1 - sig), kernel.rs:267-271
+    part[O_DW] *= reinterpret_cast<const float*>(tile[V_DWF][so])[ro];
+#pragma unroll
+    for (int m = 0; m < O_COUNT; ++m) ost[m][so][ro] = part[m];
+
+    // The loads of tile ti-1 have landed once vmcnt reaches 0 (they and the
+    // stores of the previous tile end were issued a whole tile ago). Only LDS
+    // is fenced by the barriers, so the stores below are not waited for until
+    // the next tile end.
     __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    lds_barrier();
     if (fg < 3 && sl < nst) {
       const int64_t off = tok0 + (int64_t)(t0 + sl) * tstride + 4 * pp;
       const float4 x0 = reinterpret_cast<const float4*>(ost[2 * fg][sl])[pp];
@@ -338,15 +371,14 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
       io::store(d1 + off, x1);
     }
     if (ti > 0) convert(tile_n(ti - 1));
-    __syncthreads();
+    lds_barrier();   // converted tile visible; `raw` free for the next loads
     if (ti > 1) issue(tile_t0(ti - 2), tile_n(ti - 2), (ti - 2) & 1);
   }
 
   if (p.ds0) {   // kernel.rs:299-307
-    float* base = p.ds0 + (bh * kHead + 2 * q) * kHead + 4 * L;
-    *reinterpret_cast<float4*>(base) = make_float4(dSr[0][0], dSr[0][1], dSr[0][2], dSr[0][3]);
-    *reinterpret_cast<float4*>(base + kHead) =
-        make_float4(dSr[1][0], dSr[1][1], dSr[1][2], dSr[1][3]);
+    float* base = p.ds0 + bh * (kHead * kHead) + 4 * L;
+    *reinterpret_cast<float4*>(base + ro * kHead) = make_float4(dSo[0], dSo[1], dSo[2], dSo[3]);
+    *reinterpret_cast<float4*>(base + rt * kHead) = make_float4(dSt[0], dSt[1], dSt[2], dSt[3]);
   }
 }
 
@@ -373,12 +405,11 @@ hipError_t launch_bwd_t(const BackwardDesc& d, hipStream_t stream) {
   p.T = d.T;
   p.H = d.H;
   p.C = d.C;
+  const dim3 grid(d.H, d.B, 1), block(kThreads, 1, 1);
   if (d.C % kTile == 0)
-    hipLaunchKernelGGL((wkv7_bwd_kernel<Tin, true>), dim3(d.H, d.B, 1), dim3(kThreads, 1, 1), 0,
-                       stream, p);
+    hipLaunchKernelGGL((wkv7_bwd_kernel<Tin, true>), grid, block, 0, stream, p);
   else
-    hipLaunchKernelGGL((wkv7_bwd_kernel<Tin, false>), dim3(d.H, d.B, 1), dim3(kThreads, 1, 1), 0,
-                       stream, p);
+    hipLaunchKernelGGL((wkv7_bwd_kernel<Tin, false>), grid, block, 0, stream, p);
   return hipGetLastError();
 }
 

@@ -17,6 +17,21 @@
 // LDS vector (entries 4L .. 4L+3), consumed by plain full-rate FMAs.
 // LDS bandwidth (~250 B/clk/CU on gfx950, broadcast or not) is the other
 // limit, which is why the block is 2x4 rather than 1x8.
+//
+// Lane-relative row order. Lanes 8-15 of each DPP row (up = 1) keep their row
+// pair swapped: a thread's "own" row is 2q + up, its "other" row 2q + 1 - up,
+// and every per-row quantity it holds (state rows, row operands, partial
+// sums) is ordered (own, other). The first level of a sum over the DPP row
+// pairs lane L with L ^ 8, whose own row is this lane's other row, so it adds
+// the partner's "other" value to the own value with no select; the remaining
+// levels run inside an 8-lane half, where every lane has the same own row.
+// With the plain order, every reduce-scatter level needs two v_cndmask per
+// value pair to choose what to keep and what to send.
+//
+// Sums that are outputs only (y in the forward, the six gradients in the
+// backward) are not on the recurrence's dependency chain: their partials stay
+// in registers for a whole LDS tile of timesteps and are reduced in one batch
+// at the tile end, where the independent DPP chains overlap each other.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -85,21 +100,17 @@ __device__ __forceinline__ float dpp_mov(float x) {
       0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
 }
 
-// Sum within each 8-lane half of a DPP row (pairs L/7-L, then L/L^2, then
-// L/L^1). All eight lanes get the same bits: every step adds two partial sums
-// that the lanes of the orbit form from the same operands, and IEEE addition
-// is commutative.
-__device__ __forceinline__ float half8_sum(float x) {
-  x += dpp_mov<0x141>(x);   // row_half_mirror
-  x += dpp_mov<0x4E>(x);    // quad_perm:[2,3,0,1]
-  x += dpp_mov<0xB1>(x);    // quad_perm:[1,0,3,2]
-  return x;
-}
+// DPP controls used below. row_ror:8 pairs lane L with L ^ 8 (the other half
+// of the 16-lane DPP row), row_half_mirror pairs L with 7 - L inside an 8-lane
+// half, the quad permutations pair L with L ^ 2 and L ^ 1.
+constexpr int kDppRor8 = 0x128;
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppQuadSwap2 = 0x4E;   // quad_perm:[2,3,0,1]
+constexpr int kDppQuadSwap1 = 0xB1;   // quad_perm:[1,0,3,2]
 
-// One recursive-halving step of a reduce-scatter over a DPP row: the lane
-// keeps half of its N values (the upper half when `upper`) and adds the
-// partner's copy of that half; the partner lane (the DPP source) has the
-// opposite `upper`.
+// One recursive-halving step of a reduce-scatter: the lane keeps half of its
+// N values (the upper half when `upper`) and adds the partner's copy of that
+// half; the partner lane (the DPP source) has the opposite `upper`.
 template <int CTRL, int N>
 __device__ __forceinline__ void rs_step(float* x, bool upper) {
 #pragma unroll
@@ -110,31 +121,34 @@ __device__ __forceinline__ void rs_step(float* x, bool upper) {
   }
 }
 
-// Sums of N values (N = 2, 4, 8, 16) over the 16 lanes of a DPP row, spread
-// over the lanes: afterwards x[0] of lane L holds the full sum of value
-// index L / (16/N), i.e. lanes (16/N)*m .. (16/N)*m + 16/N - 1 hold value m. Partners: L^8 (row_ror:8), the mirror inside an 8-lane half, L^2,
-// L^1; a level with one value left is a plain pairwise sum.
-template <int N>
-__device__ __forceinline__ void row16_scatter(float* x, int L) {
-  static_assert(N == 2 || N == 4 || N == 8 || N == 16, "N must be 2, 4, 8 or 16");
-  rs_step<0x128, N>(x, (L & 8) != 0);
-  if constexpr (N >= 4) rs_step<0x141, N / 2>(x, (L & 4) != 0);
-  else x[0] += dpp_mov<0x141>(x[0]);
-  if constexpr (N >= 8) rs_step<0x4E, N / 4>(x, (L & 2) != 0);
-  else x[0] += dpp_mov<0x4E>(x[0]);
-  if constexpr (N >= 16) rs_step<0xB1, N / 8>(x, (L & 1) != 0);
-  else x[0] += dpp_mov<0xB1>(x[0]);
+// Full sums over the DPP row of a pair of per-row partial sums (own, other):
+// on return `own` and `other` hold the sums of the thread's own and other
+// row, in every lane. Select-free: lane L ^ 8's other row is this lane's own
+// row, and after the first level all lanes of a half hold the same row.
+__device__ __forceinline__ void row_pair_sum(float& own, float& other) {
+  float s = own + dpp_mov<kDppRor8>(other);
+  s += dpp_mov<kDppHalfMirror>(s);
+  s += dpp_mov<kDppQuadSwap2>(s);
+  s += dpp_mov<kDppQuadSwap1>(s);
+  own = s;
+  other = dpp_mov<kDppRor8>(s);
 }
 
-// Both row sums of a lane pair (x0, x1), available in every lane of the DPP
-// row: a reduce-scatter to one value per half, then one exchange.
-__device__ __forceinline__ void row16_sum2(float& x0, float& x1, int L) {
-  float x[2] = {x0, x1};
-  row16_scatter<2>(x, L);   // lanes 0-7: sum of x0, lanes 8-15: sum of x1
-  const float other = dpp_mov<0x128>(x[0]);
-  const bool up = (L & 8) != 0;
-  x0 = up ? other : x[0];
-  x1 = up ? x[0] : other;
+// Reduce-scatter over the DPP row of N per-row partial sums (N a multiple of
+// 16) laid out as [own block | other block], value m of the other block
+// belonging to the other row as value m of the own block does to the own row.
+// Afterwards x[0 .. N/16 - 1] of lane L hold the full sums of the own-block
+// values (L & 7) * N/16 .. (L & 7) * N/16 + N/16 - 1 (of the lane's own row).
+// The first level is select-free (see row_pair_sum); the three levels inside
+// an 8-lane half use rs_step.
+template <int N>
+__device__ __forceinline__ void row16_reduce_scatter(float* x, int L) {
+  static_assert(N % 16 == 0, "N must be a multiple of 16");
+#pragma unroll
+  for (int j = 0; j < N / 2; ++j) x[j] += dpp_mov<kDppRor8>(x[N / 2 + j]);
+  rs_step<kDppHalfMirror, N / 2>(x, (L & 4) != 0);
+  rs_step<kDppQuadSwap2, N / 4>(x, (L & 2) != 0);
+  rs_step<kDppQuadSwap1, N / 8>(x, (L & 1) != 0);
 }
 
 // ---------------------------------------------------------- direct LDS loads
@@ -174,38 +188,40 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 // ------------------------------------------------------------- forward step
-// One timestep of the recurrence on a thread's 2x4 block: S0/S1 are rows 2q
-// and 2q+1, columns 4L .. 4L+3; w4, a4, b4, k4, r4 hold those columns of w~,
-// a, b, k, r and v the two rows of v (wkv7_common/kernel.rs:66-87):
+// One timestep of the recurrence on a thread's 2x4 block (wkv7_common/
+// kernel.rs:66-87): So/St are the own and other row, columns 4L .. 4L+3;
+// w4, a4, b4, k4, r4 hold those columns of w~, a, b, k, r and v = (v_own,
+// v_other):
 //   sa_j = sum_i a_i S[j,i];  S[j,i] = (S[j,i] w~_i + sa_j b_i) + k_i v_j;
 //   y_j = sum_i S[j,i] r_i.
-// On return sa0/sa1 hold sa of both rows in every lane and y holds y of row
-// 2q in lanes 0-7 and of row 2q+1 in lanes 8-15 of the DPP row.
-__device__ __forceinline__ void fwd_step(float* S0, float* S1, float4 w4, float4 a4,
-                                         float4 b4, float4 k4, float4 r4, float2 v, int L,
-                                         float& sa0, float& sa1, float& y) {
+// On return sa_o/sa_t hold sa of the own and other row (every lane) and
+// yp_o/yp_t the thread's partial y sums over its four columns; the caller
+// reduces those over the DPP row (they are not needed by the next step).
+__device__ __forceinline__ void fwd_step(float* So, float* St, float4 w4, float4 a4, float4 b4,
+                                         float4 k4, float4 r4, float2 v, float& sa_o,
+                                         float& sa_t, float& yp_o, float& yp_t) {
   const float w[4] = {w4.x, w4.y, w4.z, w4.w}, a[4] = {a4.x, a4.y, a4.z, a4.w};
   const float b[4] = {b4.x, b4.y, b4.z, b4.w}, k[4] = {k4.x, k4.y, k4.z, k4.w};
   const float r[4] = {r4.x, r4.y, r4.z, r4.w};
-  float p0 = 0.0f, p1 = 0.0f;
+  float po = 0.0f, pt = 0.0f;
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
-    p0 = __builtin_fmaf(a[c], S0[c], p0);
-    p1 = __builtin_fmaf(a[c], S1[c], p1);
+    po = __builtin_fmaf(a[c], So[c], po);
+    pt = __builtin_fmaf(a[c], St[c], pt);
   }
-  row16_sum2(p0, p1, L);
-  sa0 = p0;
-  sa1 = p1;
-  float yy[2] = {0.0f, 0.0f};
+  row_pair_sum(po, pt);
+  sa_o = po;
+  sa_t = pt;
+  float yo = 0.0f, yt = 0.0f;
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
-    S0[c] = __builtin_fmaf(k[c], v.x, __builtin_fmaf(b[c], sa0, S0[c] * w[c]));
-    S1[c] = __builtin_fmaf(k[c], v.y, __builtin_fmaf(b[c], sa1, S1[c] * w[c]));
-    yy[0] = __builtin_fmaf(r[c], S0[c], yy[0]);
-    yy[1] = __builtin_fmaf(r[c], S1[c], yy[1]);
+    So[c] = __builtin_fmaf(k[c], v.x, __builtin_fmaf(b[c], sa_o, So[c] * w[c]));
+    St[c] = __builtin_fmaf(k[c], v.y, __builtin_fmaf(b[c], sa_t, St[c] * w[c]));
+    yo = __builtin_fmaf(r[c], So[c], yo);
+    yt = __builtin_fmaf(r[c], St[c], yt);
   }
-  row16_scatter<2>(yy, L);
-  y = yy[0];
+  yp_o = yo;
+  yp_t = yt;
 }
 
 }  // namespace wkv7

@@ -9,16 +9,18 @@
 //   every C steps: checkpoint S^T (key-major), at the end: s_T = S
 //
 // Design. One 512-thread workgroup per (b, h); each thread keeps a 2x4 block
-// of the state in VGPRs (layout in wkv7_device.hpp). Rows are independent in
-// the forward, so the only cross-lane work is the two row sums (sa and y),
-// four DPP steps each. Operands are staged through LDS in tiles of 16
-// timesteps: the raw rows of the next tile (one timestep of one operand is a
-// 128/256-byte row) stream from global memory straight into LDS
-// (global_load_lds_dwordx4, no VGPRs involved); at the tile end they are
-// widened to fp32 with the decay formed once per element. The loads are in
-// flight while the current tile is consumed. Per step a thread reads its four
-// columns of w~, a, b, k, r (five ds_read_b128) and its two rows of v. y and
-// sa are staged in LDS and written once per tile with full-row stores.
+// of the state in VGPRs (layout and lane-relative row order in
+// wkv7_device.hpp). Rows are independent in the forward, so the only
+// cross-lane work is the row sums: sa (on the step-to-step dependency chain,
+// five DPP operations per step) and y (reduced once per tile for all its
+// steps). Operands are staged through LDS in tiles of 16 timesteps: the raw
+// rows of the next tile (one timestep of one operand is a 128/256-byte row)
+// stream from global memory straight into LDS (global_load_lds_dwordx4, no
+// VGPRs involved); at the tile end they are widened to fp32 with the decay
+// formed once per element. The loads are in flight while the current tile is
+// consumed. Per step a thread reads its four columns of w~, a, b, k, r (five
+// ds_read_b128) and its two rows of v. y and sa are staged in LDS and written
+// once per tile with full-row stores.
 #include "wkv7_device.hpp"
 #include "wkv7_launch.hpp"
 
@@ -27,13 +29,11 @@ namespace {
 
 constexpr int kTile = 16;   // timesteps per LDS tile
 
-// LDS operand vectors per timestep (fp32), and raw rows as loaded
+// raw operand rows as loaded (the order of FwdParams::in)
 enum { V_W = 0, V_R, V_K, V_V, V_A, V_B, V_COUNT };
-
-struct StepOps {
-  float4 w, a, b, k, r;   // columns 4L .. 4L+3
-  float2 v;               // rows 2q, 2q+1
-};
+// fp32 LDS vectors per timestep: the per-column operands, v, and v with each
+// row pair swapped (read by the upper half-rows, which hold (2q+1, 2q))
+enum { L_W = 0, L_R, L_K, L_A, L_B, L_V, L_VS, L_COUNT };
 
 template <typename Tin>
 struct FwdParams {
@@ -46,37 +46,41 @@ struct FwdParams {
   int T, H, C;
 };
 
-// kDefer: C >= kTile, so a tile holds at most one checkpoint, which is kept in
-// registers and stored at the tile end instead of in the middle of the steps.
-template <typename Tin, bool kDefer>
+// kAligned: C is a multiple of kTile, so every tile is full (T is a multiple
+// of C) and checkpoints fall on tile ends only; the steps of a tile then form
+// one branch-free block. Otherwise tiles may be partial and a checkpoint may
+// fall on any step.
+template <typename Tin, bool kAligned>
 __global__ __launch_bounds__(kThreads) void wkv7_fwd_kernel(FwdParams<Tin> p) {
   constexpr int kRow = kHead * sizeof(Tin);   // bytes of one raw row
   constexpr int kRawBytes = V_COUNT * kTile * kRow;
-  __shared__ float4 tile[V_COUNT][kTile][16];   // 24 KiB
+  __shared__ float4 tile[L_COUNT][kTile][16];   // 28 KiB
   __shared__ float ost[2][kTile][kHead];        // 8 KiB: y, sa
   __shared__ float4 raw[kRawBytes / 16];        // 12 or 24 KiB
 
   const int h = blockIdx.x, bi = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63;
-  const int L = tid & 15, q = tid >> 4;   // columns 4L.., rows 2q, 2q+1
+  const int L = tid & 15, q = tid >> 4;   // columns 4L.., row pair 2q, 2q+1
+  const int up = (L >> 3) & 1;
+  const int ro = 2 * q + up, rt = 2 * q + 1 - up;   // own and other row
   // conversion and flush: timestep sl, elements 4pp .. 4pp+3, half cg
   const int cg = tid >> 8, sl = (tid >> 4) & 15, pp = tid & 15;
 
-  const int T = p.T;
+  const int T = p.T, C = p.C;
   const int64_t bh = (int64_t)bi * p.H + h;
   const int64_t tstride = (int64_t)p.H * kHead;
   const int64_t tok0 = ((int64_t)bi * T * p.H + h) * kHead;
 
-  float S0[4], S1[4];   // rows 2q and 2q+1, columns 4L .. 4L+3
+  float So[4], St[4];   // own and other row, columns 4L .. 4L+3
   if (p.s0) {
-    const float* base = p.s0 + (bh * kHead + 2 * q) * kHead + 4 * L;
-    const float4 x0 = *reinterpret_cast<const float4*>(base);
-    const float4 x1 = *reinterpret_cast<const float4*>(base + kHead);
-    S0[0] = x0.x; S0[1] = x0.y; S0[2] = x0.z; S0[3] = x0.w;
-    S1[0] = x1.x; S1[1] = x1.y; S1[2] = x1.z; S1[3] = x1.w;
+    const float* base = p.s0 + bh * (kHead * kHead) + 4 * L;
+    const float4 x0 = *reinterpret_cast<const float4*>(base + ro * kHead);
+    const float4 x1 = *reinterpret_cast<const float4*>(base + rt * kHead);
+    So[0] = x0.x; So[1] = x0.y; So[2] = x0.z; So[3] = x0.w;
+    St[0] = x1.x; St[1] = x1.y; St[2] = x1.z; St[3] = x1.w;
   } else {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) { S0[c] = 0.0f; S1[c] = 0.0f; }
+    for (int c = 0; c < 4; ++c) { So[c] = 0.0f; St[c] = 0.0f; }
   }
 
   typedef Io<Tin> io;
@@ -108,57 +112,32 @@ __global__ __launch_bounds__(kThreads) void wkv7_fwd_kernel(FwdParams<Tin> p) {
       x.y = decay_f(sigmoid_f(x.y));
       x.z = decay_f(sigmoid_f(x.z));
       x.w = decay_f(sigmoid_f(x.w));
-      tile[V_W][sl][pp] = x;
-      tile[V_R][sl][pp] = rawv(V_R);
-      tile[V_K][sl][pp] = rawv(V_K);
+      tile[L_W][sl][pp] = x;
+      tile[L_R][sl][pp] = rawv(V_R);
+      tile[L_K][sl][pp] = rawv(V_K);
     } else {
-      tile[V_V][sl][pp] = rawv(V_V);
-      tile[V_A][sl][pp] = rawv(V_A);
-      tile[V_B][sl][pp] = rawv(V_B);
+      const float4 v = rawv(V_V);
+      tile[L_V][sl][pp] = v;
+      tile[L_VS][sl][pp] = make_float4(v.y, v.x, v.w, v.z);
+      tile[L_A][sl][pp] = rawv(V_A);
+      tile[L_B][sl][pp] = rawv(V_B);
     }
   };
-  auto lread = [&](int s) {
-    StepOps o;
-    o.w = tile[V_W][s][L];
-    o.a = tile[V_A][s][L];
-    o.b = tile[V_B][s][L];
-    o.k = tile[V_K][s][L];
-    o.r = tile[V_R][s][L];
-    o.v = reinterpret_cast<const float2*>(tile[V_V][s])[q];
-    return o;
-  };
+  // (own, other) rows of v for this thread, per step: 32 float2 per step row
+  const float2* vrow = reinterpret_cast<const float2*>(&tile[up ? L_VS : L_V][0][0]) + q;
 
-  // checkpoint c: S after step c*C + C - 1, stored key-major ([i][j])
-  const int C = p.C;
-  const int64_t nchunks = T / C;
-  float* ckpt_bh = p.ckpt + (bh * nchunks * kHead + 4 * L) * kHead + 2 * q;
-  int until_ckpt = C;
-  int64_t chunk = 0;
-  bool ck_pending = false;
-  float Ck0[4], Ck1[4];
-  auto ck_store = [&](int64_t c, const float* a0, const float* a1) {
+  // checkpoint c: S after step c*C + C - 1, stored key-major ([i][j]); the
+  // thread writes (S[2q][i], S[2q+1][i]) for its four columns i
+  float* ckpt_bh = p.ckpt + (bh * (T / C) * kHead + 4 * L) * kHead + 2 * q;
+  auto ck_store = [&](int64_t c) {
     float* dst = ckpt_bh + c * (kHead * kHead);
 #pragma unroll
     for (int m = 0; m < 4; ++m)
-      *reinterpret_cast<float2*>(dst + m * kHead) = make_float2(a0[m], a1[m]);
+      *reinterpret_cast<float2*>(dst + m * kHead) =
+          up ? make_float2(St[m], So[m]) : make_float2(So[m], St[m]);
   };
-
-  auto step = [&](const StepOps& o, int s) {
-    float sa0, sa1, y;
-    fwd_step(S0, S1, o.w, o.a, o.b, o.k, o.r, o.v, L, sa0, sa1, y);
-    if ((L & 7) == 0) ost[0][s][2 * q + (L >> 3)] = y;
-    if (L == 0) reinterpret_cast<float2*>(ost[1][s])[q] = make_float2(sa0, sa1);
-    if (--until_ckpt == 0) {   // (t + 1) % C == 0, kernel.rs:89-102
-      until_ckpt = C;
-      if constexpr (kDefer) {
-#pragma unroll
-        for (int m = 0; m < 4; ++m) { Ck0[m] = S0[m]; Ck1[m] = S1[m]; }
-        ck_pending = true;
-      } else {
-        ck_store(chunk++, S0, S1);
-      }
-    }
-  };
+  int until_ckpt = C;   // steps until the next checkpoint (unaligned C)
+  int64_t chunk = 0;
 
   // Tile pipeline. While tile ti is computed, the raw operands of tile ti+1
   // stream into LDS. At the tile end one wait + barrier makes them visible;
@@ -169,33 +148,54 @@ __global__ __launch_bounds__(kThreads) void wkv7_fwd_kernel(FwdParams<Tin> p) {
   if (ntiles > 0) {
     issue(0, tile_n(0));
     __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    lds_barrier();
     convert(tile_n(0));
-    __syncthreads();
+    lds_barrier();
     if (ntiles > 1) issue(kTile, tile_n(1));
   }
 
   for (int ti = 0; ti < ntiles; ++ti) {
     const int t0 = ti * kTile, nst = tile_n(ti);
 
-    // Two operand sets alternate so that the reads for step s+1 are in flight
-    // while step s computes, without register copies between iterations.
-    StepOps A = lread(0);
-    int s = 0;
-    for (; s + 1 < nst; s += 2) {
-      const StepOps Bo = lread(s + 1);
-      step(A, s);
-      A = lread(min(s + 2, nst - 1));
-      step(Bo, s + 1);
+    // y partials of both rows for every step, [own block | other block]
+    float yp[2 * kTile];
+    float sav[kTile];   // sa of the own row
+#pragma unroll
+    for (int s = 0; s < kTile; ++s) {
+      if constexpr (!kAligned) {
+        if (s >= nst) {   // uniform: the last tile may be partial
+          yp[s] = yp[kTile + s] = sav[s] = 0.0f;
+          continue;
+        }
+      }
+      float sa_t;
+      fwd_step(So, St, tile[L_W][s][L], tile[L_A][s][L], tile[L_B][s][L], tile[L_K][s][L],
+               tile[L_R][s][L], vrow[s * 32], sav[s], sa_t, yp[s], yp[kTile + s]);
+      if constexpr (!kAligned) {
+        if (--until_ckpt == 0) {   // (t + 1) % C == 0, kernel.rs:89-102
+          until_ckpt = C;
+          ck_store(chunk++);
+        }
+      }
     }
-    if (s < nst) step(A, s);
+    // y of the own row for steps 2(L&7) and 2(L&7)+1
+    row16_reduce_scatter<2 * kTile>(yp, L);
+    ost[0][2 * (L & 7)][ro] = yp[0];
+    ost[0][2 * (L & 7) + 1][ro] = yp[1];
+    if ((L & 7) == 0) {
+#pragma unroll
+      for (int s = 0; s < kTile; ++s) ost[1][s][ro] = sav[s];
+    }
 
-    if (ck_pending) {
-      ck_store(chunk++, Ck0, Ck1);
-      ck_pending = false;
-    }
+    // The loads of tile ti+1 have landed once vmcnt reaches 0 (they and the
+    // stores of the previous tile end were issued a whole tile ago). Only LDS
+    // is fenced by the barriers, so the stores below are not waited for until
+    // the next tile end.
     __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    lds_barrier();
+    if constexpr (kAligned) {
+      if ((t0 + kTile) % C == 0) ck_store((t0 + kTile) / C - 1);   // kernel.rs:89-102
+    }
     if (sl < nst) {   // cg 0 writes y, cg 1 writes sa
       const int64_t off = tok0 + (int64_t)(t0 + sl) * tstride + 4 * pp;
       const float4 x = reinterpret_cast<const float4*>(ost[cg][sl])[pp];
@@ -203,14 +203,14 @@ __global__ __launch_bounds__(kThreads) void wkv7_fwd_kernel(FwdParams<Tin> p) {
       else *reinterpret_cast<float4*>(p.sa + off) = x;
     }
     if (ti + 1 < ntiles) convert(tile_n(ti + 1));
-    __syncthreads();
+    lds_barrier();   // converted tile visible; `raw` free for the next loads
     if (ti + 2 < ntiles) issue((ti + 2) * kTile, tile_n(ti + 2));
   }
 
   if (p.sT) {
-    float* base = p.sT + (bh * kHead + 2 * q) * kHead + 4 * L;
-    *reinterpret_cast<float4*>(base) = make_float4(S0[0], S0[1], S0[2], S0[3]);
-    *reinterpret_cast<float4*>(base + kHead) = make_float4(S1[0], S1[1], S1[2], S1[3]);
+    float* base = p.sT + bh * (kHead * kHead) + 4 * L;
+    *reinterpret_cast<float4*>(base + ro * kHead) = make_float4(So[0], So[1], So[2], So[3]);
+    *reinterpret_cast<float4*>(base + rt * kHead) = make_float4(St[0], St[1], St[2], St[3]);
   }
 }
 
@@ -231,12 +231,11 @@ hipError_t launch_fwd_t(const ForwardDesc& d, hipStream_t stream) {
   p.T = d.T;
   p.H = d.H;
   p.C = d.C;
-  if (d.C >= kTile)
-    hipLaunchKernelGGL((wkv7_fwd_kernel<Tin, true>), dim3(d.H, d.B, 1), dim3(kThreads, 1, 1), 0,
-                       stream, p);
+  const dim3 grid(d.H, d.B, 1), block(kThreads, 1, 1);
+  if (d.C % kTile == 0)
+    hipLaunchKernelGGL((wkv7_fwd_kernel<Tin, true>), grid, block, 0, stream, p);
   else
-    hipLaunchKernelGGL((wkv7_fwd_kernel<Tin, false>), dim3(d.H, d.B, 1), dim3(kThreads, 1, 1), 0,
-                       stream, p);
+    hipLaunchKernelGGL((wkv7_fwd_kernel<Tin, false>), grid, block, 0, stream, p);
   return hipGetLastError();
 }
 

@@ -59,7 +59,9 @@ __global__ __launch_bounds__(kThreads) void wkv7_infer_kernel(InferParams<Tin> p
 
   const int h = blockIdx.x, bi = blockIdx.y;
   const int tid = threadIdx.x;
-  const int L = tid & 15, q = tid >> 4;   // columns 4L.., rows 2q, 2q+1
+  const int L = tid & 15, q = tid >> 4;   // columns 4L.., row pair 2q, 2q+1
+  const int up = (L >> 3) & 1;
+  const int ro = 2 * q + up, rt = 2 * q + 1 - up;   // own and other row
   const int sl = (tid >> 4) & 15, pp = tid & 15;   // staging (threads 0..255)
   const bool stager = tid < 16 * kTile;
 
@@ -79,13 +81,13 @@ __global__ __launch_bounds__(kThreads) void wkv7_infer_kernel(InferParams<Tin> p
   const int64_t tstride = (int64_t)p.H * kHead;
   const int64_t tok0 = ((int64_t)bi * T * p.H + h) * kHead;
 
-  float* st = p.state + ((slot * p.H + h) * kHead + 2 * q) * kHead + 4 * L;
-  float S0[4], S1[4];
+  float* st = p.state + (slot * p.H + h) * (kHead * kHead) + 4 * L;
+  float So[4], St[4];   // own and other row
   {
-    const float4 x0 = *reinterpret_cast<const float4*>(st);
-    const float4 x1 = *reinterpret_cast<const float4*>(st + kHead);
-    S0[0] = x0.x; S0[1] = x0.y; S0[2] = x0.z; S0[3] = x0.w;
-    S1[0] = x1.x; S1[1] = x1.y; S1[2] = x1.z; S1[3] = x1.w;
+    const float4 x0 = *reinterpret_cast<const float4*>(st + ro * kHead);
+    const float4 x1 = *reinterpret_cast<const float4*>(st + rt * kHead);
+    So[0] = x0.x; So[1] = x0.y; So[2] = x0.z; So[3] = x0.w;
+    St[0] = x1.x; St[1] = x1.y; St[2] = x1.z; St[3] = x1.w;
   }
 
   typedef Io<Tin> io;
@@ -155,12 +157,14 @@ __global__ __launch_bounds__(kThreads) void wkv7_infer_kernel(InferParams<Tin> p
     for (int s = 0; s < nst; ++s) {
       float y = 0.0f;
       if (live[buf][s]) {   // uniform across the workgroup
-        float sa0, sa1;
-        fwd_step(S0, S1, tile[buf][V_W][s][L], tile[buf][V_A][s][L], tile[buf][V_B][s][L],
+        const float2 v2 = reinterpret_cast<const float2*>(tile[buf][V_V][s])[q];
+        float sa_o, sa_t, y_t;
+        fwd_step(So, St, tile[buf][V_W][s][L], tile[buf][V_A][s][L], tile[buf][V_B][s][L],
                  tile[buf][V_K][s][L], tile[buf][V_R][s][L],
-                 reinterpret_cast<const float2*>(tile[buf][V_V][s])[q], L, sa0, sa1, y);
+                 up ? make_float2(v2.y, v2.x) : v2, sa_o, sa_t, y, y_t);
+        row_pair_sum(y, y_t);   // y of the own row
       }
-      if ((L & 7) == 0) ost[buf][s][2 * q + (L >> 3)] = y;
+      if ((L & 7) == 0) ost[buf][s][ro] = y;
     }
 
     if (ti + 1 < ntiles) lstore(buf ^ 1, t0 + kTile);
@@ -171,8 +175,8 @@ __global__ __launch_bounds__(kThreads) void wkv7_infer_kernel(InferParams<Tin> p
     }
   }
 
-  *reinterpret_cast<float4*>(st) = make_float4(S0[0], S0[1], S0[2], S0[3]);
-  *reinterpret_cast<float4*>(st + kHead) = make_float4(S1[0], S1[1], S1[2], S1[3]);
+  *reinterpret_cast<float4*>(st + ro * kHead) = make_float4(So[0], So[1], So[2], So[3]);
+  *reinterpret_cast<float4*>(st + rt * kHead) = make_float4(St[0], St[1], St[2], St[3]);
 }
 
 template <typename Tin>

@@ -101,6 +101,42 @@ def test_fp32_gradients_match_fp64(wk, oracle):
         assert err < FP32_TOL, (gn, err)
 
 
+@pytest.mark.parametrize("case", [
+    (1, 96, 2, 32, 0.1, 8),   # two 16-step tiles per checkpoint interval
+    (1, 48, 2, 24, 0.1, 9),   # a checkpoint in the middle of a forward tile
+])
+def test_fp32_long_chunks_as_accurate_as_reference(wk, oracle, case):
+    # The backward rebuilds S_{t-1} = (S_t - v k^T - sa b^T) / w~ (kernel.rs:239-246),
+    # which amplifies rounding roughly 1.35x per step between checkpoints: at
+    # chunk_len 24-32 the reference algorithm itself is off the exact gradient by
+    # 1e-5 .. 1e-3, and any two fp32 evaluations of it differ by as much. The
+    # gradients that use the rebuilt S (dw, dr, da) are therefore held to the
+    # reference algorithm's own accuracy against exact fp64 gradients; everything
+    # else, which does not pass through the rebuild, to the fp32 tolerance.
+    B, T, H, C, s0_std, seed = case
+    announce("fp32 long chunk", case)
+    d = load_pkg().synthetic.make_inputs(B, T, H, 64, seed=seed, s0_std=s0_std)
+    dsT = np.random.default_rng(seed + 50).standard_normal((B, H, 64, 64)).astype(np.float32)
+    fwd, bwd = run_gpu(wk, d, C, torch.float32, dsT=dsT)
+    ofwd, obwd = run_oracle(oracle, d, C, dsT=dsT)
+    exact = oracle.grad_f64(*(d[n] for n in NAMES), d["s0"], d["dy"], ds_T=dsT)
+    for key, got, want in (("output", fwd.output, ofwd["output"]),
+                           ("removal_state", fwd.removal_state, ofwd["removal_state"]),
+                           ("state", fwd.state, ofwd["state"]),
+                           ("final_state", fwd.final_state, ofwd["final_state"])):
+        assert rel_l2(to_np(got), want) <= FP32_TOL, key
+    rebuilt = ("weight_decay_grad", "receptance_grad", "removal_grad")
+    for gn in GRAD_NAMES + ("initial_state_grad",):
+        got = to_np(getattr(bwd, gn))
+        if gn in rebuilt:
+            ref_err = rel_l2(obwd[gn], exact[gn])
+            err = rel_l2(got, exact[gn])
+            print(case, gn, f"gpu {err:.2e} reference-algorithm {ref_err:.2e}", flush=True)
+            assert err <= 5 * ref_err + 1e-6, (gn, err, ref_err)
+        else:
+            assert rel_l2(got, obwd[gn]) <= FP32_TOL, gn
+
+
 @pytest.mark.parametrize("case", [(2, 128, 4, 16, 0.1, 11), (1, 64, 4, 16, None, 12)])
 def test_bf16_inputs_fp32_state(wk, oracle, case):
     B, T, H, C, s0_std, seed = case
