@@ -129,7 +129,7 @@ def pmc_summary(dirs):
     import csv
     import glob
     from collections import defaultdict
-    keys = ("wkv7_fwd_kernel", "wkv7_bwd_kernel", "wkv7_infer_kernel", "abs_kernel")
+    keys = ("wkv7_fwd_kernel", "wkv7_bwd_kernel", "wkv7_infer_kernel", "AbsFunctor")
     per = defaultdict(lambda: defaultdict(lambda: defaultdict(float)))
     for d in dirs:
         for path in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
@@ -142,13 +142,13 @@ def pmc_summary(dirs):
                     # rows of one dispatch (one per XCD / shader engine) add up
                     per[key][row["Counter_Name"]][row["Dispatch_Id"]] += float(row["Counter_Value"])
     # the probe is the last dispatch of its kernel
-    for c, v in per.get("abs_kernel", {}).items():
+    for c, v in per.get("AbsFunctor", {}).items():
         last = max(v, key=int)
-        per["abs_kernel"][c] = {last: v[last]}
+        per["AbsFunctor"][c] = {last: v[last]}
     mean = {k: {c: sum(v.values()) / len(v) for c, v in cs.items()} for k, cs in per.items()}
     probe_kib = COPY_PROBE_BYTES / 1024
-    scale = {c: probe_kib / mean["abs_kernel"][c] for c in ("FETCH_SIZE", "WRITE_SIZE")
-             if "abs_kernel" in mean and c in mean["abs_kernel"]}
+    scale = {c: probe_kib / mean["AbsFunctor"][c] for c in ("FETCH_SIZE", "WRITE_SIZE")
+             if "AbsFunctor" in mean and c in mean["AbsFunctor"]}
     print("| kernel | counter | KiB per dispatch | scale | bytes per dispatch |")
     print("|---|---|---|---|---|")
     totals = {}
@@ -156,7 +156,7 @@ def pmc_summary(dirs):
         for c, v in sorted(mean.get(k, {}).items()):
             sc = scale.get(c)
             b = v * 1024 * sc if sc else None
-            if b is not None and k != "abs_kernel":
+            if b is not None and k != "AbsFunctor":
                 totals[k] = totals.get(k, 0) + b
             print(f"| {k} | {c} | {v:.0f} | {sc if sc else '-'} | "
                   f"{'-' if b is None else f'{b:.0f}'} |")

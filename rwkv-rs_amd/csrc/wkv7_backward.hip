@@ -98,8 +98,9 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
   const int L = tid & 15, q = tid >> 4;
   const int up = (L >> 3) & 1;
   const int ro = 2 * q + up, rt = 2 * q + 1 - up;   // own and other row / column
-  // conversion: group sg = tid / 128 (0: w; 1: r, k; 2: b, a; 3: dy, v, sa),
-  // timestep sl, elements 4pp .. 4pp+3
+  // conversion: the decay of element e = tid % 64 of timestep tid / 64, then
+  // group sg = tid / 128 (0: r, k; 1: b, a; 2: dy, v, sa; 3: none) widens
+  // elements 4pp .. 4pp+3 of timestep sl; flush: the same (sl, pp)
   const int sg = tid >> 7, sl = (tid >> 4) & 7, pp = tid & 15;
 
   const int T = p.T, C = p.C;
@@ -141,8 +142,31 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
   };
   // raw tile -> fp32 operand vectors and column-pair records (plain, swapped)
   auto convert = [&](int nst) {
-    if (sl >= nst) return;
     const char* rb = reinterpret_cast<const char*>(raw);
+    {   // w -> w~, 1/w~ and the dw factor, one element per thread
+      const int ws_ = tid >> 6, e = tid & 63;
+      if (ws_ < nst) {
+        float x;
+        if constexpr (sizeof(Tin) == 2)
+          x = bf16_to_f32(reinterpret_cast<const bf16_t*>(rb + (R_W * kTile + ws_) * kRow)[e]);
+        else
+          x = reinterpret_cast<const float*>(rb + (R_W * kTile + ws_) * kRow)[e];
+        const float sig = sigmoid_f(x);
+        const float w = decay_f(sig);
+        const float iw = 1.0f / w;
+        reinterpret_cast<float*>(tile[V_W][ws_])[e] = w;
+        reinterpret_cast<float*>(tile[V_DWF][ws_])[e] = kWScale * w * sig * (1.0f - sig);
+        // record {w~[2p], w~[2p+1], iw[2p], iw[2p+1]}, e = 2p + b; swapped copy
+        float* pl = reinterpret_cast<float*>(&pairs[0][P_WI][ws_][e >> 1]);
+        float* sw = reinterpret_cast<float*>(&pairs[1][P_WI][ws_][e >> 1]);
+        const int b = e & 1;
+        pl[b] = w;
+        pl[2 + b] = iw;
+        sw[1 - b] = w;
+        sw[3 - b] = iw;
+      }
+    }
+    if (sl >= nst) return;
     auto rawv = [&](int vec) {
       return Io<Tin>::widen(*reinterpret_cast<const typename Io<Tin>::raw*>(
           rb + (vec * kTile + sl) * kRow + 4 * pp * sizeof(Tin)));
@@ -154,31 +178,16 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
       pairs[1][rec][sl][2 * pp + 1] = make_float4(x.w, x.z, y.w, y.z);
     };
     if (sg == 0) {
-      const float4 x = rawv(R_W);
-      const float xs[4] = {x.x, x.y, x.z, x.w};
-      float ws[4], iws[4], dws[4];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const float sig = sigmoid_f(xs[c]);
-        ws[c] = decay_f(sig);
-        iws[c] = 1.0f / ws[c];
-        dws[c] = kWScale * ws[c] * sig * (1.0f - sig);
-      }
-      const float4 w4 = make_float4(ws[0], ws[1], ws[2], ws[3]);
-      tile[V_W][sl][pp] = w4;
-      tile[V_DWF][sl][pp] = make_float4(dws[0], dws[1], dws[2], dws[3]);
-      put_pairs(P_WI, w4, make_float4(iws[0], iws[1], iws[2], iws[3]));
-    } else if (sg == 1) {
       const float4 r = rawv(R_R), k = rawv(R_K);
       tile[V_R][sl][pp] = r;
       tile[V_K][sl][pp] = k;
       put_pairs(P_RK, r, k);
-    } else if (sg == 2) {
+    } else if (sg == 1) {
       const float4 b = rawv(R_B), a = rawv(R_A);
       tile[V_B][sl][pp] = b;
       tile[V_A][sl][pp] = a;
       put_pairs(P_BA, b, a);
-    } else {
+    } else if (sg == 2) {
       const float4 dy = rawv(R_DY);
       tile[V_DY][sl][pp] = dy;
       tile[V_DYS][sl][pp] = make_float4(dy.y, dy.x, dy.w, dy.z);

@@ -63,7 +63,9 @@ __global__ __launch_bounds__(kThreads) void wkv7_fwd_kernel(FwdParams<Tin> p) {
   const int L = tid & 15, q = tid >> 4;   // columns 4L.., row pair 2q, 2q+1
   const int up = (L >> 3) & 1;
   const int ro = 2 * q + up, rt = 2 * q + 1 - up;   // own and other row
-  // conversion and flush: timestep sl, elements 4pp .. 4pp+3, half cg
+  // conversion: the decay of elements 2e, 2e+1 (e = tid % 32) of timestep
+  // tid / 32, then half cg widens the other operands' elements 4pp .. 4pp+3 of
+  // timestep sl; flush: the same (cg, sl, pp)
   const int cg = tid >> 8, sl = (tid >> 4) & 15, pp = tid & 15;
 
   const int T = p.T, C = p.C;
@@ -100,19 +102,27 @@ __global__ __launch_bounds__(kThreads) void wkv7_fwd_kernel(FwdParams<Tin> p) {
   };
   // raw tile -> fp32 vectors; the decay w~ is formed here, once per element
   auto convert = [&](int nst) {
-    if (sl >= nst) return;
     const char* rb = reinterpret_cast<const char*>(raw);
+    {   // w -> w~, two elements per thread
+      const int ws_ = tid >> 5, e = tid & 31;
+      if (ws_ < nst) {
+        float2 x;
+        if constexpr (sizeof(Tin) == 2) {
+          const uint32_t u = reinterpret_cast<const uint32_t*>(rb + (V_W * kTile + ws_) * kRow)[e];
+          x = make_float2(bf16_to_f32(u & 0xffffu), bf16_to_f32(u >> 16));
+        } else {
+          x = reinterpret_cast<const float2*>(rb + (V_W * kTile + ws_) * kRow)[e];
+        }
+        reinterpret_cast<float2*>(tile[L_W][ws_])[e] =
+            make_float2(decay_f(sigmoid_f(x.x)), decay_f(sigmoid_f(x.y)));
+      }
+    }
+    if (sl >= nst) return;
     auto rawv = [&](int vec) {
       return io::widen(*reinterpret_cast<const typename io::raw*>(
           rb + (vec * kTile + sl) * kRow + 4 * pp * sizeof(Tin)));
     };
     if (cg == 0) {
-      float4 x = rawv(V_W);
-      x.x = decay_f(sigmoid_f(x.x));
-      x.y = decay_f(sigmoid_f(x.y));
-      x.z = decay_f(sigmoid_f(x.z));
-      x.w = decay_f(sigmoid_f(x.w));
-      tile[L_W][sl][pp] = x;
       tile[L_R][sl][pp] = rawv(V_R);
       tile[L_K][sl][pp] = rawv(V_K);
     } else {
