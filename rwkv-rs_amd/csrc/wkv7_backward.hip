@@ -52,8 +52,10 @@ enum {
 };
 // per-column-pair records for the column role, float4 {x[2p], x[2p+1],
 // y[2p], y[2p+1]}; a second copy with each pair swapped serves the upper
-// half-rows
-enum { P_RK = 0, P_BA, P_WI, P_COUNT };   // {r, k}, {b, a}, {w~, 1/w~}
+// half-rows. k and b enter the column role only through the reversal
+// (S - k v - b sa), so they are stored negated: the FMAs then need no source
+// modifier and encode as two-operand v_fmac.
+enum { P_RK = 0, P_BA, P_WI, P_COUNT };   // {r, -k}, {-b, a}, {w~, 1/w~}
 // gradient outputs, in the order of the per-step partials
 enum { O_DV = 0, O_DR, O_DW, O_DK, O_DB, O_DA, O_COUNT };
 // raw (input dtype) operand rows as loaded from global memory
@@ -181,12 +183,12 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
       const float4 r = rawv(R_R), k = rawv(R_K);
       tile[V_R][sl][pp] = r;
       tile[V_K][sl][pp] = k;
-      put_pairs(P_RK, r, k);
+      put_pairs(P_RK, r, make_float4(-k.x, -k.y, -k.z, -k.w));
     } else if (sg == 1) {
       const float4 b = rawv(R_B), a = rawv(R_A);
       tile[V_B][sl][pp] = b;
       tile[V_A][sl][pp] = a;
-      put_pairs(P_BA, b, a);
+      put_pairs(P_BA, make_float4(-b.x, -b.y, -b.z, -b.w), a);
     } else if (sg == 2) {
       const float4 dy = rawv(R_DY);
       tile[V_DY][sl][pp] = dy;
@@ -236,11 +238,17 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
     unpack4(kk, tile[V_K][s][L]);
     unpack4(bb, tile[V_B][s][L]);
     const float2 dyr = dyrow[s * 32];
-    float dvo = 0.0f, dvt = 0.0f, dsa_o = 0.0f, dsa_t = 0.0f;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       dSo[c] = __builtin_fmaf(dyr.x, rr[c], dSo[c]);
       dSt[c] = __builtin_fmaf(dyr.y, rr[c], dSt[c]);
+    }
+    // partial sums start from their first product (a product, not an FMA
+    // with +0, which the compiler must keep as a three-operand VOP3 FMA)
+    float dvo = dSo[0] * kk[0], dvt = dSt[0] * kk[0];
+    float dsa_o = dSo[0] * bb[0], dsa_t = dSt[0] * bb[0];
+#pragma unroll
+    for (int c = 1; c < 4; ++c) {
       dvo = __builtin_fmaf(dSo[c], kk[c], dvo);
       dvt = __builtin_fmaf(dSt[c], kk[c], dvt);
       dsa_o = __builtin_fmaf(dSo[c], bb[c], dsa_o);
@@ -257,22 +265,23 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
     unpack4(v, tile[V_V][s][L]);
     unpack4(sa, tile[V_SA][s][L]);
     const float4 prk = prec[P_RK][s][q], pba = prec[P_BA][s][q], pwi = prec[P_WI][s][q];
-    const float rc[2] = {prk.x, prk.y}, kc[2] = {prk.z, prk.w};
-    const float bc[2] = {pba.x, pba.y}, ac[2] = {pba.z, pba.w};
+    const float rc[2] = {prk.x, prk.y}, nkc[2] = {prk.z, prk.w};   // r, -k
+    const float nbc[2] = {pba.x, pba.y}, ac[2] = {pba.z, pba.w};   // -b, a
     const float wc[2] = {pwi.x, pwi.y}, iwc[2] = {pwi.z, pwi.w};
-    float drp[2] = {0.0f, 0.0f}, dwp[2] = {0.0f, 0.0f}, dkp[2] = {0.0f, 0.0f};
-    float dbp[2] = {0.0f, 0.0f};
+    float drp[2], dwp[2], dkp[2], dbp[2];
 #pragma unroll
     for (int c = 0; c < 4; ++c)
 #pragma unroll
       for (int d = 0; d < 2; ++d) {
-        drp[d] = __builtin_fmaf(Sc[c][d], dy[c], drp[d]);   // kernel.rs:230-237
+        // kernel.rs:230-237
+        drp[d] = c == 0 ? Sc[c][d] * dy[c] : __builtin_fmaf(Sc[c][d], dy[c], drp[d]);
         // ((S - k v) - b sa) / w~, kernel.rs:239-246
-        Sc[c][d] = __builtin_fmaf(-bc[d], sa[c], __builtin_fmaf(-kc[d], v[c], Sc[c][d])) * iwc[d];
+        Sc[c][d] = __builtin_fmaf(nbc[d], sa[c], __builtin_fmaf(nkc[d], v[c], Sc[c][d])) * iwc[d];
         dSc[c][d] = __builtin_fmaf(rc[d], dy[c], dSc[c][d]);   // kernel.rs:249
-        dwp[d] = __builtin_fmaf(dSc[c][d], Sc[c][d], dwp[d]);   // kernel.rs:258-264
-        dkp[d] = __builtin_fmaf(dSc[c][d], v[c], dkp[d]);
-        dbp[d] = __builtin_fmaf(dSc[c][d], sa[c], dbp[d]);
+        // kernel.rs:258-264
+        dwp[d] = c == 0 ? dSc[c][d] * Sc[c][d] : __builtin_fmaf(dSc[c][d], Sc[c][d], dwp[d]);
+        dkp[d] = c == 0 ? dSc[c][d] * v[c] : __builtin_fmaf(dSc[c][d], v[c], dkp[d]);
+        dbp[d] = c == 0 ? dSc[c][d] * sa[c] : __builtin_fmaf(dSc[c][d], sa[c], dbp[d]);
       }
 
     lds_barrier();   // dsa of every row visible
@@ -289,12 +298,12 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
       dSt[c] = __builtin_fmaf(dsa_t, aa[c], dSt[c] * ww[c]);
     }
     // column role: da = S_{t-1}^T dsa (kernel.rs:280-287); dS col = dS col * w~ + a dsa
-    float dap[2] = {0.0f, 0.0f};
+    float dap[2];
 #pragma unroll
     for (int c = 0; c < 4; ++c)
 #pragma unroll
       for (int d = 0; d < 2; ++d) {
-        dap[d] = __builtin_fmaf(Sc[c][d], ds[c], dap[d]);
+        dap[d] = c == 0 ? Sc[c][d] * ds[c] : __builtin_fmaf(Sc[c][d], ds[c], dap[d]);
         dSc[c][d] = __builtin_fmaf(ac[d], ds[c], dSc[c][d] * wc[d]);   // kernel.rs:293-294
       }
     float* po = part + O_COUNT * s;

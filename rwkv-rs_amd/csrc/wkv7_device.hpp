@@ -203,22 +203,24 @@ __device__ __forceinline__ void fwd_step(float* So, float* St, float4 w4, float4
   const float w[4] = {w4.x, w4.y, w4.z, w4.w}, a[4] = {a4.x, a4.y, a4.z, a4.w};
   const float b[4] = {b4.x, b4.y, b4.z, b4.w}, k[4] = {k4.x, k4.y, k4.z, k4.w};
   const float r[4] = {r4.x, r4.y, r4.z, r4.w};
-  float po = 0.0f, pt = 0.0f;
+  // partial sums start from their first product (a product, not an FMA with
+  // +0, which the compiler must keep as a three-operand VOP3 FMA)
+  float po = a[0] * So[0], pt = a[0] * St[0];
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
+  for (int c = 1; c < 4; ++c) {
     po = __builtin_fmaf(a[c], So[c], po);
     pt = __builtin_fmaf(a[c], St[c], pt);
   }
   row_pair_sum(po, pt);
   sa_o = po;
   sa_t = pt;
-  float yo = 0.0f, yt = 0.0f;
+  float yo, yt;
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     So[c] = __builtin_fmaf(k[c], v.x, __builtin_fmaf(b[c], sa_o, So[c] * w[c]));
     St[c] = __builtin_fmaf(k[c], v.y, __builtin_fmaf(b[c], sa_t, St[c] * w[c]));
-    yo = __builtin_fmaf(r[c], So[c], yo);
-    yt = __builtin_fmaf(r[c], St[c], yt);
+    yo = c == 0 ? r[c] * So[c] : __builtin_fmaf(r[c], So[c], yo);
+    yt = c == 0 ? r[c] * St[c] : __builtin_fmaf(r[c], St[c], yt);
   }
   yp_o = yo;
   yp_t = yt;

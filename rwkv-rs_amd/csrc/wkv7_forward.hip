@@ -20,14 +20,16 @@
 // formed once per element. The loads are in flight while the current tile is
 // consumed. Per step a thread reads its four columns of w~, a, b, k, r (five
 // ds_read_b128) and its two rows of v. y and sa are staged in LDS and written
-// once per tile with full-row stores.
+// once per tile with full-row stores; checkpoints are transposed through LDS
+// and written as full 256-byte rows. The tile end has a fixed cost (waits,
+// two barriers, the widening pass), which the 32-step tile amortises.
 #include "wkv7_device.hpp"
 #include "wkv7_launch.hpp"
 
 namespace wkv7 {
 namespace {
 
-constexpr int kTile = 16;   // timesteps per LDS tile
+constexpr int kTile = 32;   // timesteps per LDS tile
 
 // raw operand rows as loaded (the order of FwdParams::in)
 enum { V_W = 0, V_R, V_K, V_V, V_A, V_B, V_COUNT };
@@ -46,27 +48,39 @@ struct FwdParams {
   int T, H, C;
 };
 
-// kAligned: C is a multiple of kTile, so every tile is full (T is a multiple
-// of C) and checkpoints fall on tile ends only; the steps of a tile then form
-// one branch-free block. Otherwise tiles may be partial and a checkpoint may
-// fall on any step.
-template <typename Tin, bool kAligned>
+// Checkpoint placement, fixed at compile time where it can be:
+//   kCkTile  C is a multiple of kTile: every tile is full (T is a multiple of
+//            C) and a checkpoint falls on a tile end or nowhere;
+//   kCkHalf  C == kTile / 2 (the reference's 16) and T a multiple of kTile:
+//            full tiles, checkpoints after steps kTile/2 - 1 and kTile - 1;
+//   kCkAny   anything else: the last tile may be partial and a checkpoint may
+//            fall on any step (stored directly, uncoalesced).
+// In the first two modes the steps of a tile form one branch-free block and
+// checkpoints go out through an LDS transpose at the tile end.
+enum CkMode { kCkAny = 0, kCkTile = 1, kCkHalf = 2 };
+
+template <typename Tin, int kMode>
 __global__ __launch_bounds__(kThreads) void wkv7_fwd_kernel(FwdParams<Tin> p) {
   constexpr int kRow = kHead * sizeof(Tin);   // bytes of one raw row
   constexpr int kRawBytes = V_COUNT * kTile * kRow;
-  __shared__ float4 tile[L_COUNT][kTile][16];   // 28 KiB
-  __shared__ float ost[2][kTile][kHead];        // 8 KiB: y, sa
-  __shared__ float4 raw[kRawBytes / 16];        // 12 or 24 KiB
+  constexpr bool kFull = kMode != kCkAny;       // every tile full, no partial steps
+  constexpr int kCkStage = kMode == kCkHalf ? 2 : kMode == kCkTile ? 1 : 0;
+  constexpr int kCkPitch = kHead + 4;           // floats per staged row (16-byte aligned)
+  __shared__ float4 tile[L_COUNT][kTile][16];   // 56 KiB
+  __shared__ float ost[2][kTile][kHead];        // 16 KiB: y, sa
+  __shared__ float4 raw[kRawBytes / 16];        // 24 or 48 KiB
+  __shared__ float ckst[kCkStage > 0 ? kCkStage : 1][kHead][kCkPitch];   // key-major staging
 
   const int h = blockIdx.x, bi = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63;
   const int L = tid & 15, q = tid >> 4;   // columns 4L.., row pair 2q, 2q+1
   const int up = (L >> 3) & 1;
   const int ro = 2 * q + up, rt = 2 * q + 1 - up;   // own and other row
-  // conversion: the decay of elements 2e, 2e+1 (e = tid % 32) of timestep
-  // tid / 32, then half cg widens the other operands' elements 4pp .. 4pp+3 of
-  // timestep sl; flush: the same (cg, sl, pp)
+  // conversion: the decay of elements 2e, 2e+1 (e = tid % 32) of timesteps
+  // tid / 32 + 16 u, then half cg widens the other operands' elements
+  // 4pp .. 4pp+3 of timesteps sl + 16 u; flush: the same (cg, sl + 16 u, pp)
   const int cg = tid >> 8, sl = (tid >> 4) & 15, pp = tid & 15;
+  static_assert(kTile % 16 == 0, "tile passes cover 16 timesteps");
 
   const int T = p.T, C = p.C;
   const int64_t bh = (int64_t)bi * p.H + h;
@@ -103,8 +117,9 @@ __global__ __launch_bounds__(kThreads) void wkv7_fwd_kernel(FwdParams<Tin> p) {
   // raw tile -> fp32 vectors; the decay w~ is formed here, once per element
   auto convert = [&](int nst) {
     const char* rb = reinterpret_cast<const char*>(raw);
-    {   // w -> w~, two elements per thread
-      const int ws_ = tid >> 5, e = tid & 31;
+#pragma unroll
+    for (int u = 0; u < kTile / 16; ++u) {   // w -> w~, two elements per thread and pass
+      const int ws_ = (tid >> 5) + 16 * u, e = tid & 31;
       if (ws_ < nst) {
         float2 x;
         if constexpr (sizeof(Tin) == 2) {
@@ -117,20 +132,24 @@ __global__ __launch_bounds__(kThreads) void wkv7_fwd_kernel(FwdParams<Tin> p) {
             make_float2(decay_f(sigmoid_f(x.x)), decay_f(sigmoid_f(x.y)));
       }
     }
-    if (sl >= nst) return;
-    auto rawv = [&](int vec) {
-      return io::widen(*reinterpret_cast<const typename io::raw*>(
-          rb + (vec * kTile + sl) * kRow + 4 * pp * sizeof(Tin)));
-    };
-    if (cg == 0) {
-      tile[L_R][sl][pp] = rawv(V_R);
-      tile[L_K][sl][pp] = rawv(V_K);
-    } else {
-      const float4 v = rawv(V_V);
-      tile[L_V][sl][pp] = v;
-      tile[L_VS][sl][pp] = make_float4(v.y, v.x, v.w, v.z);
-      tile[L_A][sl][pp] = rawv(V_A);
-      tile[L_B][sl][pp] = rawv(V_B);
+#pragma unroll
+    for (int u = 0; u < kTile / 16; ++u) {
+      const int st = sl + 16 * u;
+      if (st >= nst) break;
+      auto rawv = [&](int vec) {
+        return io::widen(*reinterpret_cast<const typename io::raw*>(
+            rb + (vec * kTile + st) * kRow + 4 * pp * sizeof(Tin)));
+      };
+      if (cg == 0) {
+        tile[L_R][st][pp] = rawv(V_R);
+        tile[L_K][st][pp] = rawv(V_K);
+      } else {
+        const float4 v = rawv(V_V);
+        tile[L_V][st][pp] = v;
+        tile[L_VS][st][pp] = make_float4(v.y, v.x, v.w, v.z);
+        tile[L_A][st][pp] = rawv(V_A);
+        tile[L_B][st][pp] = rawv(V_B);
+      }
     }
   };
   // (own, other) rows of v for this thread, per step: 32 float2 per step row
@@ -138,14 +157,34 @@ __global__ __launch_bounds__(kThreads) void wkv7_fwd_kernel(FwdParams<Tin> p) {
 
   // checkpoint c: S after step c*C + C - 1, stored key-major ([i][j]); the
   // thread writes (S[2q][i], S[2q+1][i]) for its four columns i
-  float* ckpt_bh = p.ckpt + (bh * (T / C) * kHead + 4 * L) * kHead + 2 * q;
+  float* ckpt_h = p.ckpt + bh * (T / C) * (kHead * kHead);
   auto ck_store = [&](int64_t c) {
-    float* dst = ckpt_bh + c * (kHead * kHead);
+    float* dst = ckpt_h + c * (kHead * kHead) + 4 * L * kHead + 2 * q;
 #pragma unroll
     for (int m = 0; m < 4; ++m)
       *reinterpret_cast<float2*>(dst + m * kHead) =
           up ? make_float2(St[m], So[m]) : make_float2(So[m], St[m]);
   };
+  // the same through LDS: stage the thread's block key-major, then (after a
+  // barrier) every thread writes two 16-byte pieces of full rows
+  auto ck_stage = [&](int b, const float* o, const float* t) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      ckst[b][4 * L + m][ro] = o[m];
+      ckst[b][4 * L + m][rt] = t[m];
+    }
+  };
+  auto ck_flush = [&](int b, int64_t c) {
+    float* dst = ckpt_h + c * (kHead * kHead);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int e = tid + u * kThreads;    // float4 index in the 64x64 checkpoint
+      const int i = e >> 4, j4 = (e & 15) * 4;
+      *reinterpret_cast<float4*>(dst + i * kHead + j4) =
+          *reinterpret_cast<const float4*>(&ckst[b][i][j4]);
+    }
+  };
+  float Co[4], Ct[4];   // state after step kTile/2 - 1 (kCkHalf)
   int until_ckpt = C;   // steps until the next checkpoint (unaligned C)
   int64_t chunk = 0;
 
@@ -172,7 +211,7 @@ __global__ __launch_bounds__(kThreads) void wkv7_fwd_kernel(FwdParams<Tin> p) {
     float sav[kTile];   // sa of the own row
 #pragma unroll
     for (int s = 0; s < kTile; ++s) {
-      if constexpr (!kAligned) {
+      if constexpr (!kFull) {
         if (s >= nst) {   // uniform: the last tile may be partial
           yp[s] = yp[kTile + s] = sav[s] = 0.0f;
           continue;
@@ -181,21 +220,32 @@ __global__ __launch_bounds__(kThreads) void wkv7_fwd_kernel(FwdParams<Tin> p) {
       float sa_t;
       fwd_step(So, St, tile[L_W][s][L], tile[L_A][s][L], tile[L_B][s][L], tile[L_K][s][L],
                tile[L_R][s][L], vrow[s * 32], sav[s], sa_t, yp[s], yp[kTile + s]);
-      if constexpr (!kAligned) {
+      if constexpr (kMode == kCkAny) {
         if (--until_ckpt == 0) {   // (t + 1) % C == 0, kernel.rs:89-102
           until_ckpt = C;
           ck_store(chunk++);
         }
       }
+      if constexpr (kMode == kCkHalf) {
+        if (s == kTile / 2 - 1) {
+#pragma unroll
+          for (int m = 0; m < 4; ++m) { Co[m] = So[m]; Ct[m] = St[m]; }
+        }
+      }
     }
     // y of the own row for steps 2(L&7) and 2(L&7)+1
     row16_reduce_scatter<2 * kTile>(yp, L);
-    ost[0][2 * (L & 7)][ro] = yp[0];
-    ost[0][2 * (L & 7) + 1][ro] = yp[1];
+    // y of the own row for steps kTile/8 * (L&7) ..
+#pragma unroll
+    for (int u = 0; u < kTile / 8; ++u) ost[0][kTile / 8 * (L & 7) + u][ro] = yp[u];
     if ((L & 7) == 0) {
 #pragma unroll
       for (int s = 0; s < kTile; ++s) ost[1][s][ro] = sav[s];
     }
+    // checkpoints (kernel.rs:89-102) of this tile into the staging buffer
+    const bool ck_end = kMode == kCkHalf || (kMode == kCkTile && (t0 + kTile) % C == 0);
+    if constexpr (kMode == kCkHalf) ck_stage(1, Co, Ct);
+    if (kMode != kCkAny && ck_end) ck_stage(0, So, St);
 
     // The loads of tile ti+1 have landed once vmcnt reaches 0 (they and the
     // stores of the previous tile end were issued a whole tile ago). Only LDS
@@ -203,14 +253,17 @@ __global__ __launch_bounds__(kThreads) void wkv7_fwd_kernel(FwdParams<Tin> p) {
     // the next tile end.
     __builtin_amdgcn_s_waitcnt(0);
     lds_barrier();
-    if constexpr (kAligned) {
-      if ((t0 + kTile) % C == 0) ck_store((t0 + kTile) / C - 1);   // kernel.rs:89-102
-    }
-    if (sl < nst) {   // cg 0 writes y, cg 1 writes sa
-      const int64_t off = tok0 + (int64_t)(t0 + sl) * tstride + 4 * pp;
-      const float4 x = reinterpret_cast<const float4*>(ost[cg][sl])[pp];
-      if (cg == 0) io::store(p.y + off, x);
-      else *reinterpret_cast<float4*>(p.sa + off) = x;
+    if constexpr (kMode == kCkHalf) ck_flush(1, (t0 + kTile) / C - 2);
+    if (kMode != kCkAny && ck_end) ck_flush(0, (t0 + kTile) / C - 1);
+#pragma unroll
+    for (int u = 0; u < kTile / 16; ++u) {   // cg 0 writes y, cg 1 writes sa
+      const int st = sl + 16 * u;
+      if (st < nst) {
+        const int64_t off = tok0 + (int64_t)(t0 + st) * tstride + 4 * pp;
+        const float4 x = reinterpret_cast<const float4*>(ost[cg][st])[pp];
+        if (cg == 0) io::store(p.y + off, x);
+        else *reinterpret_cast<float4*>(p.sa + off) = x;
+      }
     }
     if (ti + 1 < ntiles) convert(tile_n(ti + 1));
     lds_barrier();   // converted tile visible; `raw` free for the next loads
@@ -243,9 +296,11 @@ hipError_t launch_fwd_t(const ForwardDesc& d, hipStream_t stream) {
   p.C = d.C;
   const dim3 grid(d.H, d.B, 1), block(kThreads, 1, 1);
   if (d.C % kTile == 0)
-    hipLaunchKernelGGL((wkv7_fwd_kernel<Tin, true>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((wkv7_fwd_kernel<Tin, kCkTile>), grid, block, 0, stream, p);
+  else if (d.C == kTile / 2 && d.T % kTile == 0)
+    hipLaunchKernelGGL((wkv7_fwd_kernel<Tin, kCkHalf>), grid, block, 0, stream, p);
   else
-    hipLaunchKernelGGL((wkv7_fwd_kernel<Tin, false>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((wkv7_fwd_kernel<Tin, kCkAny>), grid, block, 0, stream, p);
   return hipGetLastError();
 }
 
