@@ -32,15 +32,19 @@
 // The only data exchanged between waves is dsa (64 floats, needed by the
 // column role): one LDS vector and one barrier per step. dsa is the only sum
 // on the step-to-step dependency chain; the twelve per-step partial sums of
-// the six gradients stay in registers for the 8 steps of a tile and are
-// reduced in one batch at the tile end.
+// the six gradients stay in registers for 8 steps and are reduced in one
+// batch.
 #include "wkv7_device.hpp"
 #include "wkv7_launch.hpp"
 
 namespace wkv7 {
 namespace {
 
-constexpr int kTile = 8;   // timesteps per LDS tile
+// Timesteps per LDS tile: 16 for bf16 operands, 8 for fp32 ones (whose raw
+// rows and staged gradients take twice the LDS). The gradient partials are
+// reduced in batches of kHalf steps (96 values per lane).
+template <typename Tin> constexpr int tile_len() { return sizeof(Tin) == 2 ? 16 : 8; }
+constexpr int kHalf = 8;
 
 // fp32 LDS vectors per timestep (64 entries)
 enum {
@@ -84,14 +88,16 @@ struct BwdParams {
 // any step.
 template <typename Tin, bool kCkTiled>
 __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
+  constexpr int kTile = tile_len<Tin>();
   constexpr int kRow = kHead * sizeof(Tin);                // bytes of one raw row
   constexpr int kRawBytes = R_COUNT * kTile * kRow + kTile * kHead * 4;
-  constexpr int kParts = 2 * O_COUNT * kTile;              // partial sums per tile
-  __shared__ float4 tile[V_COUNT][kTile][16];              // 20 KiB
-  __shared__ float4 pairs[2][P_COUNT][kTile][32];          // 24 KiB: plain, swapped
-  __shared__ float ost[O_COUNT][kTile][kHead];             // 12 KiB
+  constexpr int kParts = 2 * O_COUNT * kHalf;              // partial sums per batch
+  __shared__ float4 tile[V_COUNT][kTile][16];              // 20 KiB per 8 steps
+  __shared__ float4 pairs[2][P_COUNT][kTile][32];          // 24 KiB per 8 steps: plain, swapped
+  // total for bf16 (16 steps): 40 + 48 + 12 + 32 + 18 + 2.5 KiB; fp32 (8): 20 + 24 + 12 + 32 + 16 + 2.5
+  __shared__ Tin ost[O_COUNT][kTile][kHead];               // gradients in the output dtype
   __shared__ float4 ckbuf[2][kHead * kHead / 4];           // 32 KiB, by tile parity
-  __shared__ float4 raw[kRawBytes / 16];                   // 9 or 16 KiB
+  __shared__ float4 raw[kRawBytes / 16];                   // 18 (bf16) or 16 (fp32) KiB
   __shared__ float dsab[2][kHead];                         // dsa of the step, by parity
   __shared__ float dump[kThreads];                         // sink of unselected lanes
 
@@ -100,9 +106,10 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
   const int L = tid & 15, q = tid >> 4;
   const int up = (L >> 3) & 1;
   const int ro = 2 * q + up, rt = 2 * q + 1 - up;   // own and other row / column
-  // conversion: the decay of element e = tid % 64 of timestep tid / 64, then
-  // group sg = tid / 128 (0: r, k; 1: b, a; 2: dy, v, sa; 3: none) widens
-  // elements 4pp .. 4pp+3 of timestep sl; flush: the same (sl, pp)
+  // conversion: the decay of element pair 2e, 2e+1 (e = tid % 32) of
+  // timesteps tid / 32 + 16u, then group sg = tid / 128 (0: r, k; 1: b, a;
+  // 2: dy, v, sa; 3: none) widens elements 4pp .. 4pp+3 of timesteps
+  // sl + 8u; flush: the same (sl, pp)
   const int sg = tid >> 7, sl = (tid >> 4) & 7, pp = tid & 15;
 
   const int T = p.T, C = p.C;
@@ -113,27 +120,39 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
   const float* ckpt_bh = p.ckpt + bh * nchunks * (kHead * kHead);
   auto ck_needed = [&](int t0, int nst) { return kCkTiled && ((t0 + nst) % C) == 0; };
 
+  // Loads of one tile: 16-byte chunk c0 + lane of `raw` for c0 = wave base +
+  // kThreads * j. The source of a chunk moves by a whole number of timesteps
+  // from tile to tile, so its address at timestep 0 and its timestep within
+  // the tile are computed once here.
+  constexpr int kChunksTok = R_COUNT * kTile * kRow / 16;
+  constexpr int kChunks = kRawBytes / 16;
+  constexpr int kIssue = (kChunks + kThreads - 1) / kThreads;
+  const char* isrc[kIssue];
+  int istep[kIssue];
+#pragma unroll
+  for (int j = 0; j < kIssue; ++j) {
+    const int c0 = tid - lane + kThreads * j, c = c0 + lane;
+    if (c0 < kChunksTok) {
+      const int row = c / (kRow / 16), col = c % (kRow / 16);
+      istep[j] = row % kTile;
+      const Tin* base = p.in[__builtin_amdgcn_readfirstlane(c0 / (kRow / 16)) / kTile];
+      isrc[j] = reinterpret_cast<const char*>(base + tok0 + (int64_t)istep[j] * tstride) + 16 * col;
+    } else {
+      const int cc = c - kChunksTok;
+      istep[j] = cc / 16;
+      isrc[j] = reinterpret_cast<const char*>(p.sa + tok0 + (int64_t)istep[j] * tstride) + 16 * (cc % 16);
+    }
+  }
   // Issue the loads of tile [t0, t0+nst) into `raw` (and its checkpoint into
   // ckbuf[par]); they complete while another tile is computed.
   auto issue = [&](int t0, int nst, int par) {
-    constexpr int kChunksTok = R_COUNT * kTile * kRow / 16;
-    constexpr int kChunks = kRawBytes / 16;
-    for (int c0 = tid - lane; c0 < kChunks; c0 += kThreads) {   // wave-uniform loop
-      const int c = c0 + lane;
-      const int wrow = __builtin_amdgcn_readfirstlane(c0 < kChunksTok ? c0 / (kRow / 16) : 0);
-      const char* src;
-      int step;
-      if (c0 < kChunksTok) {
-        const int row = c / (kRow / 16), col = c % (kRow / 16);
-        step = row % kTile;
-        const Tin* base = p.in[wrow / kTile];   // one operand per wave-load (uniform)
-        src = reinterpret_cast<const char*>(base + tok0 + (int64_t)(t0 + step) * tstride) + 16 * col;
-      } else {
-        const int cc = c - kChunksTok;
-        step = cc / 16;
-        src = reinterpret_cast<const char*>(p.sa + tok0 + (int64_t)(t0 + step) * tstride) + 16 * (cc % 16);
-      }
-      if (step < nst) load_lds16(src, &raw[c0]);
+    const int64_t shift = (int64_t)t0 * tstride * (int64_t)sizeof(Tin);   // bytes, uniform
+    const int64_t shift_sa = (int64_t)t0 * tstride * 4;
+#pragma unroll
+    for (int j = 0; j < kIssue; ++j) {
+      const int c0 = tid - lane + kThreads * j;
+      if (c0 < kChunks && (kCkTiled || istep[j] < nst))
+        load_lds16(isrc[j] + (c0 < kChunksTok ? shift : shift_sa), &raw[c0]);
     }
     if (ck_needed(t0, nst)) {
       const float4* src = reinterpret_cast<const float4*>(
@@ -145,57 +164,66 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
   // raw tile -> fp32 operand vectors and column-pair records (plain, swapped)
   auto convert = [&](int nst) {
     const char* rb = reinterpret_cast<const char*>(raw);
-    {   // w -> w~, 1/w~ and the dw factor, one element per thread
-      const int ws_ = tid >> 6, e = tid & 63;
+#pragma unroll
+    for (int u = 0; u < (kTile + 15) / 16; ++u) {   // w -> w~, 1/w~, dw factor
+      const int ws_ = (tid >> 5) + 16 * u, e = tid & 31;
       if (ws_ < nst) {
-        float x;
-        if constexpr (sizeof(Tin) == 2)
-          x = bf16_to_f32(reinterpret_cast<const bf16_t*>(rb + (R_W * kTile + ws_) * kRow)[e]);
-        else
-          x = reinterpret_cast<const float*>(rb + (R_W * kTile + ws_) * kRow)[e];
-        const float sig = sigmoid_f(x);
-        const float w = decay_f(sig);
-        const float iw = 1.0f / w;
-        reinterpret_cast<float*>(tile[V_W][ws_])[e] = w;
-        reinterpret_cast<float*>(tile[V_DWF][ws_])[e] = kWScale * w * sig * (1.0f - sig);
-        // record {w~[2p], w~[2p+1], iw[2p], iw[2p+1]}, e = 2p + b; swapped copy
-        float* pl = reinterpret_cast<float*>(&pairs[0][P_WI][ws_][e >> 1]);
-        float* sw = reinterpret_cast<float*>(&pairs[1][P_WI][ws_][e >> 1]);
-        const int b = e & 1;
-        pl[b] = w;
-        pl[2 + b] = iw;
-        sw[1 - b] = w;
-        sw[3 - b] = iw;
+        float x[2];
+        if constexpr (sizeof(Tin) == 2) {
+          const uint32_t b2 = reinterpret_cast<const uint32_t*>(rb + (R_W * kTile + ws_) * kRow)[e];
+          x[0] = bf16_to_f32(b2 & 0xffffu);
+          x[1] = bf16_to_f32(b2 >> 16);
+        } else {
+          const float2 f2 = reinterpret_cast<const float2*>(rb + (R_W * kTile + ws_) * kRow)[e];
+          x[0] = f2.x;
+          x[1] = f2.y;
+        }
+        float w[2], iw[2], dwf[2];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+          const float sig = sigmoid_f(x[b]);
+          w[b] = decay_f(sig);
+          iw[b] = 1.0f / w[b];
+          dwf[b] = kWScale * w[b] * sig * (1.0f - sig);
+        }
+        reinterpret_cast<float2*>(tile[V_W][ws_])[e] = make_float2(w[0], w[1]);
+        reinterpret_cast<float2*>(tile[V_DWF][ws_])[e] = make_float2(dwf[0], dwf[1]);
+        pairs[0][P_WI][ws_][e] = make_float4(w[0], w[1], iw[0], iw[1]);
+        pairs[1][P_WI][ws_][e] = make_float4(w[1], w[0], iw[1], iw[0]);
       }
     }
-    if (sl >= nst) return;
-    auto rawv = [&](int vec) {
-      return Io<Tin>::widen(*reinterpret_cast<const typename Io<Tin>::raw*>(
-          rb + (vec * kTile + sl) * kRow + 4 * pp * sizeof(Tin)));
-    };
-    auto put_pairs = [&](int rec, float4 x, float4 y) {
-      pairs[0][rec][sl][2 * pp] = make_float4(x.x, x.y, y.x, y.y);
-      pairs[0][rec][sl][2 * pp + 1] = make_float4(x.z, x.w, y.z, y.w);
-      pairs[1][rec][sl][2 * pp] = make_float4(x.y, x.x, y.y, y.x);
-      pairs[1][rec][sl][2 * pp + 1] = make_float4(x.w, x.z, y.w, y.z);
-    };
-    if (sg == 0) {
-      const float4 r = rawv(R_R), k = rawv(R_K);
-      tile[V_R][sl][pp] = r;
-      tile[V_K][sl][pp] = k;
-      put_pairs(P_RK, r, make_float4(-k.x, -k.y, -k.z, -k.w));
-    } else if (sg == 1) {
-      const float4 b = rawv(R_B), a = rawv(R_A);
-      tile[V_B][sl][pp] = b;
-      tile[V_A][sl][pp] = a;
-      put_pairs(P_BA, make_float4(-b.x, -b.y, -b.z, -b.w), a);
-    } else if (sg == 2) {
-      const float4 dy = rawv(R_DY);
-      tile[V_DY][sl][pp] = dy;
-      tile[V_DYS][sl][pp] = make_float4(dy.y, dy.x, dy.w, dy.z);
-      tile[V_V][sl][pp] = rawv(R_V);
-      tile[V_SA][sl][pp] = *reinterpret_cast<const float4*>(
-          rb + R_COUNT * kTile * kRow + (sl * kHead + 4 * pp) * 4);
+#pragma unroll
+    for (int u = 0; u < kTile / 8; ++u) {
+      const int st = sl + 8 * u;
+      if (st >= nst) break;
+      auto rawv = [&](int vec) {
+        return Io<Tin>::widen(*reinterpret_cast<const typename Io<Tin>::raw*>(
+            rb + (vec * kTile + st) * kRow + 4 * pp * sizeof(Tin)));
+      };
+      auto put_pairs = [&](int rec, float4 x, float4 y) {
+        pairs[0][rec][st][2 * pp] = make_float4(x.x, x.y, y.x, y.y);
+        pairs[0][rec][st][2 * pp + 1] = make_float4(x.z, x.w, y.z, y.w);
+        pairs[1][rec][st][2 * pp] = make_float4(x.y, x.x, y.y, y.x);
+        pairs[1][rec][st][2 * pp + 1] = make_float4(x.w, x.z, y.w, y.z);
+      };
+      if (sg == 0) {
+        const float4 r = rawv(R_R), k = rawv(R_K);
+        tile[V_R][st][pp] = r;
+        tile[V_K][st][pp] = k;
+        put_pairs(P_RK, r, make_float4(-k.x, -k.y, -k.z, -k.w));
+      } else if (sg == 1) {
+        const float4 b = rawv(R_B), a = rawv(R_A);
+        tile[V_B][st][pp] = b;
+        tile[V_A][st][pp] = a;
+        put_pairs(P_BA, make_float4(-b.x, -b.y, -b.z, -b.w), a);
+      } else if (sg == 2) {
+        const float4 dy = rawv(R_DY);
+        tile[V_DY][st][pp] = dy;
+        tile[V_DYS][st][pp] = make_float4(dy.y, dy.x, dy.w, dy.z);
+        tile[V_V][st][pp] = rawv(R_V);
+        tile[V_SA][st][pp] = *reinterpret_cast<const float4*>(
+            rb + R_COUNT * kTile * kRow + (st * kHead + 4 * pp) * 4);
+      }
     }
   };
   // (own, other) rows of dy for the row role: 32 float2 per step row
@@ -306,8 +334,8 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
         dap[d] = c == 0 ? Sc[c][d] * ds[c] : __builtin_fmaf(Sc[c][d], ds[c], dap[d]);
         dSc[c][d] = __builtin_fmaf(ac[d], ds[c], dSc[c][d] * wc[d]);   // kernel.rs:293-294
       }
-    float* po = part + O_COUNT * s;
-    float* pt = part + O_COUNT * (kTile + s);
+    float* po = part + O_COUNT * (s % kHalf);
+    float* pt = part + O_COUNT * (kHalf + s % kHalf);
     po[O_DV] = dvo;     pt[O_DV] = dvt;
     po[O_DR] = drp[0];  pt[O_DR] = drp[1];
     po[O_DW] = dwp[0];  pt[O_DW] = dwp[1];
@@ -345,33 +373,37 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
         reload(ck[(ro * kHead + 4 * L) / 4], ck[(rt * kHead + 4 * L) / 4]);
       }
     }
-    float part[kParts];
 #pragma unroll
-    for (int s = kTile - 1; s >= 0; --s) {
-      if constexpr (!kCkTiled) {
-        if (s >= nst) {   // uniform: the first tile processed may be partial
-#pragma unroll
-          for (int m = 0; m < O_COUNT; ++m) part[O_COUNT * s + m] = part[O_COUNT * (kTile + s) + m] = 0.0f;
-          continue;
+    for (int hb = kTile / kHalf - 1; hb >= 0; --hb) {   // batches of kHalf steps, later first
+      float part[kParts];
+  #pragma unroll
+      for (int s = kHalf * hb + kHalf - 1; s >= kHalf * hb; --s) {
+        if constexpr (!kCkTiled) {
+          if (s >= nst) {   // uniform: the first tile processed may be partial
+  #pragma unroll
+            for (int m = 0; m < O_COUNT; ++m)
+              part[O_COUNT * (s % kHalf) + m] = part[O_COUNT * (kHalf + s % kHalf) + m] = 0.0f;
+            continue;
+          }
+          if (until_reload == 0) {   // (t + 1) % C == 0, kernel.rs:210-228
+            until_reload = C;
+            const float* src = ckpt_bh + reload_chunk * (kHead * kHead) + 4 * L;
+            reload(*reinterpret_cast<const float4*>(src + ro * kHead),
+                   *reinterpret_cast<const float4*>(src + rt * kHead));
+            --reload_chunk;
+          }
+          --until_reload;
         }
-        if (until_reload == 0) {   // (t + 1) % C == 0, kernel.rs:210-228
-          until_reload = C;
-          const float* src = ckpt_bh + reload_chunk * (kHead * kHead) + 4 * L;
-          reload(*reinterpret_cast<const float4*>(src + ro * kHead),
-                 *reinterpret_cast<const float4*>(src + rt * kHead));
-          --reload_chunk;
-        }
-        --until_reload;
+        step(s, (kTile - 1 - s) & 1, part);
       }
-      step(s, (kTile - 1 - s) & 1, part);
+      // the six gradients of own row/column 2q+up at step kHalf*hb + (L&7)
+      row16_reduce_scatter<kParts>(part, L);
+      const int so = kHalf * hb + (L & 7);
+      // dw = W_SCALE * dw~ * w~ * sig * (1 - sig), kernel.rs:267-271
+      part[O_DW] *= reinterpret_cast<const float*>(tile[V_DWF][so])[ro];
+  #pragma unroll
+      for (int m = 0; m < O_COUNT; ++m) Io<Tin>::put1(&ost[m][so][ro], part[m]);
     }
-    // the six gradients of own row/column 2q+up at step L&7 of the tile
-    row16_reduce_scatter<kParts>(part, L);
-    const int so = L & 7;
-    // dw = W_SCALE * dw~ * w~ * sig * (1 - sig), kernel.rs:267-271
-    part[O_DW] *= reinterpret_cast<const float*>(tile[V_DWF][so])[ro];
-#pragma unroll
-    for (int m = 0; m < O_COUNT; ++m) ost[m][so][ro] = part[m];
 
     // The loads of tile ti-1 have landed once vmcnt reaches 0 (they and the
     // stores of the previous tile end were issued a whole tile ago). Only LDS
@@ -379,14 +411,16 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
     // the next tile end.
     __builtin_amdgcn_s_waitcnt(0);
     lds_barrier();
-    if (fg < 3 && sl < nst) {
-      const int64_t off = tok0 + (int64_t)(t0 + sl) * tstride + 4 * pp;
-      const float4 x0 = reinterpret_cast<const float4*>(ost[2 * fg][sl])[pp];
-      const float4 x1 = reinterpret_cast<const float4*>(ost[2 * fg + 1][sl])[pp];
-      Tin* d0 = fg == 0 ? p.dv : fg == 1 ? p.dw : p.db;
-      Tin* d1 = fg == 0 ? p.dr : fg == 1 ? p.dk : p.da;
-      io::store(d0 + off, x0);
-      io::store(d1 + off, x1);
+#pragma unroll
+    for (int u = 0; u < kTile / 8; ++u) {
+      const int st = sl + 8 * u;
+      if (fg < 3 && st < nst) {
+        const int64_t off = tok0 + (int64_t)(t0 + st) * tstride + 4 * pp;
+        Tin* d0 = fg == 0 ? p.dv : fg == 1 ? p.dw : p.db;
+        Tin* d1 = fg == 0 ? p.dr : fg == 1 ? p.dk : p.da;
+        io::copy4(d0 + off, &ost[2 * fg][st][4 * pp]);
+        io::copy4(d1 + off, &ost[2 * fg + 1][st][4 * pp]);
+      }
     }
     if (ti > 0) convert(tile_n(ti - 1));
     lds_barrier();   // converted tile visible; `raw` free for the next loads
@@ -424,7 +458,7 @@ hipError_t launch_bwd_t(const BackwardDesc& d, hipStream_t stream) {
   p.H = d.H;
   p.C = d.C;
   const dim3 grid(d.H, d.B, 1), block(kThreads, 1, 1);
-  if (d.C % kTile == 0)
+  if (d.C % tile_len<Tin>() == 0)
     hipLaunchKernelGGL((wkv7_bwd_kernel<Tin, true>), grid, block, 0, stream, p);
   else
     hipLaunchKernelGGL((wkv7_bwd_kernel<Tin, false>), grid, block, 0, stream, p);

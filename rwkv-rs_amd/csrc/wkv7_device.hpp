@@ -70,6 +70,11 @@ template <> struct Io<float> {
   static __device__ __forceinline__ void store(float* p, float4 x) {
     *reinterpret_cast<float4*>(p) = x;
   }
+  // one value into a staging buffer of this type; 4 staged values to memory
+  static __device__ __forceinline__ void put1(float* p, float x) { *p = x; }
+  static __device__ __forceinline__ void copy4(float* dst, const float* src) {
+    *reinterpret_cast<float4*>(dst) = *reinterpret_cast<const float4*>(src);
+  }
 };
 
 template <> struct Io<bf16_t> {
@@ -86,6 +91,10 @@ template <> struct Io<bf16_t> {
     o.x = f32_to_bf16(x.x) | (f32_to_bf16(x.y) << 16);
     o.y = f32_to_bf16(x.z) | (f32_to_bf16(x.w) << 16);
     *reinterpret_cast<uint2*>(p) = o;
+  }
+  static __device__ __forceinline__ void put1(bf16_t* p, float x) { *p = (bf16_t)f32_to_bf16(x); }
+  static __device__ __forceinline__ void copy4(bf16_t* dst, const bf16_t* src) {
+    *reinterpret_cast<uint2*>(dst) = *reinterpret_cast<const uint2*>(src);
   }
 };
 

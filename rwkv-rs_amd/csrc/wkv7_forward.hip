@@ -100,19 +100,29 @@ __global__ __launch_bounds__(kThreads) void wkv7_fwd_kernel(FwdParams<Tin> p) {
   }
 
   typedef Io<Tin> io;
-  // Issue the loads of tile [t0, t0+nst) into `raw` (row vec*kTile + step).
+  // Loads of one tile: 16-byte chunk c0 + lane of `raw` (row vec*kTile +
+  // step) for c0 = wave base + kThreads * j. The source of a chunk moves by a
+  // whole number of timesteps from tile to tile, so its address at timestep 0
+  // and its timestep within the tile are computed once here.
+  constexpr int kChunks = kRawBytes / 16;
+  constexpr int kIssue = kChunks / kThreads;
+  static_assert(kChunks % kThreads == 0, "every wave issues the same number of loads");
+  const char* isrc[kIssue];
+  int istep[kIssue];
+#pragma unroll
+  for (int j = 0; j < kIssue; ++j) {
+    const int c0 = tid - lane + kThreads * j, c = c0 + lane;
+    const int row = c / (kRow / 16), col = c % (kRow / 16);
+    istep[j] = row % kTile;
+    const Tin* base = p.in[__builtin_amdgcn_readfirstlane(c0 / (kRow / 16)) / kTile];
+    isrc[j] = reinterpret_cast<const char*>(base + tok0 + (int64_t)istep[j] * tstride) + 16 * col;
+  }
+  // Issue the loads of tile [t0, t0+nst) into `raw`.
   auto issue = [&](int t0, int nst) {
-    constexpr int kChunks = kRawBytes / 16;
-    for (int c0 = tid - lane; c0 < kChunks; c0 += kThreads) {   // wave-uniform loop
-      const int c = c0 + lane;
-      const int row = c / (kRow / 16), col = c % (kRow / 16);
-      const int step = row % kTile;
-      const int vec = __builtin_amdgcn_readfirstlane(c0 / (kRow / 16)) / kTile;
-      const Tin* base = p.in[vec];   // kernel-argument array, uniform index
-      const char* src =
-          reinterpret_cast<const char*>(base + tok0 + (int64_t)(t0 + step) * tstride) + 16 * col;
-      if (step < nst) load_lds16(src, &raw[c0]);
-    }
+    const int64_t shift = (int64_t)t0 * tstride * (int64_t)sizeof(Tin);   // bytes, uniform
+#pragma unroll
+    for (int j = 0; j < kIssue; ++j)
+      if (kMode != kCkAny || istep[j] < nst) load_lds16(isrc[j] + shift, &raw[tid - lane + kThreads * j]);
   };
   // raw tile -> fp32 vectors; the decay w~ is formed here, once per element
   auto convert = [&](int nst) {
