@@ -50,8 +50,9 @@ constexpr int kHalf = 8;
 enum {
   V_R = 0, V_K, V_B, V_W, V_A,   // key-indexed: row role
   V_DY, V_V, V_SA,               // value-indexed: column role
-  V_DYS,                         // dy with each row pair swapped (row role, upper half)
   V_DWF,                         // W_SCALE * w~ * sig * (1 - sig)
+  V_DYS,                         // dy with each row pair swapped (row role, upper half);
+                                 // last: it is stored 128 bytes further (see tile_mem)
   V_COUNT
 };
 // per-column-pair records for the column role, float4 {x[2p], x[2p+1],
@@ -92,8 +93,13 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
   constexpr int kRow = kHead * sizeof(Tin);                // bytes of one raw row
   constexpr int kRawBytes = R_COUNT * kTile * kRow + kTile * kHead * 4;
   constexpr int kParts = 2 * O_COUNT * kHalf;              // partial sums per batch
-  __shared__ float4 tile[V_COUNT][kTile][16];              // 20 KiB per 8 steps
-  __shared__ float4 pairs[2][P_COUNT][kTile][32];          // 24 KiB per 8 steps: plain, swapped
+  // The swapped copies (pair records, dy) are read by the upper half-rows in
+  // the same instruction as the plain ones by the lower half-rows; they are
+  // placed 64 / 128 bytes off a 256-byte boundary relative to the plain data,
+  // so the two sets of addresses fall into different LDS banks.
+  constexpr int kPairsCopy = P_COUNT * kTile * 32 + 4;      // float4s per copy (+64 B)
+  __shared__ float4 tile_mem[V_COUNT * kTile * 16 + 8];    // 20 KiB per 8 steps
+  __shared__ float4 pairs_mem[2 * kPairsCopy];             // 24 KiB per 8 steps: plain, swapped
   // total for bf16 (16 steps): 40 + 48 + 12 + 32 + 18 + 2.5 KiB; fp32 (8): 20 + 24 + 12 + 32 + 16 + 2.5
   __shared__ Tin ost[O_COUNT][kTile][kHead];               // gradients in the output dtype
   __shared__ float4 ckbuf[2][kHead * kHead / 4];           // 32 KiB, by tile parity
@@ -101,6 +107,14 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
   __shared__ float dsab[2][kHead];                         // dsa of the step, by parity
   __shared__ float dump[kThreads];                         // sink of unselected lanes
 
+  // row s of LDS vector V (V_DYS sits 128 bytes further, see above)
+  static_assert(V_DYS == V_COUNT - 1, "the shifted vector must be the last one");
+  auto tile = [&](int V, int s) -> float4* {
+    return tile_mem + (V * kTile + s) * 16 + (V == V_DYS ? 8 : 0);
+  };
+  auto pairs = [&](int h, int rec, int s) -> float4* {
+    return pairs_mem + h * kPairsCopy + (rec * kTile + s) * 32;
+  };
   const int h = blockIdx.x, bi = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63;
   const int L = tid & 15, q = tid >> 4;
@@ -186,10 +200,10 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
           iw[b] = 1.0f / w[b];
           dwf[b] = kWScale * w[b] * sig * (1.0f - sig);
         }
-        reinterpret_cast<float2*>(tile[V_W][ws_])[e] = make_float2(w[0], w[1]);
-        reinterpret_cast<float2*>(tile[V_DWF][ws_])[e] = make_float2(dwf[0], dwf[1]);
-        pairs[0][P_WI][ws_][e] = make_float4(w[0], w[1], iw[0], iw[1]);
-        pairs[1][P_WI][ws_][e] = make_float4(w[1], w[0], iw[1], iw[0]);
+        reinterpret_cast<float2*>(tile(V_W, ws_))[e] = make_float2(w[0], w[1]);
+        reinterpret_cast<float2*>(tile(V_DWF, ws_))[e] = make_float2(dwf[0], dwf[1]);
+        pairs(0, P_WI, ws_)[e] = make_float4(w[0], w[1], iw[0], iw[1]);
+        pairs(1, P_WI, ws_)[e] = make_float4(w[1], w[0], iw[1], iw[0]);
       }
     }
 #pragma unroll
@@ -201,34 +215,34 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
             rb + (vec * kTile + st) * kRow + 4 * pp * sizeof(Tin)));
       };
       auto put_pairs = [&](int rec, float4 x, float4 y) {
-        pairs[0][rec][st][2 * pp] = make_float4(x.x, x.y, y.x, y.y);
-        pairs[0][rec][st][2 * pp + 1] = make_float4(x.z, x.w, y.z, y.w);
-        pairs[1][rec][st][2 * pp] = make_float4(x.y, x.x, y.y, y.x);
-        pairs[1][rec][st][2 * pp + 1] = make_float4(x.w, x.z, y.w, y.z);
+        pairs(0, rec, st)[2 * pp] = make_float4(x.x, x.y, y.x, y.y);
+        pairs(0, rec, st)[2 * pp + 1] = make_float4(x.z, x.w, y.z, y.w);
+        pairs(1, rec, st)[2 * pp] = make_float4(x.y, x.x, y.y, y.x);
+        pairs(1, rec, st)[2 * pp + 1] = make_float4(x.w, x.z, y.w, y.z);
       };
       if (sg == 0) {
         const float4 r = rawv(R_R), k = rawv(R_K);
-        tile[V_R][st][pp] = r;
-        tile[V_K][st][pp] = k;
+        tile(V_R, st)[pp] = r;
+        tile(V_K, st)[pp] = k;
         put_pairs(P_RK, r, make_float4(-k.x, -k.y, -k.z, -k.w));
       } else if (sg == 1) {
         const float4 b = rawv(R_B), a = rawv(R_A);
-        tile[V_B][st][pp] = b;
-        tile[V_A][st][pp] = a;
+        tile(V_B, st)[pp] = b;
+        tile(V_A, st)[pp] = a;
         put_pairs(P_BA, make_float4(-b.x, -b.y, -b.z, -b.w), a);
       } else if (sg == 2) {
         const float4 dy = rawv(R_DY);
-        tile[V_DY][st][pp] = dy;
-        tile[V_DYS][st][pp] = make_float4(dy.y, dy.x, dy.w, dy.z);
-        tile[V_V][st][pp] = rawv(R_V);
-        tile[V_SA][st][pp] = *reinterpret_cast<const float4*>(
+        tile(V_DY, st)[pp] = dy;
+        tile(V_DYS, st)[pp] = make_float4(dy.y, dy.x, dy.w, dy.z);
+        tile(V_V, st)[pp] = rawv(R_V);
+        tile(V_SA, st)[pp] = *reinterpret_cast<const float4*>(
             rb + R_COUNT * kTile * kRow + (st * kHead + 4 * pp) * 4);
       }
     }
   };
   // (own, other) rows of dy for the row role: 32 float2 per step row
-  const float2* dyrow = reinterpret_cast<const float2*>(&tile[up ? V_DYS : V_DY][0][0]) + q;
-  const float4(*prec)[kTile][32] = pairs[up];   // this half-row's pair records
+  const float2* dyrow = reinterpret_cast<const float2*>(tile(up ? V_DYS : V_DY, 0)) + q;
+  const float4* prec = pairs_mem + up * kPairsCopy + q;   // this half-row's pair records
 
   float dSo[4], dSt[4], Sc[4][2], dSc[4][2];
 #pragma unroll
@@ -262,9 +276,9 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
   auto step = [&](int s, int par, float* part) {
     // row role: dS row += dy r^T (kernel.rs:248); dv, dsa (kernel.rs:261-262)
     float rr[4], kk[4], bb[4];
-    unpack4(rr, tile[V_R][s][L]);
-    unpack4(kk, tile[V_K][s][L]);
-    unpack4(bb, tile[V_B][s][L]);
+    unpack4(rr, tile(V_R, s)[L]);
+    unpack4(kk, tile(V_K, s)[L]);
+    unpack4(bb, tile(V_B, s)[L]);
     const float2 dyr = dyrow[s * 32];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -289,10 +303,11 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
 
     // column role: dr from S_t; rebuild S_{t-1}; dS col += dy r; dw~, dk, db
     float dy[4], v[4], sa[4];
-    unpack4(dy, tile[V_DY][s][L]);
-    unpack4(v, tile[V_V][s][L]);
-    unpack4(sa, tile[V_SA][s][L]);
-    const float4 prk = prec[P_RK][s][q], pba = prec[P_BA][s][q], pwi = prec[P_WI][s][q];
+    unpack4(dy, tile(V_DY, s)[L]);
+    unpack4(v, tile(V_V, s)[L]);
+    unpack4(sa, tile(V_SA, s)[L]);
+    const float4 prk = prec[(P_RK * kTile + s) * 32], pba = prec[(P_BA * kTile + s) * 32];
+    const float4 pwi = prec[(P_WI * kTile + s) * 32];
     const float rc[2] = {prk.x, prk.y}, nkc[2] = {prk.z, prk.w};   // r, -k
     const float nbc[2] = {pba.x, pba.y}, ac[2] = {pba.z, pba.w};   // -b, a
     const float wc[2] = {pwi.x, pwi.y}, iwc[2] = {pwi.z, pwi.w};
@@ -318,8 +333,8 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
 
     // row role: dS row = dS row * w~ + dsa a^T (kernel.rs:290-291)
     float ww[4], aa[4];
-    unpack4(ww, tile[V_W][s][L]);
-    unpack4(aa, tile[V_A][s][L]);
+    unpack4(ww, tile(V_W, s)[L]);
+    unpack4(aa, tile(V_A, s)[L]);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       dSo[c] = __builtin_fmaf(dsa_o, aa[c], dSo[c] * ww[c]);
@@ -373,14 +388,26 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
         reload(ck[(ro * kHead + 4 * L) / 4], ck[(rt * kHead + 4 * L) / 4]);
       }
     }
+    // the six gradients of own row/column 2q+up at step kHalf*hb + (L&7) of
+    // a batch, from its reduce-scatter
+    auto stage = [&](float* part, int hb) {
+      const int so = kHalf * hb + (L & 7);
+      // dw = W_SCALE * dw~ * w~ * sig * (1 - sig), kernel.rs:267-271
+      part[O_DW] *= reinterpret_cast<const float*>(tile(V_DWF, so))[ro];
 #pragma unroll
-    for (int hb = kTile / kHalf - 1; hb >= 0; --hb) {   // batches of kHalf steps, later first
+      for (int m = 0; m < O_COUNT; ++m) Io<Tin>::put1(&ost[m][so][ro], part[m]);
+    };
+    // batches of kHalf steps, later first; the reduce-scatter of a batch runs
+    // one level per step during the first steps of the next batch of the tile
+    float prev[kParts];
+#pragma unroll
+    for (int hb = kTile / kHalf - 1; hb >= 0; --hb) {
       float part[kParts];
-  #pragma unroll
+#pragma unroll
       for (int s = kHalf * hb + kHalf - 1; s >= kHalf * hb; --s) {
         if constexpr (!kCkTiled) {
           if (s >= nst) {   // uniform: the first tile processed may be partial
-  #pragma unroll
+#pragma unroll
             for (int m = 0; m < O_COUNT; ++m)
               part[O_COUNT * (s % kHalf) + m] = part[O_COUNT * (kHalf + s % kHalf) + m] = 0.0f;
             continue;
@@ -395,14 +422,24 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
           --until_reload;
         }
         step(s, (kTile - 1 - s) & 1, part);
+        if (hb + 1 < kTile / kHalf) {   // the previous batch, one level per step
+          const int k = kHalf * hb + kHalf - 1 - s;
+          if (k == 0) row16_rs_level<kParts, 0>(prev, L);
+          if (k == 1) row16_rs_level<kParts, 1>(prev, L);
+          if (k == 2) row16_rs_level<kParts, 2>(prev, L);
+          if (k == 3) {
+            row16_rs_level<kParts, 3>(prev, L);
+            stage(prev, hb + 1);
+          }
+        }
       }
-      // the six gradients of own row/column 2q+up at step kHalf*hb + (L&7)
-      row16_reduce_scatter<kParts>(part, L);
-      const int so = kHalf * hb + (L & 7);
-      // dw = W_SCALE * dw~ * w~ * sig * (1 - sig), kernel.rs:267-271
-      part[O_DW] *= reinterpret_cast<const float*>(tile[V_DWF][so])[ro];
-  #pragma unroll
-      for (int m = 0; m < O_COUNT; ++m) Io<Tin>::put1(&ost[m][so][ro], part[m]);
+      if (hb > 0) {
+#pragma unroll
+        for (int j = 0; j < kParts; ++j) prev[j] = part[j];
+      } else {
+        row16_reduce_scatter<kParts>(part, L);
+        stage(part, 0);
+      }
     }
 
     // The loads of tile ti-1 have landed once vmcnt reaches 0 (they and the

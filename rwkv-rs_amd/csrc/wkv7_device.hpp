@@ -150,14 +150,29 @@ __device__ __forceinline__ void row_pair_sum(float& own, float& other) {
 // values (L & 7) * N/16 .. (L & 7) * N/16 + N/16 - 1 (of the lane's own row).
 // The first level is select-free (see row_pair_sum); the three levels inside
 // an 8-lane half use rs_step.
+// Level `lv` (0..3) of row16_reduce_scatter alone, so that the levels of one
+// batch can be spread over independent work.
+template <int N, int lv>
+__device__ __forceinline__ void row16_rs_level(float* x, int L) {
+  static_assert(N % 16 == 0, "N must be a multiple of 16");
+  if constexpr (lv == 0) {
+#pragma unroll
+    for (int j = 0; j < N / 2; ++j) x[j] += dpp_mov<kDppRor8>(x[N / 2 + j]);
+  } else if constexpr (lv == 1) {
+    rs_step<kDppHalfMirror, N / 2>(x, (L & 4) != 0);
+  } else if constexpr (lv == 2) {
+    rs_step<kDppQuadSwap2, N / 4>(x, (L & 2) != 0);
+  } else {
+    rs_step<kDppQuadSwap1, N / 8>(x, (L & 1) != 0);
+  }
+}
+
 template <int N>
 __device__ __forceinline__ void row16_reduce_scatter(float* x, int L) {
-  static_assert(N % 16 == 0, "N must be a multiple of 16");
-#pragma unroll
-  for (int j = 0; j < N / 2; ++j) x[j] += dpp_mov<kDppRor8>(x[N / 2 + j]);
-  rs_step<kDppHalfMirror, N / 2>(x, (L & 4) != 0);
-  rs_step<kDppQuadSwap2, N / 4>(x, (L & 2) != 0);
-  rs_step<kDppQuadSwap1, N / 8>(x, (L & 1) != 0);
+  row16_rs_level<N, 0>(x, L);
+  row16_rs_level<N, 1>(x, L);
+  row16_rs_level<N, 2>(x, L);
+  row16_rs_level<N, 3>(x, L);
 }
 
 // ---------------------------------------------------------- direct LDS loads

@@ -66,11 +66,19 @@ __global__ __launch_bounds__(kThreads) void wkv7_fwd_kernel(FwdParams<Tin> p) {
   constexpr bool kFull = kMode != kCkAny;       // every tile full, no partial steps
   constexpr int kCkStage = kMode == kCkHalf ? 2 : kMode == kCkTile ? 1 : 0;
   constexpr int kCkPitch = kHead + 4;           // floats per staged row (16-byte aligned)
-  __shared__ float4 tile[L_COUNT][kTile][16];   // 56 KiB
+  // The swapped copy of v is read by the upper half-rows in the same
+  // instruction as the plain one by the lower half-rows; it sits 128 bytes off
+  // a 256-byte boundary relative to it, so the two fall into different banks.
+  __shared__ float4 tile_mem[L_COUNT * kTile * 16 + 8];   // 56 KiB
   __shared__ float ost[2][kTile][kHead];        // 16 KiB: y, sa
   __shared__ float4 raw[kRawBytes / 16];        // 24 or 48 KiB
   __shared__ float ckst[kCkStage > 0 ? kCkStage : 1][kHead][kCkPitch];   // key-major staging
 
+  // row s of LDS vector V
+  static_assert(L_VS == L_COUNT - 1, "the shifted vector must be the last one");
+  auto tile = [&](int V, int s) -> float4* {
+    return tile_mem + (V * kTile + s) * 16 + (V == L_VS ? 8 : 0);
+  };
   const int h = blockIdx.x, bi = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63;
   const int L = tid & 15, q = tid >> 4;   // columns 4L.., row pair 2q, 2q+1
@@ -138,7 +146,7 @@ __global__ __launch_bounds__(kThreads) void wkv7_fwd_kernel(FwdParams<Tin> p) {
         } else {
           x = reinterpret_cast<const float2*>(rb + (V_W * kTile + ws_) * kRow)[e];
         }
-        reinterpret_cast<float2*>(tile[L_W][ws_])[e] =
+        reinterpret_cast<float2*>(tile(L_W, ws_))[e] =
             make_float2(decay_f(sigmoid_f(x.x)), decay_f(sigmoid_f(x.y)));
       }
     }
@@ -151,19 +159,19 @@ __global__ __launch_bounds__(kThreads) void wkv7_fwd_kernel(FwdParams<Tin> p) {
             rb + (vec * kTile + st) * kRow + 4 * pp * sizeof(Tin)));
       };
       if (cg == 0) {
-        tile[L_R][st][pp] = rawv(V_R);
-        tile[L_K][st][pp] = rawv(V_K);
+        tile(L_R, st)[pp] = rawv(V_R);
+        tile(L_K, st)[pp] = rawv(V_K);
       } else {
         const float4 v = rawv(V_V);
-        tile[L_V][st][pp] = v;
-        tile[L_VS][st][pp] = make_float4(v.y, v.x, v.w, v.z);
-        tile[L_A][st][pp] = rawv(V_A);
-        tile[L_B][st][pp] = rawv(V_B);
+        tile(L_V, st)[pp] = v;
+        tile(L_VS, st)[pp] = make_float4(v.y, v.x, v.w, v.z);
+        tile(L_A, st)[pp] = rawv(V_A);
+        tile(L_B, st)[pp] = rawv(V_B);
       }
     }
   };
   // (own, other) rows of v for this thread, per step: 32 float2 per step row
-  const float2* vrow = reinterpret_cast<const float2*>(&tile[up ? L_VS : L_V][0][0]) + q;
+  const float2* vrow = reinterpret_cast<const float2*>(tile(up ? L_VS : L_V, 0)) + q;
 
   // checkpoint c: S after step c*C + C - 1, stored key-major ([i][j]); the
   // thread writes (S[2q][i], S[2q+1][i]) for its four columns i
@@ -228,8 +236,8 @@ __global__ __launch_bounds__(kThreads) void wkv7_fwd_kernel(FwdParams<Tin> p) {
         }
       }
       float sa_t;
-      fwd_step(So, St, tile[L_W][s][L], tile[L_A][s][L], tile[L_B][s][L], tile[L_K][s][L],
-               tile[L_R][s][L], vrow[s * 32], sav[s], sa_t, yp[s], yp[kTile + s]);
+      fwd_step(So, St, tile(L_W, s)[L], tile(L_A, s)[L], tile(L_B, s)[L], tile(L_K, s)[L],
+               tile(L_R, s)[L], vrow[s * 32], sav[s], sa_t, yp[s], yp[kTile + s]);
       if constexpr (kMode == kCkAny) {
         if (--until_ckpt == 0) {   // (t + 1) % C == 0, kernel.rs:89-102
           until_ckpt = C;
