@@ -104,8 +104,8 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
   __shared__ Tin ost[O_COUNT][kTile][kHead];               // gradients in the output dtype
   __shared__ float4 ckbuf[2][kHead * kHead / 4];           // 32 KiB, by tile parity
   __shared__ float4 raw[kRawBytes / 16];                   // 18 (bf16) or 16 (fp32) KiB
-  __shared__ float dsab[2][kHead];                         // dsa of the step, by parity
-  __shared__ float dump[kThreads];                         // sink of unselected lanes
+  __shared__ float dsab[2][kHalf][kHead];                  // dsa of a batch, by batch parity
+  __shared__ float dump[64];                               // sink of unselected lanes
 
   // row s of LDS vector V (V_DYS sits 128 bytes further, see above)
   static_assert(V_DYS == V_COUNT - 1, "the shifted vector must be the last one");
@@ -271,14 +271,20 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
   int until_reload = 0;   // steps until the next checkpoint reload (unaligned C)
   int64_t reload_chunk = nchunks - 1;
 
-  // One timestep (kernel.rs:177-297) of tile row s; its twelve partial sums
-  // go to part[] as [own block | other block], six per step each.
-  auto step = [&](int s, int par, float* part) {
-    // row role: dS row += dy r^T (kernel.rs:248); dv, dsa (kernel.rs:261-262)
-    float rr[4], kk[4], bb[4];
+  // The two roles of one timestep (kernel.rs:177-297). The row role needs
+  // dsa of its own two rows only, which it sums itself, so it runs a batch of
+  // kHalf steps ahead of the column role: it publishes dsa of every step of
+  // the batch in dsab[buf], one barrier follows, and the column role reads
+  // them. Partial sums go to part[] as [own block | other block], six per
+  // step each (the row role's dv to dvp[] first).
+  auto row_step = [&](int s, int buf, float* dvp) {
+    // dS row += dy r^T (kernel.rs:248); dv, dsa (kernel.rs:261-262)
+    float rr[4], kk[4], bb[4], ww[4], aa[4];
     unpack4(rr, tile(V_R, s)[L]);
     unpack4(kk, tile(V_K, s)[L]);
     unpack4(bb, tile(V_B, s)[L]);
+    unpack4(ww, tile(V_W, s)[L]);
+    unpack4(aa, tile(V_A, s)[L]);
     const float2 dyr = dyrow[s * 32];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -298,20 +304,30 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
     }
     row_pair_sum(dsa_o, dsa_t);
     // one lane per half-row publishes dsa of its own row; the others write a
-    // private sink, which keeps the step free of branches
-    *((L & 7) == 0 ? &dsab[par][ro] : &dump[tid]) = dsa_o;
-
-    // column role: dr from S_t; rebuild S_{t-1}; dS col += dy r; dw~, dk, db
-    float dy[4], v[4], sa[4];
+    // sink, which keeps the step free of branches
+    *((L & 7) == 0 ? &dsab[buf][s % kHalf][ro] : &dump[lane]) = dsa_o;
+    // dS row = dS row * w~ + dsa a^T (kernel.rs:290-291)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      dSo[c] = __builtin_fmaf(dsa_o, aa[c], dSo[c] * ww[c]);
+      dSt[c] = __builtin_fmaf(dsa_t, aa[c], dSt[c] * ww[c]);
+    }
+    dvp[2 * (s % kHalf)] = dvo;
+    dvp[2 * (s % kHalf) + 1] = dvt;
+  };
+  auto col_step = [&](int s, int buf, float* part) {
+    // dr from S_t; rebuild S_{t-1}; dS col += dy r; dw~, dk, db
+    float dy[4], v[4], sa[4], ds[4];
     unpack4(dy, tile(V_DY, s)[L]);
     unpack4(v, tile(V_V, s)[L]);
     unpack4(sa, tile(V_SA, s)[L]);
+    unpack4(ds, reinterpret_cast<const float4*>(dsab[buf][s % kHalf])[L]);   // dsa of rows 4L..
     const float4 prk = prec[(P_RK * kTile + s) * 32], pba = prec[(P_BA * kTile + s) * 32];
     const float4 pwi = prec[(P_WI * kTile + s) * 32];
     const float rc[2] = {prk.x, prk.y}, nkc[2] = {prk.z, prk.w};   // r, -k
     const float nbc[2] = {pba.x, pba.y}, ac[2] = {pba.z, pba.w};   // -b, a
     const float wc[2] = {pwi.x, pwi.y}, iwc[2] = {pwi.z, pwi.w};
-    float drp[2], dwp[2], dkp[2], dbp[2];
+    float drp[2], dwp[2], dkp[2], dbp[2], dap[2];
 #pragma unroll
     for (int c = 0; c < 4; ++c)
 #pragma unroll
@@ -325,33 +341,12 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
         dwp[d] = c == 0 ? dSc[c][d] * Sc[c][d] : __builtin_fmaf(dSc[c][d], Sc[c][d], dwp[d]);
         dkp[d] = c == 0 ? dSc[c][d] * v[c] : __builtin_fmaf(dSc[c][d], v[c], dkp[d]);
         dbp[d] = c == 0 ? dSc[c][d] * sa[c] : __builtin_fmaf(dSc[c][d], sa[c], dbp[d]);
-      }
-
-    lds_barrier();   // dsa of every row visible
-    float ds[4];
-    unpack4(ds, reinterpret_cast<const float4*>(dsab[par])[L]);
-
-    // row role: dS row = dS row * w~ + dsa a^T (kernel.rs:290-291)
-    float ww[4], aa[4];
-    unpack4(ww, tile(V_W, s)[L]);
-    unpack4(aa, tile(V_A, s)[L]);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      dSo[c] = __builtin_fmaf(dsa_o, aa[c], dSo[c] * ww[c]);
-      dSt[c] = __builtin_fmaf(dsa_t, aa[c], dSt[c] * ww[c]);
-    }
-    // column role: da = S_{t-1}^T dsa (kernel.rs:280-287); dS col = dS col * w~ + a dsa
-    float dap[2];
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-#pragma unroll
-      for (int d = 0; d < 2; ++d) {
+        // da = S_{t-1}^T dsa (kernel.rs:280-287); dS col = dS col * w~ + a dsa (:293-294)
         dap[d] = c == 0 ? Sc[c][d] * ds[c] : __builtin_fmaf(Sc[c][d], ds[c], dap[d]);
-        dSc[c][d] = __builtin_fmaf(ac[d], ds[c], dSc[c][d] * wc[d]);   // kernel.rs:293-294
+        dSc[c][d] = __builtin_fmaf(ac[d], ds[c], dSc[c][d] * wc[d]);
       }
     float* po = part + O_COUNT * (s % kHalf);
     float* pt = part + O_COUNT * (kHalf + s % kHalf);
-    po[O_DV] = dvo;     pt[O_DV] = dvt;
     po[O_DR] = drp[0];  pt[O_DR] = drp[1];
     po[O_DW] = dwp[0];  pt[O_DW] = dwp[1];
     po[O_DK] = dkp[0];  pt[O_DK] = dkp[1];
@@ -397,49 +392,52 @@ __global__ __launch_bounds__(kThreads) void wkv7_bwd_kernel(BwdParams<Tin> p) {
 #pragma unroll
       for (int m = 0; m < O_COUNT; ++m) Io<Tin>::put1(&ost[m][so][ro], part[m]);
     };
-    // batches of kHalf steps, later first; the reduce-scatter of a batch runs
-    // one level per step during the first steps of the next batch of the tile
-    float prev[kParts];
+    // step guard of the unaligned path: a partial first tile, and the
+    // checkpoint reload at (t + 1) % C == 0 (kernel.rs:210-228)
+    auto live = [&](int s) { return kCkTiled || s < nst; };
+    auto col_reload = [&]() {
+      if constexpr (!kCkTiled) {
+        if (until_reload == 0) {
+          until_reload = C;
+          const float* src = ckpt_bh + reload_chunk * (kHead * kHead) + 4 * L;
+          reload(*reinterpret_cast<const float4*>(src + ro * kHead),
+                 *reinterpret_cast<const float4*>(src + rt * kHead));
+          --reload_chunk;
+        }
+        --until_reload;
+      }
+    };
+    constexpr int kBatches = kTile / kHalf;
+    // Batches run later first. The row role of batch hb runs alone for the
+    // last batch of the tile, and otherwise together with the column role of
+    // batch hb+1 (no dependency between them); one barrier per batch.
+    float dvb[kBatches][2 * kHalf];
 #pragma unroll
-    for (int hb = kTile / kHalf - 1; hb >= 0; --hb) {
+    for (int s = kTile - 1; s >= kTile - kHalf; --s)
+      if (live(s)) row_step(s, (kBatches - 1) & 1, dvb[kBatches - 1]);
+#pragma unroll
+    for (int hb = kBatches - 1; hb >= 0; --hb) {
+      lds_barrier();   // dsa of batch hb visible
       float part[kParts];
 #pragma unroll
-      for (int s = kHalf * hb + kHalf - 1; s >= kHalf * hb; --s) {
-        if constexpr (!kCkTiled) {
-          if (s >= nst) {   // uniform: the first tile processed may be partial
+      for (int k = kHalf - 1; k >= 0; --k) {
+        const int s = kHalf * hb + k;
+        if (live(s)) {
+          col_reload();
+          col_step(s, hb & 1, part);
+        } else {
 #pragma unroll
-            for (int m = 0; m < O_COUNT; ++m)
-              part[O_COUNT * (s % kHalf) + m] = part[O_COUNT * (kHalf + s % kHalf) + m] = 0.0f;
-            continue;
-          }
-          if (until_reload == 0) {   // (t + 1) % C == 0, kernel.rs:210-228
-            until_reload = C;
-            const float* src = ckpt_bh + reload_chunk * (kHead * kHead) + 4 * L;
-            reload(*reinterpret_cast<const float4*>(src + ro * kHead),
-                   *reinterpret_cast<const float4*>(src + rt * kHead));
-            --reload_chunk;
-          }
-          --until_reload;
+          for (int m = 0; m < O_COUNT; ++m) part[O_COUNT * k + m] = part[O_COUNT * (kHalf + k) + m] = 0.0f;
         }
-        step(s, (kTile - 1 - s) & 1, part);
-        if (hb + 1 < kTile / kHalf) {   // the previous batch, one level per step
-          const int k = kHalf * hb + kHalf - 1 - s;
-          if (k == 0) row16_rs_level<kParts, 0>(prev, L);
-          if (k == 1) row16_rs_level<kParts, 1>(prev, L);
-          if (k == 2) row16_rs_level<kParts, 2>(prev, L);
-          if (k == 3) {
-            row16_rs_level<kParts, 3>(prev, L);
-            stage(prev, hb + 1);
-          }
-        }
+        if (hb > 0 && live(s - kHalf)) row_step(s - kHalf, (hb - 1) & 1, dvb[hb - 1]);
       }
-      if (hb > 0) {
 #pragma unroll
-        for (int j = 0; j < kParts; ++j) prev[j] = part[j];
-      } else {
-        row16_reduce_scatter<kParts>(part, L);
-        stage(part, 0);
+      for (int k = 0; k < kHalf; ++k) {
+        part[O_COUNT * k + O_DV] = live(kHalf * hb + k) ? dvb[hb][2 * k] : 0.0f;
+        part[O_COUNT * (kHalf + k) + O_DV] = live(kHalf * hb + k) ? dvb[hb][2 * k + 1] : 0.0f;
       }
+      row16_reduce_scatter<kParts>(part, L);
+      stage(part, hb);
     }
 
     // The loads of tile ti-1 have landed once vmcnt reaches 0 (they and the
