@@ -103,10 +103,19 @@ __device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf
 __device__ __forceinline__ float decay_f(float sig) { return expf(kWScale * sig); }
 
 // ------------------------------------------------------- cross-lane reduction
+// DPP move feeding an add (the compiler fuses the pair into v_add_f32_dpp)
 template <int CTRL>
 __device__ __forceinline__ float dpp_mov(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
       0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+// DPP move whose result is used on its own. Every pattern used here reads a
+// lane of the same row for every lane, so no lane keeps an "old" value and
+// none needs to be materialised.
+template <int CTRL>
+__device__ __forceinline__ float dpp_get(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(
+      __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, true));
 }
 
 // DPP controls used below. row_ror:8 pairs lane L with L ^ 8 (the other half
@@ -140,7 +149,7 @@ __device__ __forceinline__ void row_pair_sum(float& own, float& other) {
   s += dpp_mov<kDppQuadSwap2>(s);
   s += dpp_mov<kDppQuadSwap1>(s);
   own = s;
-  other = dpp_mov<kDppRor8>(s);
+  other = dpp_get<kDppRor8>(s);
 }
 
 // Reduce-scatter over the DPP row of N per-row partial sums (N a multiple of
