@@ -137,7 +137,13 @@ def test_fp32_long_chunks_as_accurate_as_reference(wk, oracle, case):
             assert rel_l2(got, obwd[gn]) <= FP32_TOL, gn
 
 
-@pytest.mark.parametrize("case", [(2, 128, 4, 16, 0.1, 11), (1, 64, 4, 16, None, 12)])
+@pytest.mark.parametrize("case", [
+    (2, 128, 4, 16, 0.1, 11),   # 16-step checkpoints, 32-step forward tiles (two per tile)
+    (1, 64, 4, 16, None, 12),
+    (1, 48, 3, 16, 0.1, 13),    # T not a multiple of 32: partial last forward tile
+    (1, 40, 2, 8, 0.1, 14),     # backward reloads inside a 16-step tile, partial first tile
+    (1, 64, 2, 32, 0.1, 15),    # one checkpoint every 32-step forward tile
+])
 def test_bf16_inputs_fp32_state(wk, oracle, case):
     B, T, H, C, s0_std, seed = case
     announce("bf16 fwd+bwd", case)
