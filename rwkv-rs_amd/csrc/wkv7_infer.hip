@@ -22,7 +22,9 @@
 namespace wkv7 {
 namespace {
 
-constexpr int kTile = 16;
+// Timesteps staged per LDS tile: 16 for prefill; 1 for a single decode step,
+// where the small LDS footprint lets three workgroups share a CU (the step is
+// bound by the HBM latency of its state read, so workgroups in flight count).
 enum { V_W = 0, V_R, V_K, V_V, V_A, V_B, V_COUNT };
 
 
@@ -51,10 +53,10 @@ __device__ __forceinline__ bool mask_on<bf16_t>(const bf16_t* m, int64_t i) {
   return (m[i] & 0x7fffu) != 0u;   // +0 and -0 are "masked"
 }
 
-template <typename Tin>
+template <typename Tin, int kTile>
 __global__ __launch_bounds__(kThreads) void wkv7_infer_kernel(InferParams<Tin> p) {
-  __shared__ float4 tile[2][V_COUNT][kTile][16];   // 48 KiB
-  __shared__ float ost[2][kTile][kHead];           // 8 KiB
+  __shared__ float4 tile[2][V_COUNT][kTile][16];   // 1.5 KiB per step
+  __shared__ float ost[2][kTile][kHead];           // 0.5 KiB per step
   __shared__ int live[2][kTile];                   // step not masked
 
   const int h = blockIdx.x, bi = blockIdx.y;
@@ -197,7 +199,11 @@ hipError_t launch_infer_t(const InferDesc& d, hipStream_t stream) {
   p.H = d.H;
   p.full_batch = d.full_batch;
   p.use_dither = d.use_dither;
-  hipLaunchKernelGGL(wkv7_infer_kernel<Tin>, dim3(d.H, d.Ba, 1), dim3(kThreads, 1, 1), 0, stream, p);
+  const dim3 grid(d.H, d.Ba, 1), block(kThreads, 1, 1);
+  if (d.T == 1)
+    hipLaunchKernelGGL((wkv7_infer_kernel<Tin, 1>), grid, block, 0, stream, p);
+  else
+    hipLaunchKernelGGL((wkv7_infer_kernel<Tin, 16>), grid, block, 0, stream, p);
   return hipGetLastError();
 }
 
