@@ -39,6 +39,7 @@ COPY_PROBE_BYTES = 512 << 20        # fp32 stream (read once, write once) of --c
 # HBM traffic of the dominant kernel per launch, from rocprofv3 FETCH_SIZE /
 # WRITE_SIZE passes scaled by the copy probe; written by --pmc-summary
 TRAFFIC_FILE = os.path.join(HERE, "profiles", "wkv7_bwd_cfg1_traffic.md")
+TRAFFIC_FILE_DECODE = os.path.join(HERE, "profiles", "wkv7_infer_cfg3_traffic.md")
 METRIC = "WKV7 fwd+bwd Mtokens/s (B=8,T=4096,C=2048) + % FP32-VALU / HBM roofline"
 
 CONFIGS = {
@@ -94,11 +95,11 @@ def cpu_baseline(cfg, seconds_target=12.0):
                       f"{dt:.1f} s on {cores} threads (oracle/wkv7_oracle.c, reference order)"}
 
 
-def recorded_traffic(kernel: str):
-    """Bytes per launch of `kernel` recorded in TRAFFIC_FILE ("traffic_bytes
+def recorded_traffic(kernel: str, path: str = TRAFFIC_FILE):
+    """Bytes per launch of `kernel` recorded in `path` ("traffic_bytes
     <kernel>: <int>" lines), or None."""
     try:
-        with open(TRAFFIC_FILE) as f:
+        with open(path) as f:
             for line in f:
                 if line.startswith(f"traffic_bytes {kernel}:"):
                     return int(line.split(":")[1])
@@ -266,7 +267,7 @@ def bench_train(cfg, steps, warmup, with_cpu, probe=False):
     return out
 
 
-def bench_decode(cfg, steps, warmup):
+def bench_decode(cfg, steps, warmup, probe=False):
     import torch
     pkg = importlib.import_module("rwkv-rs_amd")
     native = importlib.import_module("rwkv-rs_amd._native")
@@ -291,6 +292,8 @@ def bench_decode(cfg, steps, warmup):
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
+    if probe:
+        copy_probe()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     e0.record(stream)
@@ -312,7 +315,8 @@ def bench_decode(cfg, steps, warmup):
         "roofline": {"bound": "hbm", "kernel": "wkv7_infer_kernel",
                      "achieved": nbytes / (launch_ms * 1e-3) / 1e9, "peak": PEAK_HBM / 1e9,
                      "unit": "GB/s", "frac": nbytes / (launch_ms * 1e-3) / PEAK_HBM,
-                     "traffic": None, "launch_ms": launch_ms},
+                     "traffic": recorded_traffic("wkv7_infer_kernel", TRAFFIC_FILE_DECODE),
+                     "algorithmic_bytes": nbytes, "launch_ms": launch_ms},
     }
 
 
@@ -338,7 +342,7 @@ def main():
         sys.exit(2)
     cfg = CONFIGS[args.config]
     if args.config == "cfg3":
-        out = bench_decode(cfg, args.steps, args.warmup)
+        out = bench_decode(cfg, args.steps, args.warmup, probe=args.copy_probe)
     else:
         out = bench_train(cfg, args.steps, args.warmup,
                           with_cpu=(not args.no_cpu and args.config == "cfg1"),
