@@ -10,9 +10,18 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <cstdlib>
+#include <cstring>
 #include <vector>
 
 #include "wkv7_launch.hpp"
+
+namespace wkv7 {
+bool force_step_kernels() {
+  const char* v = std::getenv("WKV7_BF16_PATH");
+  return v && std::strcmp(v, "valu") == 0;
+}
+}  // namespace wkv7
 
 namespace {
 

@@ -1,0 +1,180 @@
+// Matrix-core building blocks of the chunked WKV7 kernels (gfx950, bf16
+// operands, fp32 accumulation).
+//
+// Chunked form. Within a chunk of L = 16 steps that starts from state S0,
+// with the per-key log decays g_t = sum_{u<=t} log w~_u and gamma_t = e^{g_t}
+// (gamma_0 = 1), the reference recurrence (wkv7_common/kernel.rs:63-102)
+//   sa_t = S_{t-1} a_t,  S_t = S_{t-1} diag(w~_t) + sa_t b_t^T + v_t k_t^T,
+//   y_t = S_t r_t
+// unrolls into matrix products (rows of SA, Y, ... are the 16 steps):
+//   A^ = a o gamma_{t-1},  R^ = r o gamma_t,  K~ = k / gamma_t,  B~ = b / gamma_t,
+//   K- = k o gamma_L / gamma_t,  B- = b o gamma_L / gamma_t,
+//   A_ab = strict_lower(A^ B~^T),  A_ak = strict_lower(A^ K~^T),
+//   A_rb = lower(R^ B~^T),  A_rk = lower(R^ K~^T),  P = (I - A_ab)^{-1},
+//   SA = P A^ S0^T + P A_ak V = W S0^T + U,
+//   Y  = R^ S0^T + A_rk V + A_rb SA,
+//   S_L = S0 diag(gamma_L) + V^T K- + SA^T B-.
+// Only the last three lines depend on S0; everything else of a chunk is
+// computed off the state's dependency chain.
+//
+// Accumulation chains. A chain of MFMAs that accumulate into the same
+// registers uses one opcode throughout: on gfx950 a 16x16x16 result read as
+// the accumulator of a following 16x16x32 (or the reverse) needs more wait
+// states than the compiler inserts (measured: stale accumulator values with
+// the two it emits), while same-opcode chains forward correctly back to
+// back. 16x16x16 is used only for identity transposes, which start from zero
+// and whose results are read by VALU instructions.
+//
+// Precision. Every product whose operands are both inexact in bf16 is formed
+// from a hi/lo split (x = hi + lo, both bf16) as hi*hi + hi*lo + lo*hi with
+// fp32 accumulation, which keeps about 16 significant bits per product.
+// Products with a bf16 input tensor (v, or dy in the backward) as one operand
+// split the other operand only.
+//
+// Fragment layouts (v_mfma_f32_16x16x16_bf16 and v_mfma_f32_16x16x32_bf16,
+// lane l, quad qd = l / 16):
+//   A operand  lane l holds A[row = l % 16][k = 4*qd + e]      (x16, e < 4)
+//   B operand  lane l holds B[k = 4*qd + e][col = l % 16]       (x16)
+//   result     lane l holds D[row = 4*qd + r][col = l % 16]     (r < 4)
+// For x32 the operands hold 8 k-values per lane; the kernels use the k order
+// k(e) = 16*(e / 4) + 4*qd + e % 4 within each 32-wide half of the key axis, so
+// the two 4-value halves are exactly the result rows of two 16x16 tiles. With
+// that order a state tile kept as a result (rows = key i, columns = value j)
+// is directly the B operand of a contraction over i, and a result with rows =
+// steps is directly the B operand of a contraction over steps; no transposes
+// are needed on the state's chain.
+#pragma once
+
+#include "wkv7_device.hpp"
+
+namespace wkv7 {
+namespace chunk {
+
+constexpr int kL = 16;          // steps per chunk
+constexpr float kLog2e = 1.4426950408889634f;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+struct Split8 { bf16x8 hi, lo; };
+struct Split4 { bf16x4 hi, lo; };
+
+__device__ __forceinline__ f32x4 mma32(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mma16(bf16x4 a, bf16x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+      __builtin_bit_cast(i16x4, a), __builtin_bit_cast(i16x4, b), c, 0, 0, 0);
+}
+
+// hi*hi + hi*lo + lo*hi, small terms first
+__device__ __forceinline__ f32x4 mma32x3(const Split8& a, const Split8& b, f32x4 c) {
+  c = mma32(a.hi, b.lo, c);
+  c = mma32(a.lo, b.hi, c);
+  return mma32(a.hi, b.hi, c);
+}
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// two values to bf16 hi and lo parts, one packed conversion each
+__device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t& lo) {
+  const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+  const float ah = __uint_as_float(h << 16), bh = __uint_as_float(h & 0xffff0000u);
+  hi = h;
+  lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a - ah, b - bh}, bf16x2));
+}
+__device__ __forceinline__ Split4 split4(f32x4 x) {
+  uint32_t h0, l0, h1, l1;
+  split2(x[0], x[1], h0, l0);
+  split2(x[2], x[3], h1, l1);
+  return Split4{__builtin_bit_cast(bf16x4, make_uint2(h0, h1)),
+                __builtin_bit_cast(bf16x4, make_uint2(l0, l1))};
+}
+// x32 fragment from two 4-value halves (the result rows of two tiles)
+__device__ __forceinline__ bf16x8 cat8(bf16x4 a, bf16x4 b) {
+  return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+__device__ __forceinline__ Split8 split8(f32x4 x0, f32x4 x1) {
+  const Split4 a = split4(x0), b = split4(x1);
+  return Split8{cat8(a.hi, b.hi), cat8(a.lo, b.lo)};
+}
+__device__ __forceinline__ bf16x4 half_of(bf16x8 x, int h) {
+  return h ? __builtin_shufflevector(x, x, 4, 5, 6, 7) : __builtin_shufflevector(x, x, 0, 1, 2, 3);
+}
+__device__ __forceinline__ Split4 half_of(const Split8& x, int h) {
+  return Split4{half_of(x.hi, h), half_of(x.lo, h)};
+}
+__device__ __forceinline__ bf16x4 to_bf16x4(f32x4 x) {
+  return __builtin_convertvector(x, bf16x4);
+}
+
+// Products over a 16-long axis on the 32-deep instruction: the k axis holds
+// the hi part of the A operand in its first half and the lo part in its second
+// (a "stacked" A operand); the B operand repeats the same 16 values in both
+// halves. One instruction then forms a_hi b + a_lo b.
+__device__ __forceinline__ bf16x8 stack(const Split4& a) { return cat8(a.hi, a.lo); }
+__device__ __forceinline__ bf16x8 twice(bf16x4 b) { return cat8(b, b); }
+// a (stacked, split) times b (exact in bf16), contraction length 16
+__device__ __forceinline__ f32x4 mma_s2(bf16x8 a_stacked, bf16x4 b, f32x4 c) {
+  return mma32(a_stacked, twice(b), c);
+}
+// a (stacked, split) times b (split), contraction length 16: three terms,
+// a_hi b_lo from the B operand (b_lo | 0) and a_hi b_hi + a_lo b_hi
+__device__ __forceinline__ f32x4 mma_s3(bf16x8 a_stacked, const Split4& b, f32x4 c) {
+  c = mma32(a_stacked, cat8(b.lo, bf16x4{0, 0, 0, 0}), c);
+  return mma32(a_stacked, twice(b.hi), c);
+}
+
+// B operand of the 16x16 identity: multiplying an A fragment by it returns
+// the same 16x16 tile in the result layout, i.e. with rows and lanes swapped.
+// Exact for bf16 inputs.
+__device__ __forceinline__ bf16x4 identity_b(int lane) {
+  bf16x4 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = (__bf16)((4 * (lane >> 4) + e) == (lane & 15) ? 1.0f : 0.0f);
+  return o;
+}
+__device__ __forceinline__ bf16x4 transpose16(bf16x4 a, bf16x4 ident) {
+  return to_bf16x4(mma16(a, ident, f32x4{0.f, 0.f, 0.f, 0.f}));
+}
+
+// inclusive prefix sum over the 16 lanes of a DPP row
+__device__ __forceinline__ float row_scan16(float x) {
+  x += dpp_mov<0x111>(x);   // row_shr:1
+  x += dpp_mov<0x112>(x);   // row_shr:2
+  x += dpp_mov<0x114>(x);   // row_shr:4
+  x += dpp_mov<0x118>(x);   // row_shr:8
+  return x;
+}
+// value of lane 15 of each DPP row, broadcast to the row
+__device__ __forceinline__ float row_last16(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+      0, __builtin_bit_cast(int, x), 0x15F, 0xf, 0xf, false));   // row_newbcast:15
+}
+
+__device__ __forceinline__ float exp2_f(float x) { return __builtin_amdgcn_exp2f(x); }
+// log2 of the decay: log2(w~) = W_SCALE * sigmoid(x) * log2(e)
+__device__ __forceinline__ float log2_decay(float x) {
+  const float sig = __builtin_amdgcn_rcpf(1.0f + exp2_f(-kLog2e * x));
+  return (kWScale * kLog2e) * sig;
+}
+
+// wait until at most n vector-memory operations of this wave are in flight
+// (gfx9 s_waitcnt encoding; expcnt and lgkmcnt left at their maxima)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt(((N >> 4) << 14) | (0xF << 8) | (0x7 << 4) | (N & 0xF));
+}
+// this wave's LDS writes are done and visible to its own later reads
+__device__ __forceinline__ void wave_lds_sync() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+  __builtin_amdgcn_wave_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+}  // namespace chunk
+}  // namespace wkv7

@@ -1,0 +1,368 @@
+// Chunked WKV7 forward on the matrix cores (bf16 operands, fp32 state).
+//
+// Computes what wkv7_forward_kernel does (crates/rwkv-nn/src/kernels/
+// wkv7_common/kernel.rs:6-114, launched by wkv7_common/host.rs:29-183): the
+// per-step removal_state sa_t = S_{t-1} a_t, the output y_t = S_t r_t, the
+// transposed state every chunk_len steps, the optional initial state load and
+// final state store. It takes the matrix form of 16-step chunks (wkv7_chunk.hpp)
+// instead of stepping the state 4096 times, so the state's dependency chain is
+// 37 small matrix products per chunk instead of 16 rank-2 updates with
+// reductions.
+//
+// Work layout: one workgroup of four waves per (batch, head). Steps are taken
+// four chunks (64 steps) at a time:
+//   phase 1  wave w prepares chunk w of the batch on its own: decays, the four
+//            16x16 step-by-step products, P by forward substitution, W and U,
+//            and leaves every operand phase 2 needs in LDS, already in
+//            fragment order (one 16-byte or 8-byte load per lane);
+//   phase 2  the four chunks in order; wave w owns value columns 16w..16w+15
+//            of the state (state rows are independent in the forward) and
+//            computes SA, Y and the next state for them.
+// The raw inputs of the next batch stream into LDS (global_load_lds) during
+// phase 2.
+#include "wkv7_chunk.hpp"
+#include "wkv7_launch.hpp"
+
+namespace wkv7 {
+namespace {
+
+using namespace chunk;
+
+constexpr int kWaves = 4;
+constexpr int kBlock = 64 * kWaves;
+constexpr int kBatch = 4;                 // chunks per batch, one per wave
+constexpr int kVecs = 6;                  // staged inputs: x, r, k, a, b, v
+enum { S_X, S_R, S_K, S_A, S_B, S_V };
+constexpr int kPieces = kVecs * kBatch * kL * 8 / kBlock;   // 16-byte loads per thread
+
+// Phase-1 products of one chunk, each in the fragment order its phase-2
+// consumer loads (index [lane] last). K~ and B~ are kept without the chunk's
+// total decay gamma_L, which phase 2 applies to the updated state instead:
+// S_L^T = diag(gamma_L) (S0^T + K~^T V + B~^T SA).
+struct ChunkOps {
+  bf16x8 w[2][2][64];     // W = P A^, x32 A operand: [key half][hi/lo]
+  bf16x8 r[2][2][64];     // R^, x32 A operand
+  bf16x8 ark[64];         // A_rk stacked (hi | lo), contraction over steps
+  bf16x8 arb[64];         // A_rb stacked
+  bf16x8 kt[4][64];       // K~^T stacked, per key tile (row = key, k = step)
+  bf16x8 bt[4][64];       // B~^T stacked
+  bf16x4 v[4][64];        // V, x16 B operand per value tile (k = step)
+  f32x4 u[4][64];         // U per value tile, result layout (SA's start)
+  float gl[64];           // gamma_L
+};
+
+struct FwdChunkParams {
+  const bf16_t* in[kVecs];   // [B,T,H,64] each, in S_* order
+  const float* s0;
+  float* ckpt;
+  float* sa;
+  bf16_t* y;
+  float* sT;
+  int T, H, C;
+};
+
+// Phase 1 for one chunk, run by one wave. `stg` holds the chunk's raw rows
+// (rotated 16-byte pieces); `amat`/`pmat` are the wave's 16x16 scratch.
+__device__ __forceinline__ void prepare_chunk(const bf16_t (*stg)[kBatch][kL][64], int q,
+                                              float (*amat)[kL], float (*pmat)[kL],
+                                              ChunkOps& o, int lane) {
+  const int t = lane & 15, qd = lane >> 4;
+  const bf16x4 ident = identity_b(lane);
+  // the lane's step row t, keys 32 m + 16 hh + 4 qd + c (c < 4), as raw bf16
+  auto raw = [&](int vec, int m, int hh) -> uint2 {
+    const int c0 = 32 * m + 16 * hh + 4 * qd;
+    const int slot = ((c0 >> 3) + t) & 7;
+    return *reinterpret_cast<const uint2*>(&stg[vec][q][t][8 * slot + (c0 & 7)]);
+  };
+  auto widen = [](uint2 u) -> f32x4 {
+    return f32x4{__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
+                 __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u)};
+  };
+
+  // decays: gamma_t (prefix product over the chunk's steps, via log2 sums),
+  // 1/gamma_t, gamma_{t-1} (previous lane of the row; 1 at t = 0), gamma_L
+  f32x4 gam[2][2], gin[2][2], gpv[2][2];
+  float gL[2][2][4];
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const f32x4 x = widen(raw(S_X, m, hh));
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float g = row_scan16(log2_decay(x[c]));
+        const float e = exp2_f(g);
+        gam[m][hh][c] = e;
+        gin[m][hh][c] = exp2_f(-g);
+        gpv[m][hh][c] = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+            __builtin_bit_cast(int, 1.0f), __builtin_bit_cast(int, e), 0x111, 0xf, 0xf, false));
+        gL[m][hh][c] = row_last16(e);
+      }
+    }
+  Split8 AH[2], RH[2], KT[2], BT[2];
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    f32x4 ah[2], rh[2], kt[2], bt[2];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      ah[hh] = widen(raw(S_A, m, hh)) * gpv[m][hh];
+      rh[hh] = widen(raw(S_R, m, hh)) * gam[m][hh];
+      kt[hh] = widen(raw(S_K, m, hh)) * gin[m][hh];
+      bt[hh] = widen(raw(S_B, m, hh)) * gin[m][hh];
+    }
+    AH[m] = split8(ah[0], ah[1]);
+    RH[m] = split8(rh[0], rh[1]);
+    KT[m] = split8(kt[0], kt[1]);
+    BT[m] = split8(bt[0], bt[1]);
+  }
+  // step-by-step products, computed transposed: result row = step s, lane
+  // column = step t, which is the x16 A operand (row t, k = s) of A_xx[t][s]
+  f32x4 akT = {0.f, 0.f, 0.f, 0.f}, arkT = akT, arbT = akT, aabT = akT;
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    akT = mma32x3(KT[m], AH[m], akT);
+    arkT = mma32x3(KT[m], RH[m], arkT);
+    arbT = mma32x3(BT[m], RH[m], arbT);
+    aabT = mma32x3(BT[m], AH[m], aabT);
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int s = 4 * qd + r;
+    if (!(s < t)) { akT[r] = 0.f; aabT[r] = 0.f; }
+    if (!(s <= t)) { arkT[r] = 0.f; arbT[r] = 0.f; }
+  }
+  // P = (I - A_ab)^{-1} by forward substitution; lane column u = t
+  *reinterpret_cast<f32x4*>(&amat[t][4 * qd]) = aabT;
+  wave_lds_sync();
+  float pc[kL];
+#pragma unroll
+  for (int tt = 0; tt < kL; ++tt) {
+    float acc = (tt == t) ? 1.0f : 0.0f;
+#pragma unroll
+    for (int s4 = 0; s4 < tt; s4 += 4) {
+      const f32x4 arow = *reinterpret_cast<const f32x4*>(&amat[tt][s4]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (s4 + e < tt) acc += arow[e] * pc[s4 + e];
+    }
+    pc[tt] = acc;
+  }
+  if (qd == 0) {
+#pragma unroll
+    for (int tt = 0; tt < kL; ++tt) pmat[tt][t] = pc[tt];
+  }
+  wave_lds_sync();
+  const Split4 P = split4(*reinterpret_cast<const f32x4*>(&pmat[t][4 * qd]));
+
+  // W^T tile ib = A^T P^T (result rows = keys, lane column = step t), which
+  // is W in the x32 A-operand order; K~^T, B~^T and V by identity products
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    f32x4 Wt[2];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const int ib = 2 * m + hh;
+      const Split4 a = half_of(AH[m], hh), k = half_of(KT[m], hh), b = half_of(BT[m], hh);
+      const Split4 aT{transpose16(a.hi, ident), transpose16(a.lo, ident)};
+      Wt[hh] = mma_s3(stack(aT), P, f32x4{0.f, 0.f, 0.f, 0.f});
+      o.kt[ib][lane] = cat8(transpose16(k.hi, ident), transpose16(k.lo, ident));
+      o.bt[ib][lane] = cat8(transpose16(b.hi, ident), transpose16(b.lo, ident));
+    }
+    const Split8 w8 = split8(Wt[0], Wt[1]);
+    o.w[m][0][lane] = w8.hi;
+    o.w[m][1][lane] = w8.lo;
+    o.r[m][0][lane] = RH[m].hi;
+    o.r[m][1][lane] = RH[m].lo;
+  }
+  const bf16x8 ak = stack(split4(akT));
+  o.ark[lane] = stack(split4(arkT));
+  o.arb[lane] = stack(split4(arbT));
+  // U = P (A_ak V), per value tile
+  const bf16x8 Ps = stack(P);
+#pragma unroll
+  for (int vb = 0; vb < 4; ++vb) {
+    const uint2 vr = raw(S_V, vb >> 1, vb & 1);
+    const bf16x4 vt = transpose16(__builtin_bit_cast(bf16x4, vr), ident);
+    o.v[vb][lane] = vt;
+    const f32x4 X = mma_s2(ak, vt, f32x4{0.f, 0.f, 0.f, 0.f});
+    o.u[vb][lane] = mma_s3(Ps, split4(X), f32x4{0.f, 0.f, 0.f, 0.f});
+  }
+  if (t == 0) {
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+        *reinterpret_cast<f32x4*>(&o.gl[32 * m + 16 * hh + 4 * qd]) =
+            f32x4{gL[m][hh][0], gL[m][hh][1], gL[m][hh][2], gL[m][hh][3]};
+  }
+}
+
+// Phase-2 operands of one chunk for value tile jb, in registers
+struct ChainOps {
+  Split8 w[2], r[2];
+  bf16x8 ark, arb, kt[4], bt[4];
+  bf16x4 v;
+  f32x4 u, gl[4];
+};
+__device__ __forceinline__ ChainOps load_chain_ops(const ChunkOps& o, int jb, int lane) {
+  const int qd = lane >> 4;
+  ChainOps c;
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    c.w[m] = Split8{o.w[m][0][lane], o.w[m][1][lane]};
+    c.r[m] = Split8{o.r[m][0][lane], o.r[m][1][lane]};
+  }
+  c.ark = o.ark[lane];
+  c.arb = o.arb[lane];
+#pragma unroll
+  for (int ib = 0; ib < 4; ++ib) {
+    c.kt[ib] = o.kt[ib][lane];
+    c.bt[ib] = o.bt[ib][lane];
+    c.gl[ib] = *reinterpret_cast<const f32x4*>(&o.gl[16 * ib + 4 * qd]);
+  }
+  c.v = o.v[jb][lane];
+  c.u = o.u[jb][lane];
+  return c;
+}
+
+template <bool kHasS0>
+__global__ __launch_bounds__(kBlock, 1) void wkv7_fwd_chunk_kernel(const FwdChunkParams p) {
+  __shared__ ChunkOps ops[kBatch];
+  // raw inputs of a batch: [vec][chunk][step][64 bf16], 16-byte pieces of a
+  // row rotated by the step index so phase-1 reads spread over the banks
+  __shared__ __attribute__((aligned(16))) bf16_t stg[kVecs][kBatch][kL][64];
+  __shared__ __attribute__((aligned(16))) float amat[kWaves][kL][kL];
+  __shared__ __attribute__((aligned(16))) float pmat[kWaves][kL][kL];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int t = lane & 15, qd = lane >> 4;
+  const int h = blockIdx.x, b = blockIdx.y, H = p.H, T = p.T;
+  const int64_t bh = (int64_t)b * H + h;
+  const int64_t tstride = (int64_t)H * kHead;              // elements per step
+  const int64_t tok0 = ((int64_t)b * T * H + h) * kHead;   // step 0 of (b, h)
+  const int nchunks = T / kL, nbatches = (nchunks + kBatch - 1) / kBatch;
+
+  // ---- staging loads: thread tid moves pieces k = 0..kPieces-1 of a batch.
+  // Piece p = kBlock * k + tid is row p / 8 = (vec, chunk, step), slot p % 8,
+  // which holds global 16-byte piece (slot - step) % 8 of the row.
+  const int st_t = (tid >> 3) & 15, st_slot = tid & 7;
+  const int st_oct = (st_slot - st_t) & 7;
+  auto issue = [&](int n) {
+    const int nq = min(kBatch, nchunks - kBatch * n);
+#pragma unroll
+    for (int k = 0; k < kPieces; ++k) {
+      const int vec = k >> 1, q = 2 * (k & 1) + (tid >> 7);
+      if (q < nq) {
+        const bf16_t* src = p.in[vec] + tok0 + (int64_t)(kL * (kBatch * n + q) + st_t) * tstride + 8 * st_oct;
+        load_lds16(src, reinterpret_cast<char*>(&stg[0][0][0][0]) + (kBlock * k + 64 * wave) * 16);
+      }
+    }
+  };
+
+  // ---- state: value tile jb = wave, key tiles ib = 0..3, result layout
+  // (rows = key i = 16 ib + 4 qd + r, columns = value j = 16 jb + t)
+  const int jb = wave, jcol = 16 * jb + t;
+  f32x4 S[4];
+#pragma unroll
+  for (int ib = 0; ib < 4; ++ib) {
+    if (kHasS0)
+      S[ib] = *reinterpret_cast<const f32x4*>(p.s0 + bh * (kHead * kHead) + jcol * kHead + 16 * ib + 4 * qd);
+    else
+      S[ib] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  float* const sa_base = p.sa + tok0 + 4 * qd * tstride + jcol;
+  bf16_t* const y_base = p.y + tok0 + 4 * qd * tstride + jcol;
+  float* const ck_base = p.ckpt + bh * (T / p.C) * (kHead * kHead) + 4 * qd * kHead + jcol;
+
+  issue(0);
+  for (int n = 0; n < nbatches; ++n) {
+    const int nq = min(kBatch, nchunks - kBatch * n);
+    wait_vmcnt<0>();
+    lds_barrier();
+    if (wave < nq) prepare_chunk(stg, wave, amat[wave], pmat[wave], ops[wave], lane);
+    lds_barrier();   // chunk operands visible; staging free
+    if (n + 1 < nbatches) issue(n + 1);
+
+    // =========================== phase 2: the state's chain, value tile jb
+    ChainOps cur = load_chain_ops(ops[0], jb, lane);
+    for (int q = 0; q < nq; ++q) {
+      ChainOps nxt;
+      if (q + 1 < nq) nxt = load_chain_ops(ops[q + 1], jb, lane);
+      const int cidx = kBatch * n + q;
+      const Split8 Sx0 = split8(S[0], S[1]), Sx1 = split8(S[2], S[3]);
+      f32x4 sa = mma32x3(cur.w[0], Sx0, cur.u);
+      sa = mma32x3(cur.w[1], Sx1, sa);
+      f32x4 yv = mma32x3(cur.r[0], Sx0, f32x4{0.f, 0.f, 0.f, 0.f});
+      yv = mma32x3(cur.r[1], Sx1, yv);
+      yv = mma_s2(cur.ark, cur.v, yv);
+      const Split4 sas = split4(sa);
+      yv = mma_s3(cur.arb, sas, yv);
+#pragma unroll
+      for (int ib = 0; ib < 4; ++ib) {
+        f32x4 s = mma_s2(cur.kt[ib], cur.v, S[ib]);
+        s = mma_s3(cur.bt[ib], sas, s);
+        S[ib] = s * cur.gl[ib];
+      }
+      // outputs: rows = steps 16 cidx + 4 qd + r, column = value jcol
+      const int64_t coff = (int64_t)kL * cidx * tstride;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        sa_base[coff + r * tstride] = sa[r];
+        y_base[coff + r * tstride] = __builtin_bit_cast(bf16_t, (__bf16)yv[r]);
+      }
+      if ((kL * (cidx + 1)) % p.C == 0) {
+        float* ck = ck_base + (int64_t)(kL * (cidx + 1) / p.C - 1) * (kHead * kHead);
+#pragma unroll
+        for (int ib = 0; ib < 4; ++ib)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) ck[(16 * ib + r) * kHead] = S[ib][r];
+      }
+      cur = nxt;
+    }
+  }
+
+  if (p.sT) {
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib)
+      *reinterpret_cast<f32x4*>(p.sT + bh * (kHead * kHead) + jcol * kHead + 16 * ib + 4 * qd) = S[ib];
+  }
+}
+
+}  // namespace
+
+// bf16 operands and chunk_len 16. The checkpoints feed the reference-order
+// backward, which rebuilds each step's state by dividing by the decay and so
+// amplifies a checkpoint's deviation by about 1.35x per step: from a 16-step
+// checkpoint the ~3e-6 relative deviation of the split-bf16 products stays far
+// inside the bf16 tolerance, from a 32-step one it does not (the reference
+// algorithm itself loses ~5e-4 there), so longer chunk lengths keep the
+// step-by-step fp32 forward.
+bool chunk_forward_supported(const ForwardDesc& d) {
+  return d.dtype == Dtype::BF16 && d.C == kL && d.T % kL == 0;
+}
+
+hipError_t launch_forward_chunked(const ForwardDesc& d, hipStream_t stream) {
+  FwdChunkParams p;
+  p.in[S_X] = static_cast<const bf16_t*>(d.w);
+  p.in[S_R] = static_cast<const bf16_t*>(d.r);
+  p.in[S_K] = static_cast<const bf16_t*>(d.k);
+  p.in[S_A] = static_cast<const bf16_t*>(d.a);
+  p.in[S_B] = static_cast<const bf16_t*>(d.b);
+  p.in[S_V] = static_cast<const bf16_t*>(d.v);
+  p.s0 = d.s0;
+  p.ckpt = d.ckpt;
+  p.sa = d.sa;
+  p.y = static_cast<bf16_t*>(d.y);
+  p.sT = d.sT;
+  p.T = d.T;
+  p.H = d.H;
+  p.C = d.C;
+  const dim3 grid(d.H, d.B, 1), block(kBlock, 1, 1);
+  if (d.s0)
+    hipLaunchKernelGGL(wkv7_fwd_chunk_kernel<true>, grid, block, 0, stream, p);
+  else
+    hipLaunchKernelGGL(wkv7_fwd_chunk_kernel<false>, grid, block, 0, stream, p);
+  return hipGetLastError();
+}
+
+}  // namespace wkv7

@@ -51,6 +51,14 @@ struct InferDesc {
 };
 
 hipError_t launch_forward(const ForwardDesc& d, hipStream_t stream);
+
+// Chunked matrix-core forward (wkv7_chunk_forward.hip): bf16 operands,
+// chunk_len 16. launch_forward picks it when supported unless
+// the environment variable WKV7_BF16_PATH is "valu" (a diagnostic switch that
+// keeps the step-by-step kernels for every dtype).
+bool chunk_forward_supported(const ForwardDesc& d);
+hipError_t launch_forward_chunked(const ForwardDesc& d, hipStream_t stream);
+bool force_step_kernels();
 hipError_t launch_backward(const BackwardDesc& d, hipStream_t stream);
 hipError_t launch_infer(const InferDesc& d, hipStream_t stream);
 
