@@ -140,6 +140,59 @@ __device__ __forceinline__ bf16x4 transpose16(bf16x4 a, bf16x4 ident) {
   return to_bf16x4(mma16(a, ident, f32x4{0.f, 0.f, 0.f, 0.f}));
 }
 
+// Transposed fragment load (ds_read_b64_tr_b16). Within each group of 16
+// lanes, lane c supplies the address of 4 consecutive bf16 values; lane c' of
+// the group receives value c' % 4 of the pieces addressed by lanes
+// c' / 4 + 4 j, j = 0..3. If lane c of group g addresses row 4 g + c / 4,
+// columns c0 + 4 (c % 4) of a row-major tile, lane l receives
+// tile[4 qd + e][c0 + l % 16]: the x16 operand whose k index is the row.
+__device__ __forceinline__ bf16x4 read_tr16(const void* lds) {
+  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+  return __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_i16x4*)(__attribute__((address_space(3))) void*)(void*)lds));
+}
+
+// A tile of bf16 rows (64 columns) in LDS with each row's eight 16-byte
+// pieces rotated by the row index: element (row, c) lives in piece
+// (c / 8 + row) % 8. Reads of 8 bytes from 16 consecutive rows then spread
+// over the banks.
+__device__ __forceinline__ bf16_t* tile_at(bf16_t (*tile)[64], int row, int c) {
+  return &tile[row][8 * (((c >> 3) + row) & 7) + (c & 7)];
+}
+__device__ __forceinline__ const bf16_t* tile_at(const bf16_t (*tile)[64], int row, int c) {
+  return &tile[row][8 * (((c >> 3) + row) & 7) + (c & 7)];
+}
+__device__ __forceinline__ bf16x4 read4(const bf16_t (*tile)[64], int row, int c) {
+  return *reinterpret_cast<const bf16x4*>(tile_at(tile, row, c));
+}
+__device__ __forceinline__ void write4(bf16_t (*tile)[64], int row, int c, bf16x4 v) {
+  *reinterpret_cast<bf16x4*>(tile_at(tile, row, c)) = v;
+}
+// x32 fragment of one row (the lane's row), k over the 32 columns of half m
+// in the kernels' k order: columns 32 m + 4 qd + e and 32 m + 16 + 4 qd + e
+__device__ __forceinline__ bf16x8 row_frag(const bf16_t (*tile)[64], int row, int m, int qd) {
+  return cat8(read4(tile, row, 32 * m + 4 * qd), read4(tile, row, 32 * m + 16 + 4 * qd));
+}
+// transposed x16 fragment of a rotated tile: lane l gets
+// tile[row0 + 4 qd + e][c0 + l % 16] (k = row)
+__device__ __forceinline__ bf16x4 tr_frag(const bf16_t (*tile)[64], int row0, int c0, int lane) {
+  const int g = lane >> 4, c = lane & 15;
+  return read_tr16(tile_at(tile, row0 + 4 * g + (c >> 2), c0 + 4 * (c & 3)));
+}
+// transposed x32 fragment, k = rows 32 m .. 32 m + 31 in the kernels' k order
+__device__ __forceinline__ bf16x8 tr_frag32(const bf16_t (*tile)[64], int m, int c0, int lane) {
+  return cat8(tr_frag(tile, 32 * m, c0, lane), tr_frag(tile, 32 * m + 16, c0, lane));
+}
+
+// sum over the 16 lanes of a DPP row, result in every lane of the row
+__device__ __forceinline__ float row_sum16(float x) {
+  x += dpp_mov<0x128>(x);   // row_ror:8
+  x += dpp_mov<0x124>(x);   // row_ror:4
+  x += dpp_mov<0x122>(x);   // row_ror:2
+  x += dpp_mov<0x121>(x);   // row_ror:1
+  return x;
+}
+
 // inclusive prefix sum over the 16 lanes of a DPP row
 __device__ __forceinline__ float row_scan16(float x) {
   x += dpp_mov<0x111>(x);   // row_shr:1

@@ -61,18 +61,19 @@ struct FwdChunkParams {
   int T, H, C;
 };
 
-// Phase 1 for one chunk, run by one wave. `stg` holds the chunk's raw rows
-// (rotated 16-byte pieces); `amat`/`pmat` are the wave's 16x16 scratch.
-__device__ __forceinline__ void prepare_chunk(const bf16_t (*stg)[kBatch][kL][64], int q,
-                                              float (*amat)[kL], float (*pmat)[kL],
-                                              ChunkOps& o, int lane) {
+// Phase 1 for one chunk, run by one wave. `stg` holds the chunk's raw rows;
+// after they are read, the chunk's x, r, k, a, b rows and the wave's scratch
+// `scr` (first the 16x16 fp32 matrices of the substitution) are reused for
+// the hi/lo rows of A^, K~ and B~, from which the transposed fragments are
+// read.
+__device__ __forceinline__ void prepare_chunk(bf16_t (*stg)[kBatch][kL][64], int q,
+                                              float (*scr)[kL][kL], ChunkOps& o, int lane) {
   const int t = lane & 15, qd = lane >> 4;
-  const bf16x4 ident = identity_b(lane);
+  float (*amat)[kL] = scr[0];
+  float (*pmat)[kL] = scr[1];
   // the lane's step row t, keys 32 m + 16 hh + 4 qd + c (c < 4), as raw bf16
   auto raw = [&](int vec, int m, int hh) -> uint2 {
-    const int c0 = 32 * m + 16 * hh + 4 * qd;
-    const int slot = ((c0 >> 3) + t) & 7;
-    return *reinterpret_cast<const uint2*>(&stg[vec][q][t][8 * slot + (c0 & 7)]);
+    return *reinterpret_cast<const uint2*>(tile_at(stg[vec][q], t, 32 * m + 16 * hh + 4 * qd));
   };
   auto widen = [](uint2 u) -> f32x4 {
     return f32x4{__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
@@ -154,19 +155,40 @@ __device__ __forceinline__ void prepare_chunk(const bf16_t (*stg)[kBatch][kL][64
   wave_lds_sync();
   const Split4 P = split4(*reinterpret_cast<const f32x4*>(&pmat[t][4 * qd]));
 
+  // hi/lo rows of A^, K~, B~ into LDS (the chunk's raw rows are consumed),
+  // then their transposed fragments (row = key, k = step) by transposed loads
+  bf16_t (*rows[6])[64] = {stg[S_X][q], stg[S_R][q], stg[S_K][q], stg[S_A][q], stg[S_B][q],
+                           reinterpret_cast<bf16_t (*)[64]>(&scr[0][0][0])};
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const int c0 = 32 * m + 16 * hh + 4 * qd;
+      const Split4 a = half_of(AH[m], hh), k = half_of(KT[m], hh), b = half_of(BT[m], hh);
+      *reinterpret_cast<bf16x4*>(tile_at(rows[0], t, c0)) = a.hi;
+      *reinterpret_cast<bf16x4*>(tile_at(rows[1], t, c0)) = a.lo;
+      *reinterpret_cast<bf16x4*>(tile_at(rows[2], t, c0)) = k.hi;
+      *reinterpret_cast<bf16x4*>(tile_at(rows[3], t, c0)) = k.lo;
+      *reinterpret_cast<bf16x4*>(tile_at(rows[4], t, c0)) = b.hi;
+      *reinterpret_cast<bf16x4*>(tile_at(rows[5], t, c0)) = b.lo;
+    }
+  wave_lds_sync();
+  // lane (group g, c) addresses row 4 g + c / 4, columns 16 ib + 4 (c % 4)
+  const int tr_t = 4 * qd + (t >> 2), tr_c = 4 * (t & 3);
+  auto tr = [&](bf16_t (*tile)[64], int ib) { return read_tr16(tile_at(tile, tr_t, 16 * ib + tr_c)); };
+
   // W^T tile ib = A^T P^T (result rows = keys, lane column = step t), which
-  // is W in the x32 A-operand order; K~^T, B~^T and V by identity products
+  // is W in the x32 A-operand order
 #pragma unroll
   for (int m = 0; m < 2; ++m) {
     f32x4 Wt[2];
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
       const int ib = 2 * m + hh;
-      const Split4 a = half_of(AH[m], hh), k = half_of(KT[m], hh), b = half_of(BT[m], hh);
-      const Split4 aT{transpose16(a.hi, ident), transpose16(a.lo, ident)};
+      const Split4 aT{tr(rows[0], ib), tr(rows[1], ib)};
       Wt[hh] = mma_s3(stack(aT), P, f32x4{0.f, 0.f, 0.f, 0.f});
-      o.kt[ib][lane] = cat8(transpose16(k.hi, ident), transpose16(k.lo, ident));
-      o.bt[ib][lane] = cat8(transpose16(b.hi, ident), transpose16(b.lo, ident));
+      o.kt[ib][lane] = cat8(tr(rows[2], ib), tr(rows[3], ib));
+      o.bt[ib][lane] = cat8(tr(rows[4], ib), tr(rows[5], ib));
     }
     const Split8 w8 = split8(Wt[0], Wt[1]);
     o.w[m][0][lane] = w8.hi;
@@ -181,8 +203,7 @@ __device__ __forceinline__ void prepare_chunk(const bf16_t (*stg)[kBatch][kL][64
   const bf16x8 Ps = stack(P);
 #pragma unroll
   for (int vb = 0; vb < 4; ++vb) {
-    const uint2 vr = raw(S_V, vb >> 1, vb & 1);
-    const bf16x4 vt = transpose16(__builtin_bit_cast(bf16x4, vr), ident);
+    const bf16x4 vt = tr(stg[S_V][q], vb);
     o.v[vb][lane] = vt;
     const f32x4 X = mma_s2(ak, vt, f32x4{0.f, 0.f, 0.f, 0.f});
     o.u[vb][lane] = mma_s3(Ps, split4(X), f32x4{0.f, 0.f, 0.f, 0.f});
@@ -231,8 +252,7 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_fwd_chunk_kernel(const FwdChun
   // raw inputs of a batch: [vec][chunk][step][64 bf16], 16-byte pieces of a
   // row rotated by the step index so phase-1 reads spread over the banks
   __shared__ __attribute__((aligned(16))) bf16_t stg[kVecs][kBatch][kL][64];
-  __shared__ __attribute__((aligned(16))) float amat[kWaves][kL][kL];
-  __shared__ __attribute__((aligned(16))) float pmat[kWaves][kL][kL];
+  __shared__ __attribute__((aligned(16))) float scr[kWaves][2][kL][kL];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int t = lane & 15, qd = lane >> 4;
@@ -270,24 +290,22 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_fwd_chunk_kernel(const FwdChun
     else
       S[ib] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  float* const sa_base = p.sa + tok0 + 4 * qd * tstride + jcol;
-  bf16_t* const y_base = p.y + tok0 + 4 * qd * tstride + jcol;
-  float* const ck_base = p.ckpt + bh * (T / p.C) * (kHead * kHead) + 4 * qd * kHead + jcol;
+  const uint32_t tok_row = (uint32_t)tstride;                       // one step
+  const uint32_t tok_off = 4 * qd * tok_row + jcol;                  // row 4 qd, column jcol
+  const uint32_t ck_off = 4 * qd * kHead + jcol;
 
   issue(0);
   for (int n = 0; n < nbatches; ++n) {
     const int nq = min(kBatch, nchunks - kBatch * n);
     wait_vmcnt<0>();
     lds_barrier();
-    if (wave < nq) prepare_chunk(stg, wave, amat[wave], pmat[wave], ops[wave], lane);
+    if (wave < nq) prepare_chunk(stg, wave, scr[wave], ops[wave], lane);
     lds_barrier();   // chunk operands visible; staging free
     if (n + 1 < nbatches) issue(n + 1);
 
     // =========================== phase 2: the state's chain, value tile jb
-    ChainOps cur = load_chain_ops(ops[0], jb, lane);
     for (int q = 0; q < nq; ++q) {
-      ChainOps nxt;
-      if (q + 1 < nq) nxt = load_chain_ops(ops[q + 1], jb, lane);
+      const ChainOps cur = load_chain_ops(ops[q], jb, lane);
       const int cidx = kBatch * n + q;
       const Split8 Sx0 = split8(S[0], S[1]), Sx1 = split8(S[2], S[3]);
       f32x4 sa = mma32x3(cur.w[0], Sx0, cur.u);
@@ -304,20 +322,21 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_fwd_chunk_kernel(const FwdChun
         S[ib] = s * cur.gl[ib];
       }
       // outputs: rows = steps 16 cidx + 4 qd + r, column = value jcol
-      const int64_t coff = (int64_t)kL * cidx * tstride;
+      const int64_t cbase = tok0 + (int64_t)kL * cidx * tstride;
+      float* const sa_c = p.sa + cbase;
+      bf16_t* const y_c = p.y + cbase;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        sa_base[coff + r * tstride] = sa[r];
-        y_base[coff + r * tstride] = __builtin_bit_cast(bf16_t, (__bf16)yv[r]);
+        sa_c[tok_off + r * tok_row] = sa[r];
+        y_c[tok_off + r * tok_row] = __builtin_bit_cast(bf16_t, (__bf16)yv[r]);
       }
       if ((kL * (cidx + 1)) % p.C == 0) {
-        float* ck = ck_base + (int64_t)(kL * (cidx + 1) / p.C - 1) * (kHead * kHead);
+        float* const ck = p.ckpt + (bh * (T / p.C) + kL * (cidx + 1) / p.C - 1) * (kHead * kHead);
 #pragma unroll
         for (int ib = 0; ib < 4; ++ib)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) ck[(16 * ib + r) * kHead] = S[ib][r];
+          for (int r = 0; r < 4; ++r) ck[ck_off + (16 * ib + r) * kHead] = S[ib][r];
       }
-      cur = nxt;
     }
   }
 

@@ -59,6 +59,12 @@ hipError_t launch_forward(const ForwardDesc& d, hipStream_t stream);
 bool chunk_forward_supported(const ForwardDesc& d);
 hipError_t launch_forward_chunked(const ForwardDesc& d, hipStream_t stream);
 bool force_step_kernels();
+
+// Chunked matrix-core backward (wkv7_chunk_backward.hip): bf16 operands,
+// chunk_len 16, T a positive multiple of 16; picked by launch_backward under
+// the same switch.
+bool chunk_backward_supported(const BackwardDesc& d);
+hipError_t launch_backward_chunked(const BackwardDesc& d, hipStream_t stream);
 hipError_t launch_backward(const BackwardDesc& d, hipStream_t stream);
 hipError_t launch_infer(const InferDesc& d, hipStream_t stream);
 
