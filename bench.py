@@ -10,9 +10,12 @@ B=8, T=4096, H=32, N=64, bf16 operands, fp32 state and arithmetic,
 initial state ~ N(0, 0.1).
 
 Printed JSON line: whole-job Mtokens/s, ms per step, the roofline of the
-dominant kernel (the backward: algorithmic FLOPs per launch / mean launch time
-from HIP events recorded on the launch stream, against the MI355X FP32 vector
-peak), and the CPU baseline (the oracle's reference-order fp32 restatement,
+dominant kernel (the backward: algorithmic FP32 FLOPs per launch / mean launch
+time from HIP events recorded on the launch stream, against MI355X's 157.3
+TFLOP/s FP32 peak, which is both the packed-VALU and the dense fp32-MFMA
+figure; with bf16 operands and chunk_len 16 the kernels are the chunked
+matrix-core ones, which form the fp32 products from split bf16 MFMAs), and
+the CPU baseline (the oracle's reference-order fp32 restatement,
 OpenMP over (batch, head) pairs, timed on a bounded sample of the same
 workload on the host cores). config cfg3 is the batched decode step (T=1),
 which is HBM-bound.
@@ -33,7 +36,7 @@ sys.path.insert(0, HERE)
 N_HEAD = 64
 FLOP_FWD = 9 * N_HEAD * N_HEAD      # per head-step: sa 2N^2, update 5N^2, y 2N^2
 FLOP_BWD = 24 * N_HEAD * N_HEAD     # per head-step, non-redundant backward
-PEAK_FP32 = 157.3e12                # MI355X FP32 vector peak (packed issue)
+PEAK_FP32 = 157.3e12                # MI355X FP32 peak (packed VALU; also dense fp32 MFMA)
 PEAK_HBM = 8.0e12                   # MI355X HBM3E
 COPY_PROBE_BYTES = 512 << 20        # fp32 stream (read once, write once) of --copy-probe
 # HBM traffic of the dominant kernel per launch, from rocprofv3 FETCH_SIZE /
@@ -130,7 +133,8 @@ def pmc_summary(dirs):
     import csv
     import glob
     from collections import defaultdict
-    keys = ("wkv7_fwd_kernel", "wkv7_bwd_kernel", "wkv7_infer_kernel", "AbsFunctor")
+    keys = ("wkv7_fwd_chunk_kernel", "wkv7_bwd_chunk_kernel", "wkv7_fwd_kernel",
+            "wkv7_bwd_kernel", "wkv7_infer_kernel", "AbsFunctor")
     per = defaultdict(lambda: defaultdict(lambda: defaultdict(float)))
     for d in dirs:
         for path in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
@@ -232,6 +236,10 @@ def bench_train(cfg, steps, warmup, with_cpu, probe=False):
     # out + 1/16 of a checkpoint; bwd 7 vectors + sa in, 6 gradients out,
     # 1/16 of a checkpoint in
     e = 2 if io == torch.bfloat16 else 4
+    # which kernels ran (launch_forward / launch_backward dispatch)
+    chunked = (io == torch.bfloat16 and C == 16 and T % 16 == 0
+               and os.environ.get("WKV7_BF16_PATH") != "valu")
+    bwd_kernel = "wkv7_bwd_chunk_kernel" if chunked else "wkv7_bwd_kernel"
     fwd_bytes = head_steps * (7 * N_HEAD * e + N_HEAD * 4 + N_HEAD * N_HEAD * 4 / C)
     bwd_bytes = head_steps * (13 * N_HEAD * e + N_HEAD * 4 + N_HEAD * N_HEAD * 4 / C)
     out = {
@@ -250,11 +258,13 @@ def bench_train(cfg, steps, warmup, with_cpu, probe=False):
         "config": {"workload": "wkv7_statepass_fwd_bwd", "batch": B, "context_len": T,
                    "num_heads": H, "head_size": N_HEAD, "chunk_len": C, "io_dtype": cfg["io"],
                    "state_dtype": "f32", "initial_state_std": cfg["s0_std"]},
-        "roofline": {"bound": "valu", "kernel": "wkv7_bwd_kernel", "achieved": achieved / 1e12,
+        "roofline": {"bound": "mfma" if chunked else "valu", "kernel": bwd_kernel,
+                     "achieved": achieved / 1e12,
                      "peak": PEAK_FP32 / 1e12, "unit": "TFLOP/s", "frac": achieved / PEAK_FP32,
-                     "traffic": recorded_traffic("wkv7_bwd_kernel"),
+                     "traffic": recorded_traffic(bwd_kernel),
                      "algorithmic_bytes": bwd_bytes,
                      "flop_per_launch": bwd_flops, "launch_ms": bwd_ms},
+        "kernels": "chunked-mfma" if chunked else "step-valu",
         "fwd_ms": fwd_ms,
         "bwd_ms": bwd_ms,
         "fwd_roofline_frac": fwd_flops / (fwd_ms * 1e-3) / PEAK_FP32,

@@ -27,7 +27,7 @@
 // previous checkpoint.
 //
 // Work layout: one workgroup of four waves per (batch, head), chunks in
-// reverse order, the next chunk's inputs streaming into LDS meanwhile. Per
+// reverse order, the next chunk's inputs loaded into registers meanwhile. Per
 // chunk: (1) wave w computes decays and the split A^, R^, K~, B~ rows for keys
 // 16w..16w+15; (2) wave w computes one of the four step-by-step products of
 // decayed vectors; (3) wave 0 forms P by substitution while the others form
@@ -48,6 +48,8 @@ enum { I_X, I_R, I_K, I_A, I_B, I_V, I_DY, I_COUNT };          // staged bf16 ro
 enum { T_AH, T_AL, T_RH, T_RL, T_KH, T_KL, T_BH, T_BL, T_COUNT };   // decayed rows, hi/lo
 enum { F_AKT, F_RBT, F_RKT, F_PT, F_BYV, F_CDYV, F_BYSA, F_CDYSA, F_BSAV, F_CDSAV,
        F_BSASA, F_CDSASA, F_COUNT };                             // stacked 16x16 operands
+enum { O_DV, O_DK, O_DB, O_DR, O_DA, O_DW, O_COUNT };          // staged gradient tiles
+constexpr int kOutRounds = O_COUNT * kL * 8 / (64 * 4);            // 16-byte stores per thread
 constexpr int kBf16Pieces = I_COUNT * kL * 8;                    // 16-byte pieces per chunk
 constexpr int kBf16Rounds = (kBf16Pieces + kBlock - 1) / kBlock;
 constexpr float kSigFromLw2 = 1.0f / (kWScale * kLog2e);        // sigmoid = lw2 * this
@@ -66,6 +68,7 @@ struct BwdLds {
   float s0r[64][68];                // chunk 0's rebuilt start state, [key i][value j]
   float e3[kWaves][64];             // per-wave partial of sum_j S0 o dS'
   float red[kWaves][2][4][16];      // cross-quad scratch of the key-gradient waves
+  bf16_t outs[O_COUNT][kL][64];     // a chunk's bf16 gradients, written out as whole rows
 };
 
 struct BwdChunkParams {
@@ -104,7 +107,8 @@ __device__ __forceinline__ f32x4 gram_x3(const Split8 (&a)[2], const Split8 (&b)
 
 __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChunkParams p) {
   __shared__ BwdLds L;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
   const int t = lane & 15, qd = lane >> 4;
   const int h = blockIdx.x, b = blockIdx.y, H = p.H, T = p.T;
   const int64_t bh = (int64_t)b * H + h;
@@ -113,24 +117,38 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
   const int nchunks = T / kL;
   const float* const ckbh = p.ckpt + bh * nchunks * (kHead * kHead);
 
-  // ---- staging of chunk c into buffer sb: bf16 rows as rotated 16-byte
-  // pieces (piece p = row p / 8, slot p % 8), removal_state rows as 16-byte
-  // pieces rotated over 16 slots
-  auto issue = [&](int c, int sb) {
+  // ---- staging of chunk c: thread tid moves 16-byte pieces, through
+  // registers (loaded early, written to the free LDS buffer at the chunk's
+  // end). bf16 rows as rotated pieces (piece p = 256 k + tid is row p / 8,
+  // slot p % 8), removal_state rows as pieces rotated over 16 slots.
+  struct Pre { uint4 v[kBf16Rounds + 1]; };
+  // piece 256 k + tid lies in row (256 k + tid) / 8 of input 2 k + wave / 2:
+  // the input index is wave-uniform, so its pointer stays in scalar registers
+  auto fetch = [&](int c) {
+    Pre pr;
 #pragma unroll
     for (int k = 0; k < kBf16Rounds; ++k) {
       const int pc = kBlock * k + tid;
+      pr.v[k] = make_uint4(0, 0, 0, 0);
       if (kBlock * k + 64 * wave < kBf16Pieces) {
-        const int row = pc >> 3, slot = pc & 7, vec = row >> 4, st = row & 15;
-        const bf16_t* src = p.in[vec] + tok0 + (int64_t)(kL * c + st) * tstride + 8 * ((slot - st) & 7);
-        load_lds16(src, reinterpret_cast<char*>(&L.stg[sb][0][0][0]) + (kBlock * k + 64 * wave) * 16);
+        const int vec = 2 * k + (wave >> 1);
+        const int slot = pc & 7, st = (pc >> 3) & 15;
+        pr.v[k] = *reinterpret_cast<const uint4*>(
+            p.in[vec] + tok0 + (int64_t)(kL * c + st) * tstride + 8 * ((slot - st) & 7));
       }
     }
-    {
-      const int st = tid >> 4, slot = tid & 15;
-      const float* src = p.sa + tok0 + (int64_t)(kL * c + st) * tstride + 4 * ((slot - st) & 15);
-      load_lds16(src, reinterpret_cast<char*>(&L.sast[sb][0][0]) + 64 * wave * 16);
+    const int st = tid >> 4, slot = tid & 15;
+    pr.v[kBf16Rounds] = *reinterpret_cast<const uint4*>(
+        p.sa + tok0 + (int64_t)(kL * c + st) * tstride + 4 * ((slot - st) & 15));
+    return pr;
+  };
+  auto stage_in = [&](const Pre pr, int sb) {
+#pragma unroll
+    for (int k = 0; k < kBf16Rounds; ++k) {
+      const int pc = kBlock * k + tid;
+      if (kBlock * k + 64 * wave < kBf16Pieces) reinterpret_cast<uint4*>(&L.stg[sb][0][0][0])[pc] = pr.v[k];
     }
+    reinterpret_cast<uint4*>(&L.sast[sb][0][0])[tid] = pr.v[kBf16Rounds];
   };
 
   // ---- state gradient: value tile jb = wave, key tiles ib, result layout
@@ -146,29 +164,46 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
   }
   const int ki = 16 * wave + t;   // key of the lane in the key-gradient stage (column of its tile)
 
-  issue(nchunks - 1, (nchunks - 1) & 1);
-  for (int c = nchunks - 1; c >= 0; --c) {
-    const int sb = c & 1;
-    const bf16_t (*const stg)[kL][64] = L.stg[sb];
-    const float (*const sast)[64] = L.sast[sb];
-    // start state S0 of the chunk: result-layout tiles for sum_j S0 o dS', and
-    // the rows [key ki][value 32 m + 4 qd .. , + 16 ..] for the key stage
-    f32x4 S0t[4];
-    f32x4 S0row[2][2];
+  // start state S0 of chunk c (the checkpoint of chunk c - 1): result-layout
+  // tiles for sum_j S0 o dS', and the rows [key ki][value 32 m + 4 qd .., + 16
+  // ..] for the key stage. Loaded one chunk ahead, after the staging loads.
+  f32x4 S0t[4], S0row[2][2], S0t_n[4], S0row_n[2][2];
+  auto load_s0 = [&](int c, f32x4 (&tiles)[4], f32x4 (&rowv)[2][2]) {
     if (c > 0) {
       const float* ck = ckbh + (int64_t)(c - 1) * (kHead * kHead);
 #pragma unroll
       for (int ib = 0; ib < 4; ++ib)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) S0t[ib][r] = ck[(16 * ib + 4 * qd + r) * kHead + jcol];
+        for (int r = 0; r < 4; ++r) tiles[ib][r] = ck[(16 * ib + 4 * qd + r) * kHead + jcol];
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
-        S0row[m][0] = *reinterpret_cast<const f32x4*>(ck + ki * kHead + 32 * m + 4 * qd);
-        S0row[m][1] = *reinterpret_cast<const f32x4*>(ck + ki * kHead + 32 * m + 16 + 4 * qd);
+        rowv[m][0] = *reinterpret_cast<const f32x4*>(ck + ki * kHead + 32 * m + 4 * qd);
+        rowv[m][1] = *reinterpret_cast<const f32x4*>(ck + ki * kHead + 32 * m + 16 + 4 * qd);
       }
     }
-    wait_vmcnt<0>();
+  };
+
+  // the staged gradient tiles of chunk cc to memory: thread tid writes
+  // 16-byte pieces p = 256 k + tid (tile p / 128, row (p / 8) % 16)
+  bf16_t* const outp[O_COUNT] = {p.dv, p.dk, p.db, p.dr, p.da, p.dw};
+  auto flush = [&](int cc) {
+#pragma unroll
+    for (int k = 0; k < kOutRounds; ++k) {
+      const int pc = kBlock * k + tid, tile = pc >> 7, row = (pc >> 3) & 15, piece = pc & 7;
+      const uint4 v = *reinterpret_cast<const uint4*>(&L.outs[tile][row][8 * piece]);
+      *reinterpret_cast<uint4*>(outp[tile] + tok0 + (int64_t)(kL * cc + row) * tstride + 8 * piece) = v;
+    }
+  };
+
+  if (nchunks > 0) stage_in(fetch(nchunks - 1), (nchunks - 1) & 1);
+  Pre pre;
+  load_s0(nchunks - 1, S0t, S0row);
+  for (int c = nchunks - 1; c >= 0; --c) {
+    const int sb = c & 1;
+    const bf16_t (*const stg)[kL][64] = L.stg[sb];
+    const float (*const sast)[64] = L.sast[sb];
     lds_barrier();
+    if (c < nchunks - 1) flush(c + 1);   // gradients of the previous chunk
 
     // ================= (1) decays and decayed rows, keys 16 wave .. + 15
     {
@@ -213,7 +248,10 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
       if (t == 0) *reinterpret_cast<f32x4*>(&L.gl[c0]) = f32x4{gL[0], gL[1], gL[2], gL[3]};
     }
     lds_barrier();
-    if (c > 0) issue(c - 1, sb ^ 1);
+    if (c > 0) {
+      pre = fetch(c - 1);
+      load_s0(c - 1, S0t_n, S0row_n);
+    }
 
     // ================= (2) step-by-step products of decayed rows, one per wave
     {
@@ -353,9 +391,8 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
       dv = mma32x3(Kt1, Sx1, dv);
       dv = mma_s2(L.frag[F_RKT][lane], dycf, dv);
       dv = mma_s3(L.frag[F_AKT][lane], dsas, dv);
-      bf16_t* dvc = p.dv + tok0 + (int64_t)kL * c * tstride + jcol;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) dvc[(4 * qd + r) * tstride] = __builtin_bit_cast(bf16_t, (__bf16)dv[r]);
+      for (int r = 0; r < 4; ++r) L.outs[O_DV][4 * qd + r][jcol] = __builtin_bit_cast(bf16_t, (__bf16)dv[r]);
       // carried gradient dS0^T = dS'^T + R^^T dY + A^^T dSA
 #pragma unroll
       for (int ib = 0; ib < 4; ++ib) {
@@ -528,21 +565,32 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
       }
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) etot += L.e3[w][ki];
-      const int64_t off = tok0 + (int64_t)(kL * c + 4 * qd) * tstride + ki;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const float dlw = suf[r] + above - ad[r] + etot;
         const float dwv = dlw * kWScale * sig[r] * (1.0f - sig[r]);
-        const int64_t o = off + r * tstride;
-        p.dk[o] = __builtin_bit_cast(bf16_t, (__bf16)dk[r]);
-        p.db[o] = __builtin_bit_cast(bf16_t, (__bf16)dbv[r]);
-        p.dr[o] = __builtin_bit_cast(bf16_t, (__bf16)dr[r]);
-        p.da[o] = __builtin_bit_cast(bf16_t, (__bf16)da[r]);
-        p.dw[o] = __builtin_bit_cast(bf16_t, (__bf16)dwv);
+        const int tr = 4 * qd + r;
+        L.outs[O_DK][tr][ki] = __builtin_bit_cast(bf16_t, (__bf16)dk[r]);
+        L.outs[O_DB][tr][ki] = __builtin_bit_cast(bf16_t, (__bf16)dbv[r]);
+        L.outs[O_DR][tr][ki] = __builtin_bit_cast(bf16_t, (__bf16)dr[r]);
+        L.outs[O_DA][tr][ki] = __builtin_bit_cast(bf16_t, (__bf16)da[r]);
+        L.outs[O_DW][tr][ki] = __builtin_bit_cast(bf16_t, (__bf16)dwv);
       }
+    }
+    if (c > 0) stage_in(pre, sb ^ 1);   // next chunk's rows into the free buffer
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib) S0t[ib] = S0t_n[ib];
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      S0row[m][0] = S0row_n[m][0];
+      S0row[m][1] = S0row_n[m][1];
     }
   }
 
+  if (nchunks > 0) {
+    lds_barrier();
+    flush(0);
+  }
   if (p.ds0) {
 #pragma unroll
     for (int ib = 0; ib < 4; ++ib)

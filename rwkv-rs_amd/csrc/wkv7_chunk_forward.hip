@@ -297,7 +297,12 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_fwd_chunk_kernel(const FwdChun
   issue(0);
   for (int n = 0; n < nbatches; ++n) {
     const int nq = min(kBatch, nchunks - kBatch * n);
-    wait_vmcnt<0>();
+    // this batch's staging loads were followed by the previous batch's stores,
+    // at least 24 per chunk (sa 4, y 4, checkpoint 16); vector memory
+    // operations retire in order, so at most 20 outstanding means the loads
+    // have landed while the stores keep flying
+    if (n == 0) wait_vmcnt<0>();
+    else wait_vmcnt<20>();
     lds_barrier();
     if (wave < nq) prepare_chunk(stg, wave, scr[wave], ops[wave], lane);
     lds_barrier();   // chunk operands visible; staging free
