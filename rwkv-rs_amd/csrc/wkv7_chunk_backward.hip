@@ -62,11 +62,10 @@ struct BwdLds {
   float lwT[64][kL + 4];            // log2 step decay, [key][step]
   float gl[64];                     // gamma_L
   bf16x8 frag[F_COUNT][64];         // 16x16 step-by-step operands, stacked (hi | lo)
-  float amat[kL][kL];               // A_ab for the substitution
+  float amat[kL][kL];               // A_ab transposed, [s][t], for the substitution
   bf16_t xds[2][64][64];            // dS' hi/lo, [value j][key i]
   bf16_t xdsa[2][64][kL];           // dSA hi/lo, [value j][step t]
   float s0r[64][68];                // chunk 0's rebuilt start state, [key i][value j]
-  float e3[kWaves][64];             // per-wave partial of sum_j S0 o dS'
   float red[kWaves][2][4][16];      // cross-quad scratch of the key-gradient waves
   bf16_t outs[O_COUNT][kL][64];     // a chunk's bf16 gradients, written out as whole rows
 };
@@ -164,17 +163,13 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
   }
   const int ki = 16 * wave + t;   // key of the lane in the key-gradient stage (column of its tile)
 
-  // start state S0 of chunk c (the checkpoint of chunk c - 1): result-layout
-  // tiles for sum_j S0 o dS', and the rows [key ki][value 32 m + 4 qd .., + 16
-  // ..] for the key stage. Loaded one chunk ahead, after the staging loads.
-  f32x4 S0t[4], S0row[2][2], S0t_n[4], S0row_n[2][2];
-  auto load_s0 = [&](int c, f32x4 (&tiles)[4], f32x4 (&rowv)[2][2]) {
+  // start state S0 of chunk c (the checkpoint of chunk c - 1) as the rows
+  // [key ki][value 32 m + 4 qd .., + 16 ..] of the key stage, loaded one chunk
+  // ahead, after the staging loads
+  f32x4 S0row[2][2], S0row_n[2][2];
+  auto load_s0 = [&](int c, f32x4 (&rowv)[2][2]) {
     if (c > 0) {
       const float* ck = ckbh + (int64_t)(c - 1) * (kHead * kHead);
-#pragma unroll
-      for (int ib = 0; ib < 4; ++ib)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) tiles[ib][r] = ck[(16 * ib + 4 * qd + r) * kHead + jcol];
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
         rowv[m][0] = *reinterpret_cast<const f32x4*>(ck + ki * kHead + 32 * m + 4 * qd);
@@ -197,7 +192,7 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
 
   if (nchunks > 0) stage_in(fetch(nchunks - 1), (nchunks - 1) & 1);
   Pre pre;
-  load_s0(nchunks - 1, S0t, S0row);
+  load_s0(nchunks - 1, S0row);
   for (int c = nchunks - 1; c >= 0; --c) {
     const int sb = c & 1;
     const bf16_t (*const stg)[kL][64] = L.stg[sb];
@@ -250,7 +245,7 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
     lds_barrier();
     if (c > 0) {
       pre = fetch(c - 1);
-      load_s0(c - 1, S0t_n, S0row_n);
+      load_s0(c - 1, S0row_n);
     }
 
     // ================= (2) step-by-step products of decayed rows, one per wave
@@ -261,13 +256,13 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
           o[m] = Split8{row_frag(L.rows[th], t, m, qd), row_frag(L.rows[tl], t, m, qd)};
       };
       Split8 X[2], Y[2];
-      if (wave == 0) {          // A_ab, transposed, for the substitution
-        rowpair(T_BH, T_BL, X);
-        rowpair(T_AH, T_AL, Y);
-        f32x4 d = gram_x3(X, Y);   // [s][t] = b~_s . a^_t
+      if (wave == 0) {          // A_ab for the substitution, stored by columns
+        rowpair(T_AH, T_AL, X);
+        rowpair(T_BH, T_BL, Y);
+        f32x4 d = gram_x3(X, Y);   // [t'][s] = a^_t' . b~_s, lane column s = t
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          if (!(4 * qd + r < t)) d[r] = 0.f;
+          if (!(t < 4 * qd + r)) d[r] = 0.f;
         *reinterpret_cast<f32x4*>(&L.amat[t][4 * qd]) = d;
       } else {
         const int ta = wave == 1 ? T_AH : T_RH;
@@ -287,18 +282,20 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
 
     // ================= (3) P by substitution (wave 0); raw step products
     if (wave == 0) {
+      // column t of P = (I - A_ab)^-1, column-oriented: once pc[s] is final,
+      // it updates every later row, so the dependent chain is 15 FMAs long
       float pc[kL];
 #pragma unroll
-      for (int tt = 0; tt < kL; ++tt) {
-        float acc = (tt == t) ? 1.0f : 0.0f;
+      for (int tt = 0; tt < kL; ++tt) pc[tt] = (tt == t) ? 1.0f : 0.0f;
 #pragma unroll
-        for (int s4 = 0; s4 < tt; s4 += 4) {
-          const f32x4 arow = *reinterpret_cast<const f32x4*>(&L.amat[tt][s4]);
+      for (int s = 0; s < kL - 1; ++s) {
+#pragma unroll
+        for (int t4 = (s + 1) & ~3; t4 < kL; t4 += 4) {
+          const f32x4 acol = *reinterpret_cast<const f32x4*>(&L.amat[s][t4]);
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            if (s4 + e < tt) acc += arow[e] * pc[s4 + e];
+            if (t4 + e > s) pc[t4 + e] += acol[e] * pc[s];
         }
-        pc[tt] = acc;
       }
       // P^T as an A operand: lane l holds P[4 qd + e][l % 16], this lane's column
       f32x4 pt;
@@ -348,6 +345,7 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
       // rebuild S0 by reversing the chunk's 16 steps from its checkpoint
       // (kernel.rs:239-246): S_{t-1} = (S_t - v_t k_t^T - sa_t b_t^T) / w~_t
       const float* ck = ckbh;
+      f32x4 S0t[4];
 #pragma unroll
       for (int ib = 0; ib < 4; ++ib)
 #pragma unroll
@@ -412,16 +410,6 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
         }
       *reinterpret_cast<bf16x4*>(&L.xdsa[0][jcol][4 * qd]) = dsas.hi;
       *reinterpret_cast<bf16x4*>(&L.xdsa[1][jcol][4 * qd]) = dsas.lo;
-      // sum over this wave's values of S0 o dS', per key
-#pragma unroll
-      for (int ib = 0; ib < 4; ++ib) {
-        float prod[4], e[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) prod[r] = S0t[ib][r] * dSp[ib][r];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) e[r] = row_sum16(prod[r]);
-        if (t == 0) *reinterpret_cast<f32x4*>(&L.e3[wave][16 * ib + 4 * qd]) = f32x4{e[0], e[1], e[2], e[3]};
-      }
     }
     lds_barrier();
 
@@ -507,11 +495,22 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
       x1 = mma32(v1, Db[1].hi, x1);
       f32x4 x2 = mma32x3(s0f, Db[0], z);
       x2 = mma32x3(s1f, Db[1], x2);
-      // sum over the chunk's steps of K~ o V dS' + B~ o SA dS'
+      // sum over the chunk's steps of K~ o V dS' + B~ o SA dS', and over this
+      // lane's 16 values j of S0 o dS' (S0 and dS' hold the same j per element)
       float epart = 0.f;
 #pragma unroll
       for (int r = 0; r < 4; ++r)
         epart += ((float)Kc.hi[r] + (float)Kc.lo[r]) * x1[r] + ((float)Bc.hi[r] + (float)Bc.lo[r]) * x2[r];
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          const bf16x2 sh = {S0b[m].hi[e], S0b[m].hi[e + 1]}, sl = {S0b[m].lo[e], S0b[m].lo[e + 1]};
+          const bf16x2 dh = {Db[m].hi[e], Db[m].hi[e + 1]}, dl = {Db[m].lo[e], Db[m].lo[e + 1]};
+          epart = __builtin_amdgcn_fdot2_f32_bf16(sh, dh, epart, false);
+          epart = __builtin_amdgcn_fdot2_f32_bf16(sh, dl, epart, false);
+          epart = __builtin_amdgcn_fdot2_f32_bf16(sl, dh, epart, false);
+        }
       f32x4 dk = mma_s3(L.frag[F_BYV][lane], Rc, x1);
       dk = mma_s3(L.frag[F_BSAV][lane], Ac, dk);
       f32x4 dbv = mma_s3(L.frag[F_BYSA][lane], Rc, x2);
@@ -564,8 +563,6 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
         etot += L.red[wave][1][q][t];
       }
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) etot += L.e3[w][ki];
-#pragma unroll
       for (int r = 0; r < 4; ++r) {
         const float dlw = suf[r] + above - ad[r] + etot;
         const float dwv = dlw * kWScale * sig[r] * (1.0f - sig[r]);
@@ -578,8 +575,6 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
       }
     }
     if (c > 0) stage_in(pre, sb ^ 1);   // next chunk's rows into the free buffer
-#pragma unroll
-    for (int ib = 0; ib < 4; ++ib) S0t[ib] = S0t_n[ib];
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
       S0row[m][0] = S0row_n[m][0];
