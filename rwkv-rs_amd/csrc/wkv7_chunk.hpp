@@ -127,6 +127,29 @@ __device__ __forceinline__ f32x4 mma_s3(bf16x8 a_stacked, const Split4& b, f32x4
   return mma32(a_stacked, twice(b.hi), c);
 }
 
+// X Y in the result layout from X^T and Y in the result layout (lane l holds
+// M[4 qd + r][l % 16]): X^T's lanes are X as an A operand, Y's are Y as a B
+// operand; split-bf16 product, contraction length 16
+__device__ __forceinline__ f32x4 mma_tiles(f32x4 xt, f32x4 y, f32x4 c) {
+  return mma_s3(stack(split4(xt)), split4(y), c);
+}
+// P = (I - A)^-1 for a strictly lower triangular 16x16 A, from A and A^T in
+// the result layout (t = l % 16, qd = l / 16); P in the result layout. Since
+// A^16 = 0, P = (I + A)(I + A^2)(I + A^4)(I + A^8): five dependent products,
+// all operands in registers.
+__device__ __forceinline__ f32x4 unit_lower_inverse(f32x4 a, f32x4 at, int t, int qd) {
+  const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+  f32x4 id;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) id[r] = (4 * qd + r == t) ? 1.0f : 0.0f;
+  const f32x4 a2 = mma_tiles(at, a, z), a2t = mma_tiles(a, at, z);
+  const f32x4 a4 = mma_tiles(a2t, a2, z), a4t = mma_tiles(a2, a2t, z);
+  const f32x4 a8 = mma_tiles(a4t, a4, z);
+  const f32x4 qt = mma_tiles(a2, at, id + at + a2t);   // ((I + A)(I + A^2))^T
+  const f32x4 r = mma_tiles(a4t, a8, id + a4 + a8);    // (I + A^4)(I + A^8)
+  return mma_tiles(qt, r, z);
+}
+
 // B operand of the 16x16 identity: multiplying an A fragment by it returns
 // the same 16x16 tile in the result layout, i.e. with rows and lanes swapped.
 // Exact for bf16 inputs.
@@ -153,14 +176,18 @@ __device__ __forceinline__ bf16x4 read_tr16(const void* lds) {
 }
 
 // A tile of bf16 rows (64 columns) in LDS with each row's eight 16-byte
-// pieces rotated by the row index: element (row, c) lives in piece
-// (c / 8 + row) % 8. Reads of 8 bytes from 16 consecutive rows then spread
-// over the banks.
+// pieces rotated: element (row, c) lives in piece (c / 8 + rot(row)) % 8,
+// rot(row) = row + row / 8. The LDS (64 banks of 4 bytes) serves 32 lanes of
+// an 8-byte read per cycle; with this rotation both 8-byte row reads of 16
+// consecutive rows (the same piece of every row) and the transposed reads
+// (32 bytes of 8 consecutive rows) hit every bank once (measured: no bank
+// conflicts, where rot(row) = row gives two-way conflicts on the row reads).
+__device__ __forceinline__ int tile_rot(int row) { return row + (row >> 3); }
 __device__ __forceinline__ bf16_t* tile_at(bf16_t (*tile)[64], int row, int c) {
-  return &tile[row][8 * (((c >> 3) + row) & 7) + (c & 7)];
+  return &tile[row][8 * (((c >> 3) + tile_rot(row)) & 7) + (c & 7)];
 }
 __device__ __forceinline__ const bf16_t* tile_at(const bf16_t (*tile)[64], int row, int c) {
-  return &tile[row][8 * (((c >> 3) + row) & 7) + (c & 7)];
+  return &tile[row][8 * (((c >> 3) + tile_rot(row)) & 7) + (c & 7)];
 }
 __device__ __forceinline__ bf16x4 read4(const bf16_t (*tile)[64], int row, int c) {
   return *reinterpret_cast<const bf16x4*>(tile_at(tile, row, c));

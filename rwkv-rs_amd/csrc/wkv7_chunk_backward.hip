@@ -27,13 +27,24 @@
 // previous checkpoint.
 //
 // Work layout: one workgroup of four waves per (batch, head), chunks in
-// reverse order, the next chunk's inputs loaded into registers meanwhile. Per
-// chunk: (1) wave w computes decays and the split A^, R^, K~, B~ rows for keys
-// 16w..16w+15; (2) wave w computes one of the four step-by-step products of
-// decayed vectors; (3) wave 0 forms P by substitution while the others form
-// the step-by-step products of the raw inputs; (4) wave w carries the state
-// gradient for value columns 16w..16w+15 and writes dV; (5) the products with
-// dSA; (6) wave w computes the key-indexed gradients for keys 16w..16w+15.
+// reverse order. Only the state gradient is carried from chunk to chunk; the
+// per-chunk set-up that does not depend on it (decays, decayed rows, their
+// step-by-step products, P) is computed one chunk ahead, next to the current
+// chunk's gradients, so each phase gives every wave independent streams:
+//   phase A: state-gradient chain and dV of chunk c (wave w: value columns
+//            16w..16w+15) | decays and decayed rows of chunk c-1 (wave w:
+//            keys 16w..16w+15) | step products of v, dy, sa of chunk c
+//   phase B: step products with dSA of chunk c | step products of the
+//            decayed rows of chunk c-1
+//   phase C: key-indexed gradients of chunk c (wave w: keys 16w..16w+15) |
+//            P = (I - A_ab)^-1 of chunk c-1 on the matrix cores (every wave)
+// Within a phase each wave first issues all its LDS reads, then computes.
+// Inputs are staged through registers, loaded in phase A and written to LDS
+// in phase B: the rows only the decays read (x, r, k, a, b) in one buffer,
+// two chunks ahead; v, dy and the removal_state (split into bf16 hi/lo rows
+// once, when staged) in two, one chunk ahead.
+#include <type_traits>
+
 #include "wkv7_chunk.hpp"
 #include "wkv7_launch.hpp"
 
@@ -44,31 +55,44 @@ using namespace chunk;
 
 constexpr int kWaves = 4;
 constexpr int kBlock = 64 * kWaves;
-enum { I_X, I_R, I_K, I_A, I_B, I_V, I_DY, I_COUNT };          // staged bf16 rows
+enum { I_X, I_R, I_K, I_A, I_B, I_V, I_DY, I_COUNT };   // input tensors
+constexpr int kDecayIn = 5;                             // I_X..I_B: read by the decays only
+enum { S_V, S_DY, S_SAH, S_SAL, S_COUNT };              // rows read by the gradients
 enum { T_AH, T_AL, T_RH, T_RL, T_KH, T_KL, T_BH, T_BL, T_COUNT };   // decayed rows, hi/lo
-enum { F_AKT, F_RBT, F_RKT, F_PT, F_BYV, F_CDYV, F_BYSA, F_CDYSA, F_BSAV, F_CDSAV,
-       F_BSASA, F_CDSASA, F_COUNT };                             // stacked 16x16 operands
-enum { O_DV, O_DK, O_DB, O_DR, O_DA, O_DW, O_COUNT };          // staged gradient tiles
-constexpr int kOutRounds = O_COUNT * kL * 8 / (64 * 4);            // 16-byte stores per thread
-constexpr int kBf16Pieces = I_COUNT * kL * 8;                    // 16-byte pieces per chunk
-constexpr int kBf16Rounds = (kBf16Pieces + kBlock - 1) / kBlock;
+enum { F_AKT, F_RBT, F_RKT, F_PT, F_COUNT };            // stacked operands from the decayed rows
+enum { G_BYV, G_CDYV, G_BYSA, G_CDYSA, G_BSAV, G_CDSAV, G_BSASA, G_CDSASA, G_COUNT };
+enum { O_DV, O_DK, O_DB, O_DR, O_DA, O_DW, O_COUNT };   // staged gradient tiles
+constexpr int kOutRounds = O_COUNT * kL * 8 / kBlock;          // 16-byte stores per thread
+constexpr int kDecayPieces = kDecayIn * kL * 8;                // 16-byte pieces per chunk
+constexpr int kDecayRounds = (kDecayPieces + kBlock - 1) / kBlock;
 constexpr float kSigFromLw2 = 1.0f / (kWScale * kLog2e);        // sigmoid = lw2 * this
+static_assert(2 * kL * 8 == kBlock, "v and dy rows: one 16-byte piece per thread");
+static_assert(kL * 16 == kBlock, "removal_state rows: four values per thread");
+static_assert(O_COUNT * kL * 8 % kBlock == 0, "whole rounds of gradient stores");
 
-struct BwdLds {
-  bf16_t stg[2][I_COUNT][kL][64];   // raw rows of a chunk, double-buffered
-  float sast[2][kL][64];            // removal_state rows, 16-byte pieces rotated by row
-  bf16_t rows[T_COUNT][kL][64];     // decayed rows
+// per-chunk set-up, double-buffered (chunk c & 1)
+struct Prep {
+  bf16_t rows[T_COUNT][kL][64];     // decayed rows, rotated
   float gT[64][kL + 4];             // log2 prefix decay, [key][step]
   float lwT[64][kL + 4];            // log2 step decay, [key][step]
   float gl[64];                     // gamma_L
-  bf16x8 frag[F_COUNT][64];         // 16x16 step-by-step operands, stacked (hi | lo)
-  float amat[kL][kL];               // A_ab transposed, [s][t], for the substitution
+  f32x4 amat[2][64];                // A_ab and A_ab^T, result layout
+  bf16x8 frag[F_COUNT][64];         // stacked 16x16 operands
+};
+
+struct BwdLds {
+  bf16_t dec[kDecayIn][kL][64];     // x, r, k, a, b rows of the next chunk to set up
+  bf16_t stg[2][S_COUNT][kL][64];   // v, dy, sa hi, sa lo rows, double-buffered
+  Prep prep[2];                     // chunk 0 also keeps its rebuilt start state in prep[1]
+  bf16x8 frag[G_COUNT][64];         // step products with v, dy, sa, dsa (stacked)
   bf16_t xds[2][64][64];            // dS' hi/lo, [value j][key i]
   bf16_t xdsa[2][64][kL];           // dSA hi/lo, [value j][step t]
-  float s0r[64][68];                // chunk 0's rebuilt start state, [key i][value j]
   float red[kWaves][2][4][16];      // cross-quad scratch of the key-gradient waves
-  bf16_t outs[O_COUNT][kL][64];     // a chunk's bf16 gradients, written out as whole rows
+  bf16_t outs[O_COUNT][kL][64];     // a chunk's bf16 gradients, written out as whole rows (out_at)
+  bf16_t zero[kL][64];              // an all-zero row tile
 };
+typedef float S0Rows[64][68];       // chunk 0's rebuilt start state, [key i][value j]
+static_assert(sizeof(S0Rows) <= sizeof(Prep), "start state fits the free set-up buffer");
 
 struct BwdChunkParams {
   const bf16_t* in[I_COUNT];   // [B,T,H,64] each
@@ -85,15 +109,18 @@ struct BwdChunkParams {
   int T, H;
 };
 
-__device__ __forceinline__ float sa_at(const float (*rows)[64], int t, int c) {
-  return rows[t][4 * (((c >> 2) + t) & 15) + (c & 3)];
+// element (row, key) of a staged gradient tile: 16-byte pieces rotated by
+// two per group of four rows, so the four quads of a wave, which write rows
+// 4 qd + r, hit disjoint banks
+__device__ __forceinline__ bf16_t& out_at(bf16_t (*tile)[64], int row, int key) {
+  return tile[row][8 * (((key >> 3) + 2 * ((row >> 2) & 3)) & 7) + (key & 7)];
 }
-__device__ __forceinline__ f32x4 sa_read4(const float (*rows)[64], int t, int c) {
-  return *reinterpret_cast<const f32x4*>(&rows[t][4 * (((c >> 2) + t) & 15)]);
-}
-// x32 fragment of the lane's removal_state row, split
-__device__ __forceinline__ Split8 sa_frag(const float (*rows)[64], int t, int m, int qd) {
-  return split8(sa_read4(rows, t, 32 * m + 4 * qd), sa_read4(rows, t, 32 * m + 16 + 4 * qd));
+// 4-value piece q (steps 4 q .. 4 q + 3) of row j of a dSA exchange tile
+// ([value j][step], 32-byte rows): pieces rotated by (j / 8) % 4, so the
+// writes of 16 consecutive rows spread over the banks (unrotated: four-way
+// conflicts), while the transposed reads still take 4 whole rows per 16 lanes
+__device__ __forceinline__ bf16_t* xdsa_at(bf16_t (*tile)[kL], int j, int q) {
+  return &tile[j][4 * ((q + (j >> 3)) & 3)];
 }
 __device__ __forceinline__ f32x4 widen4(bf16x4 x) { return __builtin_convertvector(x, f32x4); }
 __device__ __forceinline__ bf16x8 stack_f(f32x4 x) { return stack(split4(x)); }
@@ -102,6 +129,102 @@ __device__ __forceinline__ f32x4 gram_x3(const Split8 (&a)[2], const Split8 (&b)
   f32x4 c = {0.f, 0.f, 0.f, 0.f};
   c = mma32x3(a[0], b[0], c);
   return mma32x3(a[1], b[1], c);
+}
+__device__ __forceinline__ Split8 row_pair(const bf16_t (*hi)[64], const bf16_t (*lo)[64], int t, int m, int qd) {
+  return Split8{row_frag(hi, t, m, qd), row_frag(lo, t, m, qd)};
+}
+__device__ __forceinline__ float hi_lo(bf16x4 h, bf16x4 l, int r) { return (float)h[r] + (float)l[r]; }
+
+// ---- set-up of one chunk, step 1: decays and decayed rows, keys 16 wave ..
+struct DecayIn { uint2 x; bf16x4 a, r, k, b; };
+__device__ __forceinline__ DecayIn decay_load(const bf16_t (*dec)[kL][64], int wave, int t, int qd) {
+  const int c0 = 16 * wave + 4 * qd;
+  return DecayIn{*reinterpret_cast<const uint2*>(tile_at(dec[I_X], t, c0)), read4(dec[I_A], t, c0),
+                 read4(dec[I_R], t, c0), read4(dec[I_K], t, c0), read4(dec[I_B], t, c0)};
+}
+__device__ __forceinline__ void setup_decays(Prep& P, const DecayIn& in, int wave, int t, int qd) {
+  const int c0 = 16 * wave + 4 * qd;
+  // plain float arrays around the cross-lane (DPP) operations: this compiler
+  // folds DPP builtins whose source is an element of an ext_vector value into
+  // a single one (all elements get element 0's)
+  const uint2 xr = in.x;
+  const float xs[4] = {__uint_as_float(xr.x << 16), __uint_as_float(xr.x & 0xffff0000u),
+                       __uint_as_float(xr.y << 16), __uint_as_float(xr.y & 0xffff0000u)};
+  float g2[4], lw2[4], gam[4], gin[4], gpv[4], gL[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    lw2[e] = log2_decay(xs[e]);
+    g2[e] = row_scan16(lw2[e]);
+    gam[e] = exp2_f(g2[e]);
+    gin[e] = exp2_f(-g2[e]);
+    gpv[e] = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+        __builtin_bit_cast(int, 1.0f), __builtin_bit_cast(int, gam[e]), 0x111, 0xf, 0xf, false));
+    gL[e] = row_last16(gam[e]);
+  }
+  const f32x4 gamv = {gam[0], gam[1], gam[2], gam[3]};
+  const f32x4 ginv = {gin[0], gin[1], gin[2], gin[3]};
+  const f32x4 gpvv = {gpv[0], gpv[1], gpv[2], gpv[3]};
+  const Split4 ah = split4(widen4(in.a) * gpvv);
+  const Split4 rh = split4(widen4(in.r) * gamv);
+  const Split4 kt = split4(widen4(in.k) * ginv);
+  const Split4 bt = split4(widen4(in.b) * ginv);
+  write4(P.rows[T_AH], t, c0, ah.hi);
+  write4(P.rows[T_AL], t, c0, ah.lo);
+  write4(P.rows[T_RH], t, c0, rh.hi);
+  write4(P.rows[T_RL], t, c0, rh.lo);
+  write4(P.rows[T_KH], t, c0, kt.hi);
+  write4(P.rows[T_KL], t, c0, kt.lo);
+  write4(P.rows[T_BH], t, c0, bt.hi);
+  write4(P.rows[T_BL], t, c0, bt.lo);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    P.gT[c0 + e][t] = g2[e];
+    P.lwT[c0 + e][t] = lw2[e];
+  }
+  if (t == 0) *reinterpret_cast<f32x4*>(&P.gl[c0]) = f32x4{gL[0], gL[1], gL[2], gL[3]};
+}
+
+// ---- set-up step 2: one step-by-step product of decayed rows per wave.
+// wave 0: A_ab and A_ab^T (for P = (I - A_ab)^-1, step 3); 1: A_ak^T;
+// 2: A_rb^T; 3: A_rk^T.
+struct GramIn { Split8 X[2], Y[2]; };
+__device__ __forceinline__ GramIn products_load(const Prep& P, int wave, int t, int qd) {
+  const int xa = wave < 2 ? T_AH : T_RH;
+  const int yb = (wave & 1) ? T_KH : T_BH;
+  GramIn g;
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    g.X[m] = row_pair(P.rows[xa], P.rows[xa + 1], t, m, qd);
+    g.Y[m] = row_pair(P.rows[yb], P.rows[yb + 1], t, m, qd);
+  }
+  return g;
+}
+__device__ __forceinline__ void setup_products(Prep& P, const GramIn& g, int wave, int t, int qd, int lane) {
+  const int strict = wave < 2 ? 1 : 0;
+  const Split8 (&X)[2] = g.X;
+  const Split8 (&Y)[2] = g.Y;
+  f32x4 d = gram_x3(X, Y);   // [t'][s] = x_t' . y_s, lane column s = t
+#pragma unroll
+  for (int r = 0; r < 4; ++r) d[r] = 4 * qd + r - t >= strict ? d[r] : 0.f;
+  if (wave == 0) {
+    // d = A_ab[t'][s]; the swapped product is A_ab^T, masked the other way
+    f32x4 dt = gram_x3(Y, X);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) dt[r] = t - (4 * qd + r) >= 1 ? dt[r] : 0.f;
+    P.amat[0][lane] = d;
+    P.amat[1][lane] = dt;
+  } else {
+    P.frag[wave - 1][lane] = stack_f(d);
+  }
+}
+
+// ---- set-up step 3: P = (I - A_ab)^-1 on the matrix cores (registers only,
+// no LDS round trips). Every wave computes it next to its key gradients and
+// stores the same P^T as an A operand (lane l holds P[4 qd + e][l % 16], P's
+// result layout): a store by one wave alone would leave the others nothing to
+// compute and put the whole chain on that wave.
+__device__ __forceinline__ void setup_inverse(Prep& P, f32x4 a, f32x4 at, int t, int qd, int lane) {
+  P.frag[F_PT][lane] = stack_f(unit_lower_inverse(a, at, t, qd));
 }
 
 __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChunkParams p) {
@@ -116,38 +239,42 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
   const int nchunks = T / kL;
   const float* const ckbh = p.ckpt + bh * nchunks * (kHead * kHead);
 
-  // ---- staging of chunk c: thread tid moves 16-byte pieces, through
-  // registers (loaded early, written to the free LDS buffer at the chunk's
-  // end). bf16 rows as rotated pieces (piece p = 256 k + tid is row p / 8,
-  // slot p % 8), removal_state rows as pieces rotated over 16 slots.
-  struct Pre { uint4 v[kBf16Rounds + 1]; };
-  // piece 256 k + tid lies in row (256 k + tid) / 8 of input 2 k + wave / 2:
-  // the input index is wave-uniform, so its pointer stays in scalar registers
-  auto fetch = [&](int c) {
-    Pre pr;
+  // ---- staging through registers. bf16 rows as rotated pieces: piece p =
+  // 256 k + tid is row (p / 8) % 16, slot p % 8 of input p / 128, whose index
+  // is wave-uniform, so its pointer stays in scalar registers. The
+  // removal_state: thread tid holds row tid / 16, values 4 (tid % 16) .. + 3.
+  struct Pre { uint4 dec[kDecayRounds]; uint4 vy; f32x4 sa; };
+  // the sources, chosen once (waves 2 and 3 have no piece in the last decay
+  // round: they load input 4's again and do not stage it)
+  const bf16_t* src[kDecayRounds + 1];
 #pragma unroll
-    for (int k = 0; k < kBf16Rounds; ++k) {
-      const int pc = kBlock * k + tid;
-      pr.v[k] = make_uint4(0, 0, 0, 0);
-      if (kBlock * k + 64 * wave < kBf16Pieces) {
-        const int vec = 2 * k + (wave >> 1);
-        const int slot = pc & 7, st = (pc >> 3) & 15;
-        pr.v[k] = *reinterpret_cast<const uint4*>(
-            p.in[vec] + tok0 + (int64_t)(kL * c + st) * tstride + 8 * ((slot - st) & 7));
-      }
-    }
-    const int st = tid >> 4, slot = tid & 15;
-    pr.v[kBf16Rounds] = *reinterpret_cast<const uint4*>(
-        p.sa + tok0 + (int64_t)(kL * c + st) * tstride + 4 * ((slot - st) & 15));
+  for (int k = 0; k < kDecayRounds; ++k) {
+    const int in = 2 * k + (wave >> 1);
+    src[k] = p.in[in < kDecayIn ? in : kDecayIn - 1] + tok0;
+  }
+  src[kDecayRounds] = p.in[I_V + (wave >> 1)] + tok0;
+  const float* const sa_src = p.sa + tok0 + (int64_t)(tid >> 4) * tstride + 4 * (tid & 15);
+  // piece offset within a chunk: row (tid / 8) % 16, rotated slot
+  const int64_t piece_off = (int64_t)((tid >> 3) & 15) * tstride + 8 * (((tid & 7) - tile_rot((tid >> 3) & 15)) & 7);
+  auto fetch = [&](int cdec, int cg) {   // chunk of the decay rows, chunk of the gradient rows
+    Pre pr;
+    const int64_t od = (int64_t)kL * cdec * tstride + piece_off;
+#pragma unroll
+    for (int k = 0; k < kDecayRounds; ++k) pr.dec[k] = *reinterpret_cast<const uint4*>(src[k] + od);
+    pr.vy = *reinterpret_cast<const uint4*>(src[kDecayRounds] + (int64_t)kL * cg * tstride + piece_off);
+    pr.sa = *reinterpret_cast<const f32x4*>(sa_src + (int64_t)kL * cg * tstride);
     return pr;
   };
-  auto stage_in = [&](const Pre pr, int sb) {
+  auto stage_dec = [&](const Pre& pr) {
 #pragma unroll
-    for (int k = 0; k < kBf16Rounds; ++k) {
-      const int pc = kBlock * k + tid;
-      if (kBlock * k + 64 * wave < kBf16Pieces) reinterpret_cast<uint4*>(&L.stg[sb][0][0][0])[pc] = pr.v[k];
-    }
-    reinterpret_cast<uint4*>(&L.sast[sb][0][0])[tid] = pr.v[kBf16Rounds];
+    for (int k = 0; k < kDecayRounds; ++k)
+      if (2 * k + (wave >> 1) < kDecayIn) reinterpret_cast<uint4*>(&L.dec[0][0][0])[kBlock * k + tid] = pr.dec[k];
+  };
+  auto stage_grad = [&](const Pre& pr, int sb) {
+    reinterpret_cast<uint4*>(&L.stg[sb][0][0][0])[tid] = pr.vy;   // v rows, then dy rows
+    const Split4 s = split4(pr.sa);
+    write4(L.stg[sb][S_SAH], tid >> 4, 4 * (tid & 15), s.hi);
+    write4(L.stg[sb][S_SAL], tid >> 4, 4 * (tid & 15), s.lo);
   };
 
   // ---- state gradient: value tile jb = wave, key tiles ib, result layout
@@ -163,187 +290,80 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
   }
   const int ki = 16 * wave + t;   // key of the lane in the key-gradient stage (column of its tile)
 
-  // start state S0 of chunk c (the checkpoint of chunk c - 1) as the rows
-  // [key ki][value 32 m + 4 qd .., + 16 ..] of the key stage, loaded one chunk
-  // ahead, after the staging loads
-  f32x4 S0row[2][2], S0row_n[2][2];
+  // start state S0 of chunk c >= 1 (the checkpoint of chunk c - 1) as the
+  // rows [key ki][value 32 m + 4 qd .., + 16 ..] of the key stage; loaded at
+  // the start of the chunk, used two phases later
   auto load_s0 = [&](int c, f32x4 (&rowv)[2][2]) {
-    if (c > 0) {
-      const float* ck = ckbh + (int64_t)(c - 1) * (kHead * kHead);
+    const float* ck = ckbh + (int64_t)(c - 1) * (kHead * kHead);
 #pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        rowv[m][0] = *reinterpret_cast<const f32x4*>(ck + ki * kHead + 32 * m + 4 * qd);
-        rowv[m][1] = *reinterpret_cast<const f32x4*>(ck + ki * kHead + 32 * m + 16 + 4 * qd);
-      }
+    for (int m = 0; m < 2; ++m) {
+      rowv[m][0] = *reinterpret_cast<const f32x4*>(ck + ki * kHead + 32 * m + 4 * qd);
+      rowv[m][1] = *reinterpret_cast<const f32x4*>(ck + ki * kHead + 32 * m + 16 + 4 * qd);
     }
   };
 
   // the staged gradient tiles of chunk cc to memory: thread tid writes
   // 16-byte pieces p = 256 k + tid (tile p / 128, row (p / 8) % 16)
-  bf16_t* const outp[O_COUNT] = {p.dv, p.dk, p.db, p.dr, p.da, p.dw};
+  // (tile 2 k + wave / 2 is wave-uniform: the destination is picked by scalar
+  // selects and stays a global pointer)
+  bf16_t* dst[kOutRounds];
+#pragma unroll
+  for (int k = 0; k < kOutRounds; ++k) {
+    const int tile = 2 * k + (wave >> 1);
+    bf16_t* const q = tile == O_DV ? p.dv : tile == O_DK ? p.dk : tile == O_DB ? p.db
+                    : tile == O_DR ? p.dr : tile == O_DA ? p.da : p.dw;
+    dst[k] = q + tok0 + (int64_t)((tid >> 3) & 15) * tstride + 8 * (tid & 7);
+  }
   auto flush = [&](int cc) {
 #pragma unroll
     for (int k = 0; k < kOutRounds; ++k) {
-      const int pc = kBlock * k + tid, tile = pc >> 7, row = (pc >> 3) & 15, piece = pc & 7;
-      const uint4 v = *reinterpret_cast<const uint4*>(&L.outs[tile][row][8 * piece]);
-      *reinterpret_cast<uint4*>(outp[tile] + tok0 + (int64_t)(kL * cc + row) * tstride + 8 * piece) = v;
+      const int tile = 2 * k + (wave >> 1), row = (tid >> 3) & 15;
+      const uint4 v = *reinterpret_cast<const uint4*>(&out_at(L.outs[tile], row, 8 * (tid & 7)));
+      *reinterpret_cast<uint4*>(dst[k] + (int64_t)kL * cc * tstride) = v;
     }
   };
 
-  if (nchunks > 0) stage_in(fetch(nchunks - 1), (nchunks - 1) & 1);
-  Pre pre;
-  load_s0(nchunks - 1, S0row);
-  for (int c = nchunks - 1; c >= 0; --c) {
+  // ---- prologue: set up the last chunk
+  const int last = nchunks - 1;
+  reinterpret_cast<uint2*>(&L.zero[0][0])[tid] = make_uint2(0, 0);
+  {
+    const Pre pr = fetch(last, last);
+    stage_dec(pr);
+    stage_grad(pr, last & 1);
+  }
+  lds_barrier();
+  setup_decays(L.prep[last & 1], decay_load(L.dec, wave, t, qd), wave, t, qd);
+  lds_barrier();
+  if (last >= 1) stage_dec(fetch(last - 1, last));
+  setup_products(L.prep[last & 1], products_load(L.prep[last & 1], wave, t, qd), wave, t, qd, lane);
+  lds_barrier();
+  setup_inverse(L.prep[last & 1], L.prep[last & 1].amat[0][lane], L.prep[last & 1].amat[1][lane], t, qd, lane);
+
+  // one chunk; kFull: chunk c - 1 exists and is set up alongside (c >= 1).
+  // The last iteration (c == 0) is peeled so the loop body has no branches
+  // between the streams of a phase.
+  auto run_chunk = [&](const int c, auto full) {
+    constexpr bool kFull = decltype(full)::value;
     const int sb = c & 1;
+    Prep& P = L.prep[sb];
+    Prep& Pn = L.prep[sb ^ 1];   // set-up of chunk c - 1
     const bf16_t (*const stg)[kL][64] = L.stg[sb];
-    const float (*const sast)[64] = L.sast[sb];
-    lds_barrier();
-    if (c < nchunks - 1) flush(c + 1);   // gradients of the previous chunk
-
-    // ================= (1) decays and decayed rows, keys 16 wave .. + 15
-    {
-      const int c0 = 16 * wave + 4 * qd;
-      // plain float arrays around the cross-lane (DPP) operations: this
-      // compiler folds DPP builtins whose source is an element of an
-      // ext_vector value into a single one (all elements get element 0's)
-      const uint2 xr = *reinterpret_cast<const uint2*>(tile_at(stg[I_X], t, c0));
-      const float xs[4] = {__uint_as_float(xr.x << 16), __uint_as_float(xr.x & 0xffff0000u),
-                           __uint_as_float(xr.y << 16), __uint_as_float(xr.y & 0xffff0000u)};
-      float g2[4], lw2[4], gam[4], gin[4], gpv[4], gL[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        lw2[e] = log2_decay(xs[e]);
-        g2[e] = row_scan16(lw2[e]);
-        gam[e] = exp2_f(g2[e]);
-        gin[e] = exp2_f(-g2[e]);
-        gpv[e] = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-            __builtin_bit_cast(int, 1.0f), __builtin_bit_cast(int, gam[e]), 0x111, 0xf, 0xf, false));
-        gL[e] = row_last16(gam[e]);
-      }
-      const f32x4 gamv = {gam[0], gam[1], gam[2], gam[3]};
-      const f32x4 ginv = {gin[0], gin[1], gin[2], gin[3]};
-      const f32x4 gpvv = {gpv[0], gpv[1], gpv[2], gpv[3]};
-      const Split4 ah = split4(widen4(read4(stg[I_A], t, c0)) * gpvv);
-      const Split4 rh = split4(widen4(read4(stg[I_R], t, c0)) * gamv);
-      const Split4 kt = split4(widen4(read4(stg[I_K], t, c0)) * ginv);
-      const Split4 bt = split4(widen4(read4(stg[I_B], t, c0)) * ginv);
-      write4(L.rows[T_AH], t, c0, ah.hi);
-      write4(L.rows[T_AL], t, c0, ah.lo);
-      write4(L.rows[T_RH], t, c0, rh.hi);
-      write4(L.rows[T_RL], t, c0, rh.lo);
-      write4(L.rows[T_KH], t, c0, kt.hi);
-      write4(L.rows[T_KL], t, c0, kt.lo);
-      write4(L.rows[T_BH], t, c0, bt.hi);
-      write4(L.rows[T_BL], t, c0, bt.lo);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        L.gT[c0 + e][t] = g2[e];
-        L.lwT[c0 + e][t] = lw2[e];
-      }
-      if (t == 0) *reinterpret_cast<f32x4*>(&L.gl[c0]) = f32x4{gL[0], gL[1], gL[2], gL[3]};
-    }
-    lds_barrier();
-    if (c > 0) {
-      pre = fetch(c - 1);
-      load_s0(c - 1, S0row_n);
-    }
-
-    // ================= (2) step-by-step products of decayed rows, one per wave
-    {
-      auto rowpair = [&](int th, int tl, Split8 (&o)[2]) {
-#pragma unroll
-        for (int m = 0; m < 2; ++m)
-          o[m] = Split8{row_frag(L.rows[th], t, m, qd), row_frag(L.rows[tl], t, m, qd)};
-      };
-      Split8 X[2], Y[2];
-      if (wave == 0) {          // A_ab for the substitution, stored by columns
-        rowpair(T_AH, T_AL, X);
-        rowpair(T_BH, T_BL, Y);
-        f32x4 d = gram_x3(X, Y);   // [t'][s] = a^_t' . b~_s, lane column s = t
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (!(t < 4 * qd + r)) d[r] = 0.f;
-        *reinterpret_cast<f32x4*>(&L.amat[t][4 * qd]) = d;
-      } else {
-        const int ta = wave == 1 ? T_AH : T_RH;
-        const int tb = wave == 2 ? T_BH : T_KH;
-        rowpair(ta, ta + 1, X);
-        rowpair(tb, tb + 1, Y);
-        f32x4 d = gram_x3(X, Y);   // [t'][s'] = x_t' . y_s', the A operand of the transpose
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int tp = 4 * qd + r;
-          if (wave == 1 ? !(t < tp) : !(t <= tp)) d[r] = 0.f;
-        }
-        L.frag[wave == 1 ? F_AKT : wave == 2 ? F_RBT : F_RKT][lane] = stack_f(d);
-      }
-    }
+    S0Rows& s0r = *reinterpret_cast<S0Rows*>(&L.prep[1]);   // used at c == 0 only
     lds_barrier();
 
-    // ================= (3) P by substitution (wave 0); raw step products
-    if (wave == 0) {
-      // column t of P = (I - A_ab)^-1, column-oriented: once pc[s] is final,
-      // it updates every later row, so the dependent chain is 15 FMAs long
-      float pc[kL];
-#pragma unroll
-      for (int tt = 0; tt < kL; ++tt) pc[tt] = (tt == t) ? 1.0f : 0.0f;
-#pragma unroll
-      for (int s = 0; s < kL - 1; ++s) {
-#pragma unroll
-        for (int t4 = (s + 1) & ~3; t4 < kL; t4 += 4) {
-          const f32x4 acol = *reinterpret_cast<const f32x4*>(&L.amat[s][t4]);
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (t4 + e > s) pc[t4 + e] += acol[e] * pc[s];
-        }
-      }
-      // P^T as an A operand: lane l holds P[4 qd + e][l % 16], this lane's column
-      f32x4 pt;
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        pt[e] = qd == 0 ? pc[e] : qd == 1 ? pc[4 + e] : qd == 2 ? pc[8 + e] : pc[12 + e];
-      L.frag[F_PT][lane] = stack_f(pt);
+    // ================= phase A
+    if (c < last) flush(c + 1);   // gradients of the previous chunk
+    Pre pre;
+    f32x4 S0row[2][2];
+    if constexpr (kFull) {
+      // at c == 1 the decay rows of chunk 0 are fetched again (harmless, and
+      // the reversal of chunk 0 reads them)
+      pre = fetch(c >= 2 ? c - 2 : 0, c - 1);
+      load_s0(c, S0row);
     } else {
-      const bf16x8 v0 = row_frag(stg[I_V], t, 0, qd), v1 = row_frag(stg[I_V], t, 1, qd);
-      const bf16x8 y0 = row_frag(stg[I_DY], t, 0, qd), y1 = row_frag(stg[I_DY], t, 1, qd);
-      f32x4 z = {0.f, 0.f, 0.f, 0.f};
-      if (wave == 1) {
-        // B_yv^T[s][t] = dy_s . v_t, kept where s >= t; C_dyv^T[s][t] = v_s . dy_t, s <= t
-        f32x4 d = mma32(y1, v1, mma32(y0, v0, z));
-        f32x4 e = mma32(v1, y1, mma32(v0, y0, z));
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          if (!(4 * qd + r >= t)) d[r] = 0.f;
-          if (!(4 * qd + r <= t)) e[r] = 0.f;
-        }
-        L.frag[F_BYV][lane] = stack_f(d);
-        L.frag[F_CDYV][lane] = stack_f(e);
-      } else {
-        const Split8 s0f = sa_frag(sast, t, 0, qd), s1f = sa_frag(sast, t, 1, qd);
-        f32x4 d;
-        if (wave == 2) {   // B_ysa^T[s][t] = dy_s . sa_t, s >= t
-          d = mma32(y0, s0f.lo, z);
-          d = mma32(y1, s1f.lo, d);
-          d = mma32(y0, s0f.hi, d);
-          d = mma32(y1, s1f.hi, d);
-        } else {           // C_dysa^T[s][t] = sa_s . dy_t, s <= t
-          d = mma32(s0f.lo, y0, z);
-          d = mma32(s1f.lo, y1, d);
-          d = mma32(s0f.hi, y0, d);
-          d = mma32(s1f.hi, y1, d);
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (wave == 2 ? !(4 * qd + r >= t) : !(4 * qd + r <= t)) d[r] = 0.f;
-        L.frag[wave == 2 ? F_BYSA : F_CDYSA][lane] = stack_f(d);
-      }
-    }
-    lds_barrier();
-
-    // ================= (4) state gradient, value tile jb
-    if (c == 0) {
       // rebuild S0 by reversing the chunk's 16 steps from its checkpoint
-      // (kernel.rs:239-246): S_{t-1} = (S_t - v_t k_t^T - sa_t b_t^T) / w~_t
+      // (kernel.rs:239-246): S_{t-1} = (S_t - v_t k_t^T - sa_t b_t^T) / w~_t.
+      // The decay-rows buffer still holds chunk 0's rows; sa in fp32 from memory.
       const float* ck = ckbh;
       f32x4 S0t[4];
 #pragma unroll
@@ -351,15 +371,15 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
 #pragma unroll
         for (int r = 0; r < 4; ++r) S0t[ib][r] = ck[(16 * ib + 4 * qd + r) * kHead + jcol];
       for (int tt = kL - 1; tt >= 0; --tt) {
-        const float vj = __uint_as_float((uint32_t)stg[I_V][tt][8 * (((jcol >> 3) + tt) & 7) + (jcol & 7)] << 16);
-        const float sj = sa_at(sast, tt, jcol);
+        const float vj = __uint_as_float((uint32_t)__builtin_bit_cast(uint16_t, *tile_at(stg[S_V], tt, jcol)) << 16);
+        const float sj = p.sa[tok0 + (int64_t)tt * tstride + jcol];
 #pragma unroll
         for (int ib = 0; ib < 4; ++ib) {
-          const f32x4 kv = widen4(read4(stg[I_K], tt, 16 * ib + 4 * qd));
-          const f32x4 bv = widen4(read4(stg[I_B], tt, 16 * ib + 4 * qd));
+          const f32x4 kv = widen4(read4(L.dec[I_K], tt, 16 * ib + 4 * qd));
+          const f32x4 bv = widen4(read4(L.dec[I_B], tt, 16 * ib + 4 * qd));
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const float winv = exp2_f(-L.lwT[16 * ib + 4 * qd + r][tt]);
+            const float winv = exp2_f(-P.lwT[16 * ib + 4 * qd + r][tt]);
             S0t[ib][r] = (S0t[ib][r] - kv[r] * vj - bv[r] * sj) * winv;
           }
         }
@@ -367,37 +387,66 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
 #pragma unroll
       for (int ib = 0; ib < 4; ++ib)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) L.s0r[16 * ib + 4 * qd + r][jcol] = S0t[ib][r];
+        for (int r = 0; r < 4; ++r) s0r[16 * ib + 4 * qd + r][jcol] = S0t[ib][r];
     }
+    // all of phase A's LDS operands first, so their latency overlaps
+    f32x4 glv[4];
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib) glv[ib] = *reinterpret_cast<const f32x4*>(&P.gl[16 * ib + 4 * qd]);
+    const Split8 Bt0 = row_pair(P.rows[T_BH], P.rows[T_BL], t, 0, qd);
+    const Split8 Bt1 = row_pair(P.rows[T_BH], P.rows[T_BL], t, 1, qd);
+    const Split8 Kt0 = row_pair(P.rows[T_KH], P.rows[T_KL], t, 0, qd);
+    const Split8 Kt1 = row_pair(P.rows[T_KH], P.rows[T_KL], t, 1, qd);
+    const bf16x4 dycf = tr_frag(stg[S_DY], 0, 16 * jb, lane);   // dY[s][j] (k = s)
+    const bf16x8 f_rbt = P.frag[F_RBT][lane], f_pt = P.frag[F_PT][lane];
+    const bf16x8 f_rkt = P.frag[F_RKT][lane], f_akt = P.frag[F_AKT][lane];
+    bf16x8 rT[4], aT[4];
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib) {
+      rT[ib] = cat8(tr_frag(P.rows[T_RH], 0, 16 * ib, lane), tr_frag(P.rows[T_RL], 0, 16 * ib, lane));
+      aT[ib] = cat8(tr_frag(P.rows[T_AH], 0, 16 * ib, lane), tr_frag(P.rows[T_AL], 0, 16 * ib, lane));
+    }
+    DecayIn din;
+    if constexpr (kFull) din = decay_load(L.dec, wave, t, qd);
+    // step products of v, dy, sa (one per wave), as D = X1 Y1^T + X2 Y2^T:
+    // B_yv^T = dy v^T (s >= t), C_dyv^T = v dy^T (s <= t),
+    // B_ysa^T = dy sa^T (s >= t), C_dysa^T = sa dy^T (s <= t)
+    bf16x8 px1[2], py1[2], px2[2], py2[2];
+    {
+      const int x1 = wave == 1 ? S_V : wave == 3 ? S_SAH : S_DY;
+      const int y1 = wave == 0 ? S_V : wave == 2 ? S_SAH : S_DY;
+      const int y2 = wave == 0 ? S_V : wave == 2 ? S_SAL : S_DY;
+      const bf16_t (*const x2)[64] = wave == 2 ? stg[S_DY] : wave == 3 ? stg[S_SAL] : L.zero;
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        px1[m] = row_frag(stg[x1], t, m, qd);
+        py1[m] = row_frag(stg[y1], t, m, qd);
+        px2[m] = row_frag(x2, t, m, qd);
+        py2[m] = row_frag(stg[y2], t, m, qd);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    f32x4 dv;
     {
       f32x4 dSp[4];
 #pragma unroll
-      for (int ib = 0; ib < 4; ++ib)
-        dSp[ib] = dS[ib] * *reinterpret_cast<const f32x4*>(&L.gl[16 * ib + 4 * qd]);
+      for (int ib = 0; ib < 4; ++ib) dSp[ib] = dS[ib] * glv[ib];
       const Split8 Sx0 = split8(dSp[0], dSp[1]), Sx1 = split8(dSp[2], dSp[3]);
-      const Split8 Bt0{row_frag(L.rows[T_BH], t, 0, qd), row_frag(L.rows[T_BL], t, 0, qd)};
-      const Split8 Bt1{row_frag(L.rows[T_BH], t, 1, qd), row_frag(L.rows[T_BL], t, 1, qd)};
-      const Split8 Kt0{row_frag(L.rows[T_KH], t, 0, qd), row_frag(L.rows[T_KL], t, 0, qd)};
-      const Split8 Kt1{row_frag(L.rows[T_KH], t, 1, qd), row_frag(L.rows[T_KL], t, 1, qd)};
-      const bf16x4 dycf = tr_frag(stg[I_DY], 0, 16 * jb, lane);   // dY[s][j] (k = s)
       f32x4 z = mma32x3(Bt0, Sx0, f32x4{0.f, 0.f, 0.f, 0.f});
       z = mma32x3(Bt1, Sx1, z);
-      z = mma_s2(L.frag[F_RBT][lane], dycf, z);
-      const f32x4 dsa = mma_s3(L.frag[F_PT][lane], split4(z), f32x4{0.f, 0.f, 0.f, 0.f});
+      z = mma_s2(f_rbt, dycf, z);
+      const f32x4 dsa = mma_s3(f_pt, split4(z), f32x4{0.f, 0.f, 0.f, 0.f});
       const Split4 dsas = split4(dsa);
-      f32x4 dv = mma32x3(Kt0, Sx0, f32x4{0.f, 0.f, 0.f, 0.f});
+      dv = mma32x3(Kt0, Sx0, f32x4{0.f, 0.f, 0.f, 0.f});
       dv = mma32x3(Kt1, Sx1, dv);
-      dv = mma_s2(L.frag[F_RKT][lane], dycf, dv);
-      dv = mma_s3(L.frag[F_AKT][lane], dsas, dv);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) L.outs[O_DV][4 * qd + r][jcol] = __builtin_bit_cast(bf16_t, (__bf16)dv[r]);
+      dv = mma_s2(f_rkt, dycf, dv);
+      dv = mma_s3(f_akt, dsas, dv);
       // carried gradient dS0^T = dS'^T + R^^T dY + A^^T dSA
 #pragma unroll
       for (int ib = 0; ib < 4; ++ib) {
-        const bf16x8 rT = cat8(tr_frag(L.rows[T_RH], 0, 16 * ib, lane), tr_frag(L.rows[T_RL], 0, 16 * ib, lane));
-        const bf16x8 aT = cat8(tr_frag(L.rows[T_AH], 0, 16 * ib, lane), tr_frag(L.rows[T_AL], 0, 16 * ib, lane));
-        f32x4 acc = mma_s2(rT, dycf, dSp[ib]);
-        dS[ib] = mma_s3(aT, dsas, acc);
+        f32x4 acc = mma_s2(rT[ib], dycf, dSp[ib]);
+        dS[ib] = mma_s3(aT[ib], dsas, acc);
       }
       // exchange for the key stage: dS' as [value j][key i], dSA as [j][step]
 #pragma unroll
@@ -408,85 +457,120 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
           write4(L.xds[0], jcol, 32 * m + 16 * hh + 4 * qd, half_of(sx.hi, hh));
           write4(L.xds[1], jcol, 32 * m + 16 * hh + 4 * qd, half_of(sx.lo, hh));
         }
-      *reinterpret_cast<bf16x4*>(&L.xdsa[0][jcol][4 * qd]) = dsas.hi;
-      *reinterpret_cast<bf16x4*>(&L.xdsa[1][jcol][4 * qd]) = dsas.lo;
+      *reinterpret_cast<bf16x4*>(xdsa_at(L.xdsa[0], jcol, qd)) = dsas.hi;
+      *reinterpret_cast<bf16x4*>(xdsa_at(L.xdsa[1], jcol, qd)) = dsas.lo;
+    }
+    if constexpr (kFull) setup_decays(Pn, din, wave, t, qd);
+    {
+      f32x4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        d = mma32(px2[m], py2[m], d);
+        d = mma32(px1[m], py1[m], d);
+      }
+      const int sgn = (wave & 1) ? -1 : 1;   // keep s >= t (B_), s <= t (C_)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) d[r] = sgn * (4 * qd + r - t) >= 0 ? d[r] : 0.f;
+      L.frag[G_BYV + wave][lane] = stack_f(d);
+    }
+    // issue order: each matrix product followed by independent vector work
+    // (decays, splits), which fills the product's latency
+#pragma unroll
+    for (int i = 0; i < 34; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
     }
     lds_barrier();
 
-    // ================= (5) step products with dSA
+    // ================= phase B
+    if constexpr (kFull) {
+      stage_dec(pre);             // decay rows of chunk c - 2 (the decays of phase A are done)
+      stage_grad(pre, sb ^ 1);    // gradient rows of chunk c - 1 (free buffer)
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) out_at(L.outs[O_DV], 4 * qd + r, jcol) = __builtin_bit_cast(bf16_t, (__bf16)dv[r]);
     // dSA as row fragments (row = step t, k = value), from the [j][t] tiles
     auto dsa_frag = [&](int hl, int m) {
-      return cat8(read_tr16(&L.xdsa[hl][32 * m + 4 * qd + (t >> 2)][4 * (t & 3)]) ,
-                  read_tr16(&L.xdsa[hl][32 * m + 16 + 4 * qd + (t >> 2)][4 * (t & 3)]));
+      return cat8(read_tr16(xdsa_at(L.xdsa[hl], 32 * m + 4 * qd + (t >> 2), t & 3)),
+                  read_tr16(xdsa_at(L.xdsa[hl], 32 * m + 16 + 4 * qd + (t >> 2), t & 3)));
     };
-    if (wave < 3) {
-      const Split8 q0{dsa_frag(0, 0), dsa_frag(1, 0)}, q1{dsa_frag(0, 1), dsa_frag(1, 1)};
-      f32x4 z = {0.f, 0.f, 0.f, 0.f};
-      if (wave == 0) {
-        const bf16x8 v0 = row_frag(stg[I_V], t, 0, qd), v1 = row_frag(stg[I_V], t, 1, qd);
-        // B_sav^T[s][t] = dsa_s . v_t, s > t; C_dsav^T[s][t] = v_s . dsa_t, s < t
-        f32x4 d = mma32(q0.lo, v0, z);
-        d = mma32(q1.lo, v1, d);
-        d = mma32(q0.hi, v0, d);
-        d = mma32(q1.hi, v1, d);
-        f32x4 e = mma32(v0, q0.lo, z);
-        e = mma32(v1, q1.lo, e);
-        e = mma32(v0, q0.hi, e);
-        e = mma32(v1, q1.hi, e);
+    GramIn gin;
+    if constexpr (kFull) gin = products_load(Pn, wave, t, qd);
+    // step products with dSA (one per wave): B_sav^T = dsa v^T (s > t),
+    // C_dsav^T = v dsa^T (s < t), B_sasa^T = dsa sa^T (s > t),
+    // C_dsasa^T = sa dsa^T (s < t)
+    const Split8 q[2] = {{dsa_frag(0, 0), dsa_frag(1, 0)}, {dsa_frag(0, 1), dsa_frag(1, 1)}};
+    Split8 g[2];
+    {
+      const bf16_t (*const ylo)[64] = wave >= 2 ? stg[S_SAL] : L.zero;
+      const int yhi = wave >= 2 ? S_SAH : S_V;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          if (!(4 * qd + r > t)) d[r] = 0.f;
-          if (!(4 * qd + r < t)) e[r] = 0.f;
-        }
-        L.frag[F_BSAV][lane] = stack_f(d);
-        L.frag[F_CDSAV][lane] = stack_f(e);
-      } else {
-        const Split8 s0f = sa_frag(sast, t, 0, qd), s1f = sa_frag(sast, t, 1, qd);
-        f32x4 d;
-        if (wave == 1) {   // B_sasa^T[s][t] = dsa_s . sa_t, s > t
-          d = mma32x3(q0, s0f, z);
-          d = mma32x3(q1, s1f, d);
-        } else {           // C_dsasa^T[s][t] = sa_s . dsa_t, s < t
-          d = mma32x3(s0f, q0, z);
-          d = mma32x3(s1f, q1, d);
-        }
+      for (int m = 0; m < 2; ++m) g[m] = Split8{row_frag(stg[yhi], t, m, qd), row_frag(ylo, t, m, qd)};
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (kFull) setup_products(Pn, gin, wave, t, qd, lane);
+    {
+      // both orientations, the wave keeps one (no branch in the phase)
+      f32x4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = d0;
+      d0 = mma32x3(q[0], g[0], d0);
+      d0 = mma32x3(q[1], g[1], d0);
+      d1 = mma32x3(g[0], q[0], d1);
+      d1 = mma32x3(g[1], q[1], d1);
+      const int sgn = (wave & 1) ? -1 : 1;   // keep s > t (B_), s < t (C_)
+      f32x4 d = (wave & 1) ? d1 : d0;
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (wave == 1 ? !(4 * qd + r > t) : !(4 * qd + r < t)) d[r] = 0.f;
-        L.frag[wave == 1 ? F_BSASA : F_CDSASA][lane] = stack_f(d);
-      }
+      for (int r = 0; r < 4; ++r) d[r] = sgn * (4 * qd + r - t) > 0 ? d[r] : 0.f;
+      L.frag[G_BSAV + wave][lane] = stack_f(d);
     }
     lds_barrier();
 
-    // ================= (6) key-indexed gradients, keys 16 wave .. + 15
+    // ================= phase C
     {
       const int kb = wave;   // key tile; result layout rows = step 4 qd + r, column = key ki
-      // decayed rows as B operands (k = step, column = key), split
-      const Split4 Rc{tr_frag(L.rows[T_RH], 0, 16 * kb, lane), tr_frag(L.rows[T_RL], 0, 16 * kb, lane)};
-      const Split4 Ac{tr_frag(L.rows[T_AH], 0, 16 * kb, lane), tr_frag(L.rows[T_AL], 0, 16 * kb, lane)};
-      const Split4 Kc{tr_frag(L.rows[T_KH], 0, 16 * kb, lane), tr_frag(L.rows[T_KL], 0, 16 * kb, lane)};
-      const Split4 Bc{tr_frag(L.rows[T_BH], 0, 16 * kb, lane), tr_frag(L.rows[T_BL], 0, 16 * kb, lane)};
-      // start state as B operand (k = value j, column = key ki), split
-      Split8 S0b[2];
-      if (c > 0) {
+      // all LDS operands first: decayed rows as B operands (k = step, column
+      // = key), split
+      const Split4 Rc{tr_frag(P.rows[T_RH], 0, 16 * kb, lane), tr_frag(P.rows[T_RL], 0, 16 * kb, lane)};
+      const Split4 Ac{tr_frag(P.rows[T_AH], 0, 16 * kb, lane), tr_frag(P.rows[T_AL], 0, 16 * kb, lane)};
+      const Split4 Kc{tr_frag(P.rows[T_KH], 0, 16 * kb, lane), tr_frag(P.rows[T_KL], 0, 16 * kb, lane)};
+      const Split4 Bc{tr_frag(P.rows[T_BH], 0, 16 * kb, lane), tr_frag(P.rows[T_BL], 0, 16 * kb, lane)};
+      // start state (k = value j, column = key ki)
+      f32x4 S0v[2][2];
 #pragma unroll
-        for (int m = 0; m < 2; ++m) S0b[m] = split8(S0row[m][0], S0row[m][1]);
-      } else {
-#pragma unroll
-        for (int m = 0; m < 2; ++m)
-          S0b[m] = split8(*reinterpret_cast<const f32x4*>(&L.s0r[ki][32 * m + 4 * qd]),
-                          *reinterpret_cast<const f32x4*>(&L.s0r[ki][32 * m + 16 + 4 * qd]));
+      for (int m = 0; m < 2; ++m) {
+        if constexpr (kFull) {
+          S0v[m][0] = S0row[m][0];
+          S0v[m][1] = S0row[m][1];
+        } else {
+          S0v[m][0] = *reinterpret_cast<const f32x4*>(&s0r[ki][32 * m + 4 * qd]);
+          S0v[m][1] = *reinterpret_cast<const f32x4*>(&s0r[ki][32 * m + 16 + 4 * qd]);
+        }
       }
-      const f32x4 z = {0.f, 0.f, 0.f, 0.f};
       // dS' as B operand (k = value j, column = key ki)
       Split8 Db[2];
 #pragma unroll
       for (int m = 0; m < 2; ++m)
         Db[m] = Split8{tr_frag32(L.xds[0], m, 16 * kb, lane), tr_frag32(L.xds[1], m, 16 * kb, lane)};
-      const bf16x8 v0 = row_frag(stg[I_V], t, 0, qd), v1 = row_frag(stg[I_V], t, 1, qd);
-      const bf16x8 y0 = row_frag(stg[I_DY], t, 0, qd), y1 = row_frag(stg[I_DY], t, 1, qd);
-      const Split8 s0f = sa_frag(sast, t, 0, qd), s1f = sa_frag(sast, t, 1, qd);
+      const bf16x8 v0 = row_frag(stg[S_V], t, 0, qd), v1 = row_frag(stg[S_V], t, 1, qd);
+      const bf16x8 y0 = row_frag(stg[S_DY], t, 0, qd), y1 = row_frag(stg[S_DY], t, 1, qd);
+      const Split8 s0f = row_pair(stg[S_SAH], stg[S_SAL], t, 0, qd);
+      const Split8 s1f = row_pair(stg[S_SAH], stg[S_SAL], t, 1, qd);
       const Split8 q0{dsa_frag(0, 0), dsa_frag(1, 0)}, q1{dsa_frag(0, 1), dsa_frag(1, 1)};
+      bf16x8 fg[G_COUNT];
+#pragma unroll
+      for (int i = 0; i < G_COUNT; ++i) fg[i] = L.frag[i][lane];
+      const f32x4 g4 = *reinterpret_cast<const f32x4*>(&P.gT[ki][4 * qd]);
+      const f32x4 lw4 = *reinterpret_cast<const f32x4*>(&P.lwT[ki][4 * qd]);
+      f32x4 am, amt;
+      if constexpr (kFull) {
+        am = Pn.amat[0][lane];
+        amt = Pn.amat[1][lane];
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (kFull) setup_inverse(Pn, am, amt, t, qd, lane);   // chunk c - 1
+      Split8 S0b[2];
+#pragma unroll
+      for (int m = 0; m < 2; ++m) S0b[m] = split8(S0v[m][0], S0v[m][1]);
+      const f32x4 z = {0.f, 0.f, 0.f, 0.f};
 
       // V dS' (= d k- gamma_L) and SA dS' (= d b- gamma_L)
       f32x4 x1 = mma32(v0, Db[0].lo, z);
@@ -495,12 +579,20 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
       x1 = mma32(v1, Db[1].hi, x1);
       f32x4 x2 = mma32x3(s0f, Db[0], z);
       x2 = mma32x3(s1f, Db[1], x2);
+      // the decayed rows at (step 4 qd + r, key ki) in fp32
+      float Rf[4], Af[4], Kf[4], Bf[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        Rf[r] = hi_lo(Rc.hi, Rc.lo, r);
+        Af[r] = hi_lo(Ac.hi, Ac.lo, r);
+        Kf[r] = hi_lo(Kc.hi, Kc.lo, r);
+        Bf[r] = hi_lo(Bc.hi, Bc.lo, r);
+      }
       // sum over the chunk's steps of K~ o V dS' + B~ o SA dS', and over this
       // lane's 16 values j of S0 o dS' (S0 and dS' hold the same j per element)
       float epart = 0.f;
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        epart += ((float)Kc.hi[r] + (float)Kc.lo[r]) * x1[r] + ((float)Bc.hi[r] + (float)Bc.lo[r]) * x2[r];
+      for (int r = 0; r < 4; ++r) epart += Kf[r] * x1[r] + Bf[r] * x2[r];
 #pragma unroll
       for (int m = 0; m < 2; ++m)
 #pragma unroll
@@ -511,39 +603,34 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
           epart = __builtin_amdgcn_fdot2_f32_bf16(sh, dl, epart, false);
           epart = __builtin_amdgcn_fdot2_f32_bf16(sl, dh, epart, false);
         }
-      f32x4 dk = mma_s3(L.frag[F_BYV][lane], Rc, x1);
-      dk = mma_s3(L.frag[F_BSAV][lane], Ac, dk);
-      f32x4 dbv = mma_s3(L.frag[F_BYSA][lane], Rc, x2);
-      dbv = mma_s3(L.frag[F_BSASA][lane], Ac, dbv);
+      f32x4 dk = mma_s3(fg[G_BYV], Rc, x1);
+      dk = mma_s3(fg[G_BSAV], Ac, dk);
+      f32x4 dbv = mma_s3(fg[G_BYSA], Rc, x2);
+      dbv = mma_s3(fg[G_BSASA], Ac, dbv);
       // dY S0 and dSA S0
       f32x4 dr = mma32(y0, S0b[0].lo, z);
       dr = mma32(y1, S0b[1].lo, dr);
       dr = mma32(y0, S0b[0].hi, dr);
       dr = mma32(y1, S0b[1].hi, dr);
-      dr = mma_s3(L.frag[F_CDYV][lane], Kc, dr);
-      dr = mma_s3(L.frag[F_CDYSA][lane], Bc, dr);
+      dr = mma_s3(fg[G_CDYV], Kc, dr);
+      dr = mma_s3(fg[G_CDYSA], Bc, dr);
       f32x4 da = mma32x3(q0, S0b[0], z);
       da = mma32x3(q1, S0b[1], da);
-      da = mma_s3(L.frag[F_CDSAV][lane], Kc, da);
-      da = mma_s3(L.frag[F_CDSASA][lane], Bc, da);
+      da = mma_s3(fg[G_CDSAV], Kc, da);
+      da = mma_s3(fg[G_CDSASA], Bc, da);
 
-      // decay factors at (step 4 qd + r, key ki)
-      const f32x4 g4 = *reinterpret_cast<const f32x4*>(&L.gT[ki][4 * qd]);
-      const f32x4 lw4 = *reinterpret_cast<const f32x4*>(&L.lwT[ki][4 * qd]);
-      const f32x4 rv = widen4(tr_frag(stg[I_R], 0, 16 * kb, lane));
-      const f32x4 kv = widen4(tr_frag(stg[I_K], 0, 16 * kb, lane));
-      const f32x4 bv = widen4(tr_frag(stg[I_B], 0, 16 * kb, lane));
-      const f32x4 av = widen4(tr_frag(stg[I_A], 0, 16 * kb, lane));
+      // dL/dg: r dr - k dk - b db + a da, formed before the decay factors as
+      // R^ o dr' - K~ o dk' - B~ o db' + A^ o da' (x' = the products above)
       f32x4 f, ad, sig;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
+        ad[r] = Af[r] * da[r];
+        f[r] = Rf[r] * dr[r] - Kf[r] * dk[r] - Bf[r] * dbv[r] + ad[r];
         const float gam = exp2_f(g4[r]), gin = exp2_f(-g4[r]), gpv = exp2_f(g4[r] - lw4[r]);
         dk[r] *= gin;
         dbv[r] *= gin;
         dr[r] *= gam;
         da[r] *= gpv;
-        ad[r] = av[r] * da[r];
-        f[r] = rv[r] * dr[r] - kv[r] * dk[r] - bv[r] * dbv[r] + ad[r];
         sig[r] = lw4[r] * kSigFromLw2;
       }
       // suffix sums over the chunk's steps: in-lane over r, then over quads
@@ -567,25 +654,19 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
         const float dlw = suf[r] + above - ad[r] + etot;
         const float dwv = dlw * kWScale * sig[r] * (1.0f - sig[r]);
         const int tr = 4 * qd + r;
-        L.outs[O_DK][tr][ki] = __builtin_bit_cast(bf16_t, (__bf16)dk[r]);
-        L.outs[O_DB][tr][ki] = __builtin_bit_cast(bf16_t, (__bf16)dbv[r]);
-        L.outs[O_DR][tr][ki] = __builtin_bit_cast(bf16_t, (__bf16)dr[r]);
-        L.outs[O_DA][tr][ki] = __builtin_bit_cast(bf16_t, (__bf16)da[r]);
-        L.outs[O_DW][tr][ki] = __builtin_bit_cast(bf16_t, (__bf16)dwv);
+        out_at(L.outs[O_DK], tr, ki) = __builtin_bit_cast(bf16_t, (__bf16)dk[r]);
+        out_at(L.outs[O_DB], tr, ki) = __builtin_bit_cast(bf16_t, (__bf16)dbv[r]);
+        out_at(L.outs[O_DR], tr, ki) = __builtin_bit_cast(bf16_t, (__bf16)dr[r]);
+        out_at(L.outs[O_DA], tr, ki) = __builtin_bit_cast(bf16_t, (__bf16)da[r]);
+        out_at(L.outs[O_DW], tr, ki) = __builtin_bit_cast(bf16_t, (__bf16)dwv);
       }
     }
-    if (c > 0) stage_in(pre, sb ^ 1);   // next chunk's rows into the free buffer
-#pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      S0row[m][0] = S0row_n[m][0];
-      S0row[m][1] = S0row_n[m][1];
-    }
-  }
+  };
+  for (int c = last; c >= 1; --c) run_chunk(c, std::true_type{});
+  run_chunk(0, std::false_type{});
 
-  if (nchunks > 0) {
-    lds_barrier();
-    flush(0);
-  }
+  lds_barrier();
+  flush(0);
   if (p.ds0) {
 #pragma unroll
     for (int ib = 0; ib < 4; ++ib)

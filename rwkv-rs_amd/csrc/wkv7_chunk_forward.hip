@@ -264,9 +264,9 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_fwd_chunk_kernel(const FwdChun
 
   // ---- staging loads: thread tid moves pieces k = 0..kPieces-1 of a batch.
   // Piece p = kBlock * k + tid is row p / 8 = (vec, chunk, step), slot p % 8,
-  // which holds global 16-byte piece (slot - step) % 8 of the row.
+  // which holds global 16-byte piece (slot - tile_rot(step)) % 8 of the row.
   const int st_t = (tid >> 3) & 15, st_slot = tid & 7;
-  const int st_oct = (st_slot - st_t) & 7;
+  const int st_oct = (st_slot - tile_rot(st_t)) & 7;
   auto issue = [&](int n) {
     const int nq = min(kBatch, nchunks - kBatch * n);
 #pragma unroll
