@@ -133,10 +133,10 @@ __device__ __forceinline__ f32x4 mma_s3(bf16x8 a_stacked, const Split4& b, f32x4
 __device__ __forceinline__ f32x4 mma_tiles(f32x4 xt, f32x4 y, f32x4 c) {
   return mma_s3(stack(split4(xt)), split4(y), c);
 }
-// P = (I - A)^-1 for a strictly lower triangular 16x16 A, from A and A^T in
-// the result layout (t = l % 16, qd = l / 16); P in the result layout. Since
-// A^16 = 0, P = (I + A)(I + A^2)(I + A^4)(I + A^8): five dependent products,
-// all operands in registers.
+// P = (I - A)^-1 for a strictly triangular 16x16 A (lower or upper), from A
+// and A^T in the result layout (t = l % 16, qd = l / 16); P in the result
+// layout. Since A^16 = 0, P = (I + A)(I + A^2)(I + A^4)(I + A^8): five
+// dependent products, all operands in registers.
 __device__ __forceinline__ f32x4 unit_lower_inverse(f32x4 a, f32x4 at, int t, int qd) {
   const f32x4 z = {0.f, 0.f, 0.f, 0.f};
   f32x4 id;

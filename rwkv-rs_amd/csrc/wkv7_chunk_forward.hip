@@ -12,7 +12,7 @@
 // Work layout: one workgroup of four waves per (batch, head). Steps are taken
 // four chunks (64 steps) at a time:
 //   phase 1  wave w prepares chunk w of the batch on its own: decays, the four
-//            16x16 step-by-step products, P by forward substitution, W and U,
+//            16x16 step-by-step products, P on the matrix cores, W and U,
 //            and leaves every operand phase 2 needs in LDS, already in
 //            fragment order (one 16-byte or 8-byte load per lane);
 //   phase 2  the four chunks in order; wave w owns value columns 16w..16w+15
@@ -63,14 +63,11 @@ struct FwdChunkParams {
 
 // Phase 1 for one chunk, run by one wave. `stg` holds the chunk's raw rows;
 // after they are read, the chunk's x, r, k, a, b rows and the wave's scratch
-// `scr` (first the 16x16 fp32 matrices of the substitution) are reused for
-// the hi/lo rows of A^, K~ and B~, from which the transposed fragments are
-// read.
+// `scr` are reused for the hi/lo rows of A^, K~ and B~, from which the
+// transposed fragments are read.
 __device__ __forceinline__ void prepare_chunk(bf16_t (*stg)[kBatch][kL][64], int q,
                                               float (*scr)[kL][kL], ChunkOps& o, int lane) {
   const int t = lane & 15, qd = lane >> 4;
-  float (*amat)[kL] = scr[0];
-  float (*pmat)[kL] = scr[1];
   // the lane's step row t, keys 32 m + 16 hh + 4 qd + c (c < 4), as raw bf16
   auto raw = [&](int vec, int m, int hh) -> uint2 {
     return *reinterpret_cast<const uint2*>(tile_at(stg[vec][q], t, 32 * m + 16 * hh + 4 * qd));
@@ -118,42 +115,26 @@ __device__ __forceinline__ void prepare_chunk(bf16_t (*stg)[kBatch][kL][64], int
   }
   // step-by-step products, computed transposed: result row = step s, lane
   // column = step t, which is the x16 A operand (row t, k = s) of A_xx[t][s]
-  f32x4 akT = {0.f, 0.f, 0.f, 0.f}, arkT = akT, arbT = akT, aabT = akT;
+  f32x4 akT = {0.f, 0.f, 0.f, 0.f}, arkT = akT, arbT = akT, aabT = akT, aab = akT;
 #pragma unroll
   for (int m = 0; m < 2; ++m) {
     akT = mma32x3(KT[m], AH[m], akT);
     arkT = mma32x3(KT[m], RH[m], arkT);
     arbT = mma32x3(BT[m], RH[m], arbT);
     aabT = mma32x3(BT[m], AH[m], aabT);
+    aab = mma32x3(AH[m], BT[m], aab);
   }
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int s = 4 * qd + r;
     if (!(s < t)) { akT[r] = 0.f; aabT[r] = 0.f; }
     if (!(s <= t)) { arkT[r] = 0.f; arbT[r] = 0.f; }
+    if (!(t < s)) aab[r] = 0.f;
   }
-  // P = (I - A_ab)^{-1} by forward substitution; lane column u = t
-  *reinterpret_cast<f32x4*>(&amat[t][4 * qd]) = aabT;
-  wave_lds_sync();
-  float pc[kL];
-#pragma unroll
-  for (int tt = 0; tt < kL; ++tt) {
-    float acc = (tt == t) ? 1.0f : 0.0f;
-#pragma unroll
-    for (int s4 = 0; s4 < tt; s4 += 4) {
-      const f32x4 arow = *reinterpret_cast<const f32x4*>(&amat[tt][s4]);
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (s4 + e < tt) acc += arow[e] * pc[s4 + e];
-    }
-    pc[tt] = acc;
-  }
-  if (qd == 0) {
-#pragma unroll
-    for (int tt = 0; tt < kL; ++tt) pmat[tt][t] = pc[tt];
-  }
-  wave_lds_sync();
-  const Split4 P = split4(*reinterpret_cast<const f32x4*>(&pmat[t][4 * qd]));
+  // P^T = (I - A_ab^T)^{-1} on the matrix cores, in the result layout: lane
+  // (qd, t) holds P[t][4 qd + r], which is P as an A operand and P^T as a B
+  // operand
+  const Split4 P = split4(unit_lower_inverse(aabT, aab, t, qd));
 
   // hi/lo rows of A^, K~, B~ into LDS (the chunk's raw rows are consumed),
   // then their transposed fragments (row = key, k = step) by transposed loads
