@@ -35,9 +35,8 @@
 //            16w..16w+15) | decays and decayed rows of chunk c-1 (wave w:
 //            keys 16w..16w+15) | step products of v, dy, sa of chunk c
 //   phase B: step products with dSA of chunk c | step products of the
-//            decayed rows of chunk c-1
-//   phase C: key-indexed gradients of chunk c (wave w: keys 16w..16w+15) |
-//            P = (I - A_ab)^-1 of chunk c-1 on the matrix cores (every wave)
+//            decayed rows of chunk c-1 and P = (I - A_ab)^-1 (wave 0)
+//   phase C: key-indexed gradients of chunk c (wave w: keys 16w..16w+15)
 // Within a phase each wave first issues all its LDS reads, then computes.
 // Inputs are staged through registers, loaded in phase A and written to LDS
 // in phase B: the rows only the decays read (x, r, k, a, b) in one buffer,
@@ -76,7 +75,6 @@ struct Prep {
   float gT[64][kL + 4];             // log2 prefix decay, [key][step]
   float lwT[64][kL + 4];            // log2 step decay, [key][step]
   float gl[64];                     // gamma_L
-  f32x4 amat[2][64];                // A_ab and A_ab^T, result layout
   bf16x8 frag[F_COUNT][64];         // stacked 16x16 operands
 };
 
@@ -185,8 +183,8 @@ __device__ __forceinline__ void setup_decays(Prep& P, const DecayIn& in, int wav
 }
 
 // ---- set-up step 2: one step-by-step product of decayed rows per wave.
-// wave 0: A_ab and A_ab^T (for P = (I - A_ab)^-1, step 3); 1: A_ak^T;
-// 2: A_rb^T; 3: A_rk^T.
+// wave 0: A_ab and A_ab^T, and from them P = (I - A_ab)^-1 on the matrix
+// cores (registers only, no LDS round trips); 1: A_ak^T; 2: A_rb^T; 3: A_rk^T.
 struct GramIn { Split8 X[2], Y[2]; };
 __device__ __forceinline__ GramIn products_load(const Prep& P, int wave, int t, int qd) {
   const int xa = wave < 2 ? T_AH : T_RH;
@@ -211,20 +209,11 @@ __device__ __forceinline__ void setup_products(Prep& P, const GramIn& g, int wav
     f32x4 dt = gram_x3(Y, X);
 #pragma unroll
     for (int r = 0; r < 4; ++r) dt[r] = t - (4 * qd + r) >= 1 ? dt[r] : 0.f;
-    P.amat[0][lane] = d;
-    P.amat[1][lane] = dt;
+    // P^T as an A operand: lane l holds P[4 qd + e][l % 16], P's result layout
+    P.frag[F_PT][lane] = stack_f(unit_lower_inverse(d, dt, t, qd));
   } else {
     P.frag[wave - 1][lane] = stack_f(d);
   }
-}
-
-// ---- set-up step 3: P = (I - A_ab)^-1 on the matrix cores (registers only,
-// no LDS round trips). Every wave computes it next to its key gradients and
-// stores the same P^T as an A operand (lane l holds P[4 qd + e][l % 16], P's
-// result layout): a store by one wave alone would leave the others nothing to
-// compute and put the whole chain on that wave.
-__device__ __forceinline__ void setup_inverse(Prep& P, f32x4 a, f32x4 at, int t, int qd, int lane) {
-  P.frag[F_PT][lane] = stack_f(unit_lower_inverse(a, at, t, qd));
 }
 
 __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChunkParams p) {
@@ -336,8 +325,6 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
   lds_barrier();
   if (last >= 1) stage_dec(fetch(last - 1, last));
   setup_products(L.prep[last & 1], products_load(L.prep[last & 1], wave, t, qd), wave, t, qd, lane);
-  lds_barrier();
-  setup_inverse(L.prep[last & 1], L.prep[last & 1].amat[0][lane], L.prep[last & 1].amat[1][lane], t, qd, lane);
 
   // one chunk; kFull: chunk c - 1 exists and is set up alongside (c >= 1).
   // The last iteration (c == 0) is peeled so the loop body has no branches
@@ -473,13 +460,6 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
       for (int r = 0; r < 4; ++r) d[r] = sgn * (4 * qd + r - t) >= 0 ? d[r] : 0.f;
       L.frag[G_BYV + wave][lane] = stack_f(d);
     }
-    // issue order: each matrix product followed by independent vector work
-    // (decays, splits), which fills the product's latency
-#pragma unroll
-    for (int i = 0; i < 34; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
-    }
     lds_barrier();
 
     // ================= phase B
@@ -560,13 +540,7 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
       for (int i = 0; i < G_COUNT; ++i) fg[i] = L.frag[i][lane];
       const f32x4 g4 = *reinterpret_cast<const f32x4*>(&P.gT[ki][4 * qd]);
       const f32x4 lw4 = *reinterpret_cast<const f32x4*>(&P.lwT[ki][4 * qd]);
-      f32x4 am, amt;
-      if constexpr (kFull) {
-        am = Pn.amat[0][lane];
-        amt = Pn.amat[1][lane];
-      }
       __builtin_amdgcn_sched_barrier(0);
-      if constexpr (kFull) setup_inverse(Pn, am, amt, t, qd, lane);   // chunk c - 1
       Split8 S0b[2];
 #pragma unroll
       for (int m = 0; m < 2; ++m) S0b[m] = split8(S0v[m][0], S0v[m][1]);
