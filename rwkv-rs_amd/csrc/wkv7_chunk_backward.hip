@@ -52,8 +52,10 @@ namespace {
 
 using namespace chunk;
 
-constexpr int kWaves = 4;
+constexpr int kWaves = 8;
 constexpr int kBlock = 64 * kWaves;
+constexpr int kGradWaves = 4;          // waves 0-3: gradients; 4-7: set-up of the next chunk
+constexpr int kSetup = 64 * 4;         // threads of either group of four waves
 enum { I_X, I_R, I_K, I_A, I_B, I_V, I_DY, I_COUNT };   // input tensors
 constexpr int kDecayIn = 5;                             // I_X..I_B: read by the decays only
 enum { S_V, S_DY, S_SAH, S_SAL, S_COUNT };              // rows read by the gradients
@@ -61,13 +63,13 @@ enum { T_AH, T_AL, T_RH, T_RL, T_KH, T_KL, T_BH, T_BL, T_COUNT };   // decayed r
 enum { F_AKT, F_RBT, F_RKT, F_PT, F_COUNT };            // stacked operands from the decayed rows
 enum { G_BYV, G_CDYV, G_BYSA, G_CDYSA, G_BSAV, G_CDSAV, G_BSASA, G_CDSASA, G_COUNT };
 enum { O_DV, O_DK, O_DB, O_DR, O_DA, O_DW, O_COUNT };   // staged gradient tiles
-constexpr int kOutRounds = O_COUNT * kL * 8 / kBlock;          // 16-byte stores per thread
+constexpr int kOutRounds = O_COUNT * kL * 8 / kSetup;          // 16-byte stores per set-up thread
 constexpr int kDecayPieces = kDecayIn * kL * 8;                // 16-byte pieces per chunk
-constexpr int kDecayRounds = (kDecayPieces + kBlock - 1) / kBlock;
+constexpr int kDecayRounds = (kDecayPieces + kSetup - 1) / kSetup;
 constexpr float kSigFromLw2 = 1.0f / (kWScale * kLog2e);        // sigmoid = lw2 * this
-static_assert(2 * kL * 8 == kBlock, "v and dy rows: one 16-byte piece per thread");
-static_assert(kL * 16 == kBlock, "removal_state rows: four values per thread");
-static_assert(O_COUNT * kL * 8 % kBlock == 0, "whole rounds of gradient stores");
+static_assert(2 * kL * 8 == kSetup, "v and dy rows: one 16-byte piece per set-up thread");
+static_assert(kL * 16 == kSetup, "removal_state rows: four values per set-up thread");
+static_assert(O_COUNT * kL * 8 % kSetup == 0, "whole rounds of gradient stores");
 
 // per-chunk set-up, double-buffered (chunk c & 1)
 struct Prep {
@@ -85,8 +87,9 @@ struct BwdLds {
   bf16x8 frag[G_COUNT][64];         // step products with v, dy, sa, dsa (stacked)
   bf16_t xds[2][64][64];            // dS' hi/lo, [value j][key i]
   bf16_t xdsa[2][64][kL];           // dSA hi/lo, [value j][step t]
-  float red[kWaves][2][4][16];      // cross-quad scratch of the key-gradient waves
-  bf16_t outs[O_COUNT][kL][64];     // a chunk's bf16 gradients, written out as whole rows (out_at)
+  float red[kWaves][2][4][16];      // cross-quad scratch of the key-gradient stage
+  f32x4 kx[4][64];                  // the gradient waves' part of the decay gradient, per key tile
+  bf16_t outs[2][O_COUNT][kL][64];  // a chunk's bf16 gradients, written out as whole rows (out_at), double-buffered
   bf16_t zero[kL][64];              // an all-zero row tile
 };
 typedef float S0Rows[64][68];       // chunk 0's rebuilt start state, [key i][value j]
@@ -220,6 +223,9 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
   __shared__ BwdLds L;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
+  const bool grad = wave < kGradWaves;   // gradient waves 0-3, set-up waves 4-7
+  const int wq = wave & 3;               // value tile / key tile / key slice of the wave
+  const int utid = tid & (kSetup - 1);   // thread index within its group of four waves
   const int t = lane & 15, qd = lane >> 4;
   const int h = blockIdx.x, b = blockIdx.y, H = p.H, T = p.T;
   const int64_t bh = (int64_t)b * H + h;
@@ -228,23 +234,24 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
   const int nchunks = T / kL;
   const float* const ckbh = p.ckpt + bh * nchunks * (kHead * kHead);
 
-  // ---- staging through registers. bf16 rows as rotated pieces: piece p =
-  // 256 k + tid is row (p / 8) % 16, slot p % 8 of input p / 128, whose index
-  // is wave-uniform, so its pointer stays in scalar registers. The
-  // removal_state: thread tid holds row tid / 16, values 4 (tid % 16) .. + 3.
+  // ---- staging through registers (set-up waves). bf16 rows as rotated
+  // pieces: piece p = 256 k + utid is row (p / 8) % 16, slot p % 8 of input
+  // p / 128, whose index is wave-uniform, so its pointer stays in scalar
+  // registers. The removal_state: thread utid holds row utid / 16, values
+  // 4 (utid % 16) .. + 3.
   struct Pre { uint4 dec[kDecayRounds]; uint4 vy; f32x4 sa; };
-  // the sources, chosen once (waves 2 and 3 have no piece in the last decay
+  // the sources, chosen once (waves 6 and 7 have no piece in the last decay
   // round: they load input 4's again and do not stage it)
   const bf16_t* src[kDecayRounds + 1];
 #pragma unroll
   for (int k = 0; k < kDecayRounds; ++k) {
-    const int in = 2 * k + (wave >> 1);
+    const int in = 2 * k + (wq >> 1);
     src[k] = p.in[in < kDecayIn ? in : kDecayIn - 1] + tok0;
   }
-  src[kDecayRounds] = p.in[I_V + (wave >> 1)] + tok0;
-  const float* const sa_src = p.sa + tok0 + (int64_t)(tid >> 4) * tstride + 4 * (tid & 15);
-  // piece offset within a chunk: row (tid / 8) % 16, rotated slot
-  const int64_t piece_off = (int64_t)((tid >> 3) & 15) * tstride + 8 * (((tid & 7) - tile_rot((tid >> 3) & 15)) & 7);
+  src[kDecayRounds] = p.in[I_V + (wq >> 1)] + tok0;
+  const float* const sa_src = p.sa + tok0 + (int64_t)(utid >> 4) * tstride + 4 * (utid & 15);
+  // piece offset within a chunk: row (utid / 8) % 16, rotated slot
+  const int64_t piece_off = (int64_t)((utid >> 3) & 15) * tstride + 8 * (((utid & 7) - tile_rot((utid >> 3) & 15)) & 7);
   auto fetch = [&](int cdec, int cg) {   // chunk of the decay rows, chunk of the gradient rows
     Pre pr;
     const int64_t od = (int64_t)kL * cdec * tstride + piece_off;
@@ -257,27 +264,27 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
   auto stage_dec = [&](const Pre& pr) {
 #pragma unroll
     for (int k = 0; k < kDecayRounds; ++k)
-      if (2 * k + (wave >> 1) < kDecayIn) reinterpret_cast<uint4*>(&L.dec[0][0][0])[kBlock * k + tid] = pr.dec[k];
+      if (2 * k + (wq >> 1) < kDecayIn) reinterpret_cast<uint4*>(&L.dec[0][0][0])[kSetup * k + utid] = pr.dec[k];
   };
   auto stage_grad = [&](const Pre& pr, int sb) {
-    reinterpret_cast<uint4*>(&L.stg[sb][0][0][0])[tid] = pr.vy;   // v rows, then dy rows
+    reinterpret_cast<uint4*>(&L.stg[sb][0][0][0])[utid] = pr.vy;   // v rows, then dy rows
     const Split4 s = split4(pr.sa);
-    write4(L.stg[sb][S_SAH], tid >> 4, 4 * (tid & 15), s.hi);
-    write4(L.stg[sb][S_SAL], tid >> 4, 4 * (tid & 15), s.lo);
+    write4(L.stg[sb][S_SAH], utid >> 4, 4 * (utid & 15), s.hi);
+    write4(L.stg[sb][S_SAL], utid >> 4, 4 * (utid & 15), s.lo);
   };
 
-  // ---- state gradient: value tile jb = wave, key tiles ib, result layout
-  // (rows = key i = 16 ib + 4 qd + r, columns = value j = 16 jb + t)
-  const int jb = wave, jcol = 16 * jb + t;
+  // ---- state gradient (gradient waves): value tile jb = wq, key tiles ib,
+  // result layout (rows = key i = 16 ib + 4 qd + r, columns = value j = 16 jb + t)
+  const int jb = wq, jcol = 16 * jb + t;
   f32x4 dS[4];
 #pragma unroll
   for (int ib = 0; ib < 4; ++ib) {
-    if (p.dsT)
+    if (grad && p.dsT)
       dS[ib] = *reinterpret_cast<const f32x4*>(p.dsT + bh * (kHead * kHead) + jcol * kHead + 16 * ib + 4 * qd);
     else
       dS[ib] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  const int ki = 16 * wave + t;   // key of the lane in the key-gradient stage (column of its tile)
+  const int ki = 16 * wq + t;   // key of the lane in the key-gradient stage (column of its tile)
 
   // start state S0 of chunk c >= 1 (the checkpoint of chunk c - 1) as the
   // rows [key ki][value 32 m + 4 qd .., + 16 ..] of the key stage; loaded at
@@ -291,131 +298,119 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
     }
   };
 
-  // the staged gradient tiles of chunk cc to memory: thread tid writes
-  // 16-byte pieces p = 256 k + tid (tile p / 128, row (p / 8) % 16)
-  // (tile 2 k + wave / 2 is wave-uniform: the destination is picked by scalar
-  // selects and stays a global pointer)
+  // the staged gradient tiles of chunk cc to memory (set-up waves): thread
+  // utid writes 16-byte pieces p = 256 k + utid (tile p / 128, row (p / 8) %
+  // 16); tile 2 k + wq / 2 is wave-uniform, so the destination is picked by
+  // scalar selects and stays a global pointer
   bf16_t* dst[kOutRounds];
 #pragma unroll
   for (int k = 0; k < kOutRounds; ++k) {
-    const int tile = 2 * k + (wave >> 1);
+    const int tile = 2 * k + (wq >> 1);
     bf16_t* const q = tile == O_DV ? p.dv : tile == O_DK ? p.dk : tile == O_DB ? p.db
                     : tile == O_DR ? p.dr : tile == O_DA ? p.da : p.dw;
-    dst[k] = q + tok0 + (int64_t)((tid >> 3) & 15) * tstride + 8 * (tid & 7);
+    dst[k] = q + tok0 + (int64_t)((utid >> 3) & 15) * tstride + 8 * (utid & 7);
   }
   auto flush = [&](int cc) {
 #pragma unroll
     for (int k = 0; k < kOutRounds; ++k) {
-      const int tile = 2 * k + (wave >> 1), row = (tid >> 3) & 15;
-      const uint4 v = *reinterpret_cast<const uint4*>(&out_at(L.outs[tile], row, 8 * (tid & 7)));
+      const int tile = 2 * k + (wq >> 1), row = (utid >> 3) & 15;
+      const uint4 v = *reinterpret_cast<const uint4*>(&out_at(L.outs[cc & 1][tile], row, 8 * (utid & 7)));
       *reinterpret_cast<uint4*>(dst[k] + (int64_t)kL * cc * tstride) = v;
     }
   };
 
-  // ---- prologue: set up the last chunk
+  // the decay gradient of chunk cc, finished by the set-up wave of key tile
+  // wq from its own part (carried in registers) and the gradient wave's part
+  f32x4 carry = {0.f, 0.f, 0.f, 0.f}, sig = carry;
+  auto finish = [&](int cc) {
+    const f32x4 kpart = L.kx[wq][lane];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float dwv = (carry[r] - kpart[r]) * kWScale * sig[r] * (1.0f - sig[r]);
+      out_at(L.outs[cc & 1][O_DW], 4 * qd + r, ki) = __builtin_bit_cast(bf16_t, (__bf16)dwv);
+    }
+  };
+
+  // ---- prologue: set up the last chunk (set-up waves)
   const int last = nchunks - 1;
-  reinterpret_cast<uint2*>(&L.zero[0][0])[tid] = make_uint2(0, 0);
-  {
+  if (!grad) {
+    reinterpret_cast<uint2*>(&L.zero[0][0])[utid] = make_uint2(0, 0);
     const Pre pr = fetch(last, last);
     stage_dec(pr);
     stage_grad(pr, last & 1);
   }
   lds_barrier();
-  setup_decays(L.prep[last & 1], decay_load(L.dec, wave, t, qd), wave, t, qd);
+  if (!grad) setup_decays(L.prep[last & 1], decay_load(L.dec, wq, t, qd), wq, t, qd);
   lds_barrier();
-  if (last >= 1) stage_dec(fetch(last - 1, last));
-  setup_products(L.prep[last & 1], products_load(L.prep[last & 1], wave, t, qd), wave, t, qd, lane);
+  if (!grad) {
+    if (last >= 1) stage_dec(fetch(last - 1, last));
+    setup_products(L.prep[last & 1], products_load(L.prep[last & 1], wq, t, qd), wq, t, qd, lane);
+  }
 
   // one chunk; kFull: chunk c - 1 exists and is set up alongside (c >= 1).
-  // The last iteration (c == 0) is peeled so the loop body has no branches
-  // between the streams of a phase.
+  // The last iteration (c == 0) is peeled.
   auto run_chunk = [&](const int c, auto full) {
     constexpr bool kFull = decltype(full)::value;
     const int sb = c & 1;
     Prep& P = L.prep[sb];
     Prep& Pn = L.prep[sb ^ 1];   // set-up of chunk c - 1
     const bf16_t (*const stg)[kL][64] = L.stg[sb];
+    bf16_t (*const outs)[kL][64] = L.outs[sb];
     S0Rows& s0r = *reinterpret_cast<S0Rows*>(&L.prep[1]);   // used at c == 0 only
     lds_barrier();
 
     // ================= phase A
-    if (c < last) flush(c + 1);   // gradients of the previous chunk
     Pre pre;
     f32x4 S0row[2][2];
-    if constexpr (kFull) {
-      // at c == 1 the decay rows of chunk 0 are fetched again (harmless, and
-      // the reversal of chunk 0 reads them)
-      pre = fetch(c >= 2 ? c - 2 : 0, c - 1);
-      load_s0(c, S0row);
-    } else {
-      // rebuild S0 by reversing the chunk's 16 steps from its checkpoint
-      // (kernel.rs:239-246): S_{t-1} = (S_t - v_t k_t^T - sa_t b_t^T) / w~_t.
-      // The decay-rows buffer still holds chunk 0's rows; sa in fp32 from memory.
-      const float* ck = ckbh;
-      f32x4 S0t[4];
+    f32x4 dv;
+    if (grad) {
+      if constexpr (!kFull) {
+        // rebuild S0 by reversing the chunk's 16 steps from its checkpoint
+        // (kernel.rs:239-246): S_{t-1} = (S_t - v_t k_t^T - sa_t b_t^T) / w~_t.
+        // The decay-rows buffer still holds chunk 0's rows; sa in fp32 from memory.
+        const float* ck = ckbh;
+        f32x4 S0t[4];
 #pragma unroll
-      for (int ib = 0; ib < 4; ++ib)
+        for (int ib = 0; ib < 4; ++ib)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) S0t[ib][r] = ck[(16 * ib + 4 * qd + r) * kHead + jcol];
-      for (int tt = kL - 1; tt >= 0; --tt) {
-        const float vj = __uint_as_float((uint32_t)__builtin_bit_cast(uint16_t, *tile_at(stg[S_V], tt, jcol)) << 16);
-        const float sj = p.sa[tok0 + (int64_t)tt * tstride + jcol];
+          for (int r = 0; r < 4; ++r) S0t[ib][r] = ck[(16 * ib + 4 * qd + r) * kHead + jcol];
+        for (int tt = kL - 1; tt >= 0; --tt) {
+          const float vj = __uint_as_float((uint32_t)__builtin_bit_cast(uint16_t, *tile_at(stg[S_V], tt, jcol)) << 16);
+          const float sj = p.sa[tok0 + (int64_t)tt * tstride + jcol];
 #pragma unroll
-        for (int ib = 0; ib < 4; ++ib) {
-          const f32x4 kv = widen4(read4(L.dec[I_K], tt, 16 * ib + 4 * qd));
-          const f32x4 bv = widen4(read4(L.dec[I_B], tt, 16 * ib + 4 * qd));
+          for (int ib = 0; ib < 4; ++ib) {
+            const f32x4 kv = widen4(read4(L.dec[I_K], tt, 16 * ib + 4 * qd));
+            const f32x4 bv = widen4(read4(L.dec[I_B], tt, 16 * ib + 4 * qd));
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float winv = exp2_f(-P.lwT[16 * ib + 4 * qd + r][tt]);
-            S0t[ib][r] = (S0t[ib][r] - kv[r] * vj - bv[r] * sj) * winv;
+            for (int r = 0; r < 4; ++r) {
+              const float winv = exp2_f(-P.lwT[16 * ib + 4 * qd + r][tt]);
+              S0t[ib][r] = (S0t[ib][r] - kv[r] * vj - bv[r] * sj) * winv;
+            }
           }
         }
+#pragma unroll
+        for (int ib = 0; ib < 4; ++ib)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) s0r[16 * ib + 4 * qd + r][jcol] = S0t[ib][r];
       }
+      // the chain's LDS operands first, so their latency overlaps
+      f32x4 glv[4];
 #pragma unroll
-      for (int ib = 0; ib < 4; ++ib)
+      for (int ib = 0; ib < 4; ++ib) glv[ib] = *reinterpret_cast<const f32x4*>(&P.gl[16 * ib + 4 * qd]);
+      const Split8 Bt0 = row_pair(P.rows[T_BH], P.rows[T_BL], t, 0, qd);
+      const Split8 Bt1 = row_pair(P.rows[T_BH], P.rows[T_BL], t, 1, qd);
+      const Split8 Kt0 = row_pair(P.rows[T_KH], P.rows[T_KL], t, 0, qd);
+      const Split8 Kt1 = row_pair(P.rows[T_KH], P.rows[T_KL], t, 1, qd);
+      const bf16x4 dycf = tr_frag(stg[S_DY], 0, 16 * jb, lane);   // dY[s][j] (k = s)
+      const bf16x8 f_rbt = P.frag[F_RBT][lane], f_pt = P.frag[F_PT][lane];
+      const bf16x8 f_rkt = P.frag[F_RKT][lane], f_akt = P.frag[F_AKT][lane];
+      bf16x8 rT[4], aT[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) s0r[16 * ib + 4 * qd + r][jcol] = S0t[ib][r];
-    }
-    // all of phase A's LDS operands first, so their latency overlaps
-    f32x4 glv[4];
-#pragma unroll
-    for (int ib = 0; ib < 4; ++ib) glv[ib] = *reinterpret_cast<const f32x4*>(&P.gl[16 * ib + 4 * qd]);
-    const Split8 Bt0 = row_pair(P.rows[T_BH], P.rows[T_BL], t, 0, qd);
-    const Split8 Bt1 = row_pair(P.rows[T_BH], P.rows[T_BL], t, 1, qd);
-    const Split8 Kt0 = row_pair(P.rows[T_KH], P.rows[T_KL], t, 0, qd);
-    const Split8 Kt1 = row_pair(P.rows[T_KH], P.rows[T_KL], t, 1, qd);
-    const bf16x4 dycf = tr_frag(stg[S_DY], 0, 16 * jb, lane);   // dY[s][j] (k = s)
-    const bf16x8 f_rbt = P.frag[F_RBT][lane], f_pt = P.frag[F_PT][lane];
-    const bf16x8 f_rkt = P.frag[F_RKT][lane], f_akt = P.frag[F_AKT][lane];
-    bf16x8 rT[4], aT[4];
-#pragma unroll
-    for (int ib = 0; ib < 4; ++ib) {
-      rT[ib] = cat8(tr_frag(P.rows[T_RH], 0, 16 * ib, lane), tr_frag(P.rows[T_RL], 0, 16 * ib, lane));
-      aT[ib] = cat8(tr_frag(P.rows[T_AH], 0, 16 * ib, lane), tr_frag(P.rows[T_AL], 0, 16 * ib, lane));
-    }
-    DecayIn din;
-    if constexpr (kFull) din = decay_load(L.dec, wave, t, qd);
-    // step products of v, dy, sa (one per wave), as D = X1 Y1^T + X2 Y2^T:
-    // B_yv^T = dy v^T (s >= t), C_dyv^T = v dy^T (s <= t),
-    // B_ysa^T = dy sa^T (s >= t), C_dysa^T = sa dy^T (s <= t)
-    bf16x8 px1[2], py1[2], px2[2], py2[2];
-    {
-      const int x1 = wave == 1 ? S_V : wave == 3 ? S_SAH : S_DY;
-      const int y1 = wave == 0 ? S_V : wave == 2 ? S_SAH : S_DY;
-      const int y2 = wave == 0 ? S_V : wave == 2 ? S_SAL : S_DY;
-      const bf16_t (*const x2)[64] = wave == 2 ? stg[S_DY] : wave == 3 ? stg[S_SAL] : L.zero;
-#pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        px1[m] = row_frag(stg[x1], t, m, qd);
-        py1[m] = row_frag(stg[y1], t, m, qd);
-        px2[m] = row_frag(x2, t, m, qd);
-        py2[m] = row_frag(stg[y2], t, m, qd);
+      for (int ib = 0; ib < 4; ++ib) {
+        rT[ib] = cat8(tr_frag(P.rows[T_RH], 0, 16 * ib, lane), tr_frag(P.rows[T_RL], 0, 16 * ib, lane));
+        aT[ib] = cat8(tr_frag(P.rows[T_AH], 0, 16 * ib, lane), tr_frag(P.rows[T_AL], 0, 16 * ib, lane));
       }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-
-    f32x4 dv;
-    {
+      __builtin_amdgcn_sched_barrier(0);
       f32x4 dSp[4];
 #pragma unroll
       for (int ib = 0; ib < 4; ++ib) dSp[ib] = dS[ib] * glv[ib];
@@ -446,169 +441,191 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
         }
       *reinterpret_cast<bf16x4*>(xdsa_at(L.xdsa[0], jcol, qd)) = dsas.hi;
       *reinterpret_cast<bf16x4*>(xdsa_at(L.xdsa[1], jcol, qd)) = dsas.lo;
+    } else {
+      if (c < last) finish(c + 1);
+      if constexpr (kFull) {
+        // at c == 1 the decay rows of chunk 0 are fetched again (harmless, and
+        // the reversal of chunk 0 reads them)
+        pre = fetch(c >= 2 ? c - 2 : 0, c - 1);
+        load_s0(c, S0row);
+        setup_decays(Pn, decay_load(L.dec, wq, t, qd), wq, t, qd);
+      }
     }
-    if constexpr (kFull) setup_decays(Pn, din, wave, t, qd);
-    {
+    lds_barrier();
+
+    // ================= phase B
+    // dSA as row fragments (row = step t, k = value), from the [j][t] tiles
+    auto dsa_frag = [&](int hl, int m) {
+      return cat8(read_tr16(xdsa_at(L.xdsa[hl], 32 * m + 4 * qd + (t >> 2), t & 3)),
+                  read_tr16(xdsa_at(L.xdsa[hl], 32 * m + 16 + 4 * qd + (t >> 2), t & 3)));
+    };
+    if (grad) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) out_at(outs[O_DV], 4 * qd + r, jcol) = __builtin_bit_cast(bf16_t, (__bf16)dv[r]);
+      // step products of v, dy, sa (one per wave), as D = X1 Y1^T + X2 Y2^T:
+      // B_yv^T = dy v^T (s >= t), C_dyv^T = v dy^T (s <= t),
+      // B_ysa^T = dy sa^T (s >= t), C_dysa^T = sa dy^T (s <= t)
+      const int x1 = wq == 1 ? S_V : wq == 3 ? S_SAH : S_DY;
+      const int y1 = wq == 0 ? S_V : wq == 2 ? S_SAH : S_DY;
+      const int y2 = wq == 0 ? S_V : wq == 2 ? S_SAL : S_DY;
+      const bf16_t (*const x2)[64] = wq == 2 ? stg[S_DY] : wq == 3 ? stg[S_SAL] : L.zero;
+      bf16x8 px1[2], py1[2], px2[2], py2[2];
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        px1[m] = row_frag(stg[x1], t, m, qd);
+        py1[m] = row_frag(stg[y1], t, m, qd);
+        px2[m] = row_frag(x2, t, m, qd);
+        py2[m] = row_frag(stg[y2], t, m, qd);
+      }
+      // step products with dSA (one per wave): B_sav^T = dsa v^T (s > t),
+      // C_dsav^T = v dsa^T (s < t), B_sasa^T = dsa sa^T (s > t),
+      // C_dsasa^T = sa dsa^T (s < t)
+      const Split8 q[2] = {{dsa_frag(0, 0), dsa_frag(1, 0)}, {dsa_frag(0, 1), dsa_frag(1, 1)}};
+      Split8 g[2];
+      {
+        const bf16_t (*const ylo)[64] = wq >= 2 ? stg[S_SAL] : L.zero;
+        const int yhi = wq >= 2 ? S_SAH : S_V;
+#pragma unroll
+        for (int m = 0; m < 2; ++m) g[m] = Split8{row_frag(stg[yhi], t, m, qd), row_frag(ylo, t, m, qd)};
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      const int sgn = (wq & 1) ? -1 : 1;   // keep s >= t / s > t (B_), s <= t / s < t (C_)
       f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
         d = mma32(px2[m], py2[m], d);
         d = mma32(px1[m], py1[m], d);
       }
-      const int sgn = (wave & 1) ? -1 : 1;   // keep s >= t (B_), s <= t (C_)
 #pragma unroll
       for (int r = 0; r < 4; ++r) d[r] = sgn * (4 * qd + r - t) >= 0 ? d[r] : 0.f;
-      L.frag[G_BYV + wave][lane] = stack_f(d);
-    }
-    lds_barrier();
-
-    // ================= phase B
-    if constexpr (kFull) {
-      stage_dec(pre);             // decay rows of chunk c - 2 (the decays of phase A are done)
-      stage_grad(pre, sb ^ 1);    // gradient rows of chunk c - 1 (free buffer)
-    }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) out_at(L.outs[O_DV], 4 * qd + r, jcol) = __builtin_bit_cast(bf16_t, (__bf16)dv[r]);
-    // dSA as row fragments (row = step t, k = value), from the [j][t] tiles
-    auto dsa_frag = [&](int hl, int m) {
-      return cat8(read_tr16(xdsa_at(L.xdsa[hl], 32 * m + 4 * qd + (t >> 2), t & 3)),
-                  read_tr16(xdsa_at(L.xdsa[hl], 32 * m + 16 + 4 * qd + (t >> 2), t & 3)));
-    };
-    GramIn gin;
-    if constexpr (kFull) gin = products_load(Pn, wave, t, qd);
-    // step products with dSA (one per wave): B_sav^T = dsa v^T (s > t),
-    // C_dsav^T = v dsa^T (s < t), B_sasa^T = dsa sa^T (s > t),
-    // C_dsasa^T = sa dsa^T (s < t)
-    const Split8 q[2] = {{dsa_frag(0, 0), dsa_frag(1, 0)}, {dsa_frag(0, 1), dsa_frag(1, 1)}};
-    Split8 g[2];
-    {
-      const bf16_t (*const ylo)[64] = wave >= 2 ? stg[S_SAL] : L.zero;
-      const int yhi = wave >= 2 ? S_SAH : S_V;
-#pragma unroll
-      for (int m = 0; m < 2; ++m) g[m] = Split8{row_frag(stg[yhi], t, m, qd), row_frag(ylo, t, m, qd)};
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    if constexpr (kFull) setup_products(Pn, gin, wave, t, qd, lane);
-    {
+      L.frag[G_BYV + wq][lane] = stack_f(d);
       // both orientations, the wave keeps one (no branch in the phase)
       f32x4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = d0;
       d0 = mma32x3(q[0], g[0], d0);
       d0 = mma32x3(q[1], g[1], d0);
       d1 = mma32x3(g[0], q[0], d1);
       d1 = mma32x3(g[1], q[1], d1);
-      const int sgn = (wave & 1) ? -1 : 1;   // keep s > t (B_), s < t (C_)
-      f32x4 d = (wave & 1) ? d1 : d0;
+      f32x4 e = (wq & 1) ? d1 : d0;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) d[r] = sgn * (4 * qd + r - t) > 0 ? d[r] : 0.f;
-      L.frag[G_BSAV + wave][lane] = stack_f(d);
+      for (int r = 0; r < 4; ++r) e[r] = sgn * (4 * qd + r - t) > 0 ? e[r] : 0.f;
+      L.frag[G_BSAV + wq][lane] = stack_f(e);
+    } else {
+      if (c < last) flush(c + 1);
+      if constexpr (kFull) {
+        stage_dec(pre);             // decay rows of chunk c - 2 (the decays of phase A are done)
+        stage_grad(pre, sb ^ 1);    // gradient rows of chunk c - 1 (free buffer)
+        setup_products(Pn, products_load(Pn, wq, t, qd), wq, t, qd, lane);
+      }
     }
     lds_barrier();
 
-    // ================= phase C
+    // ================= phase C: key-indexed gradients of key tile kb = wq,
+    // result layout rows = step 4 qd + r, column = key ki; the gradient wave
+    // forms dK and dB, the set-up wave dR, dA and the decay gradient's parts
     {
-      const int kb = wave;   // key tile; result layout rows = step 4 qd + r, column = key ki
-      // all LDS operands first: decayed rows as B operands (k = step, column
-      // = key), split
+      const int kb = wq;
+      // decayed rows as B operands (k = step, column = key), split
       const Split4 Rc{tr_frag(P.rows[T_RH], 0, 16 * kb, lane), tr_frag(P.rows[T_RL], 0, 16 * kb, lane)};
       const Split4 Ac{tr_frag(P.rows[T_AH], 0, 16 * kb, lane), tr_frag(P.rows[T_AL], 0, 16 * kb, lane)};
       const Split4 Kc{tr_frag(P.rows[T_KH], 0, 16 * kb, lane), tr_frag(P.rows[T_KL], 0, 16 * kb, lane)};
       const Split4 Bc{tr_frag(P.rows[T_BH], 0, 16 * kb, lane), tr_frag(P.rows[T_BL], 0, 16 * kb, lane)};
-      // start state (k = value j, column = key ki)
-      f32x4 S0v[2][2];
-#pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        if constexpr (kFull) {
-          S0v[m][0] = S0row[m][0];
-          S0v[m][1] = S0row[m][1];
-        } else {
-          S0v[m][0] = *reinterpret_cast<const f32x4*>(&s0r[ki][32 * m + 4 * qd]);
-          S0v[m][1] = *reinterpret_cast<const f32x4*>(&s0r[ki][32 * m + 16 + 4 * qd]);
-        }
-      }
       // dS' as B operand (k = value j, column = key ki)
       Split8 Db[2];
 #pragma unroll
       for (int m = 0; m < 2; ++m)
         Db[m] = Split8{tr_frag32(L.xds[0], m, 16 * kb, lane), tr_frag32(L.xds[1], m, 16 * kb, lane)};
-      const bf16x8 v0 = row_frag(stg[S_V], t, 0, qd), v1 = row_frag(stg[S_V], t, 1, qd);
-      const bf16x8 y0 = row_frag(stg[S_DY], t, 0, qd), y1 = row_frag(stg[S_DY], t, 1, qd);
-      const Split8 s0f = row_pair(stg[S_SAH], stg[S_SAL], t, 0, qd);
-      const Split8 s1f = row_pair(stg[S_SAH], stg[S_SAL], t, 1, qd);
-      const Split8 q0{dsa_frag(0, 0), dsa_frag(1, 0)}, q1{dsa_frag(0, 1), dsa_frag(1, 1)};
-      bf16x8 fg[G_COUNT];
-#pragma unroll
-      for (int i = 0; i < G_COUNT; ++i) fg[i] = L.frag[i][lane];
       const f32x4 g4 = *reinterpret_cast<const f32x4*>(&P.gT[ki][4 * qd]);
-      const f32x4 lw4 = *reinterpret_cast<const f32x4*>(&P.lwT[ki][4 * qd]);
-      __builtin_amdgcn_sched_barrier(0);
-      Split8 S0b[2];
-#pragma unroll
-      for (int m = 0; m < 2; ++m) S0b[m] = split8(S0v[m][0], S0v[m][1]);
       const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-
-      // V dS' (= d k- gamma_L) and SA dS' (= d b- gamma_L)
-      f32x4 x1 = mma32(v0, Db[0].lo, z);
-      x1 = mma32(v1, Db[1].lo, x1);
-      x1 = mma32(v0, Db[0].hi, x1);
-      x1 = mma32(v1, Db[1].hi, x1);
-      f32x4 x2 = mma32x3(s0f, Db[0], z);
-      x2 = mma32x3(s1f, Db[1], x2);
-      // the decayed rows at (step 4 qd + r, key ki) in fp32
-      float Rf[4], Af[4], Kf[4], Bf[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        Rf[r] = hi_lo(Rc.hi, Rc.lo, r);
-        Af[r] = hi_lo(Ac.hi, Ac.lo, r);
-        Kf[r] = hi_lo(Kc.hi, Kc.lo, r);
-        Bf[r] = hi_lo(Bc.hi, Bc.lo, r);
-      }
-      // sum over the chunk's steps of K~ o V dS' + B~ o SA dS', and over this
-      // lane's 16 values j of S0 o dS' (S0 and dS' hold the same j per element)
       float epart = 0.f;
+      f32x4 f, suf;
+      if (grad) {
+        const bf16x8 v0 = row_frag(stg[S_V], t, 0, qd), v1 = row_frag(stg[S_V], t, 1, qd);
+        const Split8 s0f = row_pair(stg[S_SAH], stg[S_SAL], t, 0, qd);
+        const Split8 s1f = row_pair(stg[S_SAH], stg[S_SAL], t, 1, qd);
+        const bf16x8 f_byv = L.frag[G_BYV][lane], f_bsav = L.frag[G_BSAV][lane];
+        const bf16x8 f_bysa = L.frag[G_BYSA][lane], f_bsasa = L.frag[G_BSASA][lane];
+        __builtin_amdgcn_sched_barrier(0);
+        // V dS' (= d k- gamma_L) and SA dS' (= d b- gamma_L)
+        f32x4 x1 = mma32(v0, Db[0].lo, z);
+        x1 = mma32(v1, Db[1].lo, x1);
+        x1 = mma32(v0, Db[0].hi, x1);
+        x1 = mma32(v1, Db[1].hi, x1);
+        f32x4 x2 = mma32x3(s0f, Db[0], z);
+        x2 = mma32x3(s1f, Db[1], x2);
+        f32x4 dk = mma_s3(f_byv, Rc, x1);
+        dk = mma_s3(f_bsav, Ac, dk);
+        f32x4 dbv = mma_s3(f_bysa, Rc, x2);
+        dbv = mma_s3(f_bsasa, Ac, dbv);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) epart += Kf[r] * x1[r] + Bf[r] * x2[r];
-#pragma unroll
-      for (int m = 0; m < 2; ++m)
-#pragma unroll
-        for (int e = 0; e < 8; e += 2) {
-          const bf16x2 sh = {S0b[m].hi[e], S0b[m].hi[e + 1]}, sl = {S0b[m].lo[e], S0b[m].lo[e + 1]};
-          const bf16x2 dh = {Db[m].hi[e], Db[m].hi[e + 1]}, dl = {Db[m].lo[e], Db[m].lo[e + 1]};
-          epart = __builtin_amdgcn_fdot2_f32_bf16(sh, dh, epart, false);
-          epart = __builtin_amdgcn_fdot2_f32_bf16(sh, dl, epart, false);
-          epart = __builtin_amdgcn_fdot2_f32_bf16(sl, dh, epart, false);
+        for (int r = 0; r < 4; ++r) {
+          const float kf = hi_lo(Kc.hi, Kc.lo, r), bf = hi_lo(Bc.hi, Bc.lo, r);
+          // sum over the chunk's steps of K~ o V dS' + B~ o SA dS'
+          epart += kf * x1[r] + bf * x2[r];
+          // this wave's part of dL/dg, before the decay factors: K~ o dk' + B~ o db'
+          f[r] = kf * dk[r] + bf * dbv[r];
+          const float gin = exp2_f(-g4[r]);
+          out_at(outs[O_DK], 4 * qd + r, ki) = __builtin_bit_cast(bf16_t, (__bf16)(dk[r] * gin));
+          out_at(outs[O_DB], 4 * qd + r, ki) = __builtin_bit_cast(bf16_t, (__bf16)(dbv[r] * gin));
         }
-      f32x4 dk = mma_s3(fg[G_BYV], Rc, x1);
-      dk = mma_s3(fg[G_BSAV], Ac, dk);
-      f32x4 dbv = mma_s3(fg[G_BYSA], Rc, x2);
-      dbv = mma_s3(fg[G_BSASA], Ac, dbv);
-      // dY S0 and dSA S0
-      f32x4 dr = mma32(y0, S0b[0].lo, z);
-      dr = mma32(y1, S0b[1].lo, dr);
-      dr = mma32(y0, S0b[0].hi, dr);
-      dr = mma32(y1, S0b[1].hi, dr);
-      dr = mma_s3(fg[G_CDYV], Kc, dr);
-      dr = mma_s3(fg[G_CDYSA], Bc, dr);
-      f32x4 da = mma32x3(q0, S0b[0], z);
-      da = mma32x3(q1, S0b[1], da);
-      da = mma_s3(fg[G_CDSAV], Kc, da);
-      da = mma_s3(fg[G_CDSASA], Bc, da);
-
-      // dL/dg: r dr - k dk - b db + a da, formed before the decay factors as
-      // R^ o dr' - K~ o dk' - B~ o db' + A^ o da' (x' = the products above)
-      f32x4 f, ad, sig;
+      } else {
+        // start state as B operand (k = value j, column = key ki), split
+        f32x4 S0v[2][2];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        ad[r] = Af[r] * da[r];
-        f[r] = Rf[r] * dr[r] - Kf[r] * dk[r] - Bf[r] * dbv[r] + ad[r];
-        const float gam = exp2_f(g4[r]), gin = exp2_f(-g4[r]), gpv = exp2_f(g4[r] - lw4[r]);
-        dk[r] *= gin;
-        dbv[r] *= gin;
-        dr[r] *= gam;
-        da[r] *= gpv;
-        sig[r] = lw4[r] * kSigFromLw2;
+        for (int m = 0; m < 2; ++m) {
+          if constexpr (kFull) {
+            S0v[m][0] = S0row[m][0];
+            S0v[m][1] = S0row[m][1];
+          } else {
+            S0v[m][0] = *reinterpret_cast<const f32x4*>(&s0r[ki][32 * m + 4 * qd]);
+            S0v[m][1] = *reinterpret_cast<const f32x4*>(&s0r[ki][32 * m + 16 + 4 * qd]);
+          }
+        }
+        const bf16x8 y0 = row_frag(stg[S_DY], t, 0, qd), y1 = row_frag(stg[S_DY], t, 1, qd);
+        const Split8 q0{dsa_frag(0, 0), dsa_frag(1, 0)}, q1{dsa_frag(0, 1), dsa_frag(1, 1)};
+        const bf16x8 f_cdyv = L.frag[G_CDYV][lane], f_cdysa = L.frag[G_CDYSA][lane];
+        const bf16x8 f_cdsav = L.frag[G_CDSAV][lane], f_cdsasa = L.frag[G_CDSASA][lane];
+        const f32x4 lw4 = *reinterpret_cast<const f32x4*>(&P.lwT[ki][4 * qd]);
+        __builtin_amdgcn_sched_barrier(0);
+        Split8 S0b[2];
+#pragma unroll
+        for (int m = 0; m < 2; ++m) S0b[m] = split8(S0v[m][0], S0v[m][1]);
+        // dY S0 and dSA S0
+        f32x4 dr = mma32(y0, S0b[0].lo, z);
+        dr = mma32(y1, S0b[1].lo, dr);
+        dr = mma32(y0, S0b[0].hi, dr);
+        dr = mma32(y1, S0b[1].hi, dr);
+        dr = mma_s3(f_cdyv, Kc, dr);
+        dr = mma_s3(f_cdysa, Bc, dr);
+        f32x4 da = mma32x3(q0, S0b[0], z);
+        da = mma32x3(q1, S0b[1], da);
+        da = mma_s3(f_cdsav, Kc, da);
+        da = mma_s3(f_cdsasa, Bc, da);
+        // sum over this lane's 16 values j of S0 o dS' (S0 and dS' hold the
+        // same j per element)
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+#pragma unroll
+          for (int e = 0; e < 8; e += 2) {
+            const bf16x2 sh = {S0b[m].hi[e], S0b[m].hi[e + 1]}, sl = {S0b[m].lo[e], S0b[m].lo[e + 1]};
+            const bf16x2 dh = {Db[m].hi[e], Db[m].hi[e + 1]}, dl = {Db[m].lo[e], Db[m].lo[e + 1]};
+            epart = __builtin_amdgcn_fdot2_f32_bf16(sh, dh, epart, false);
+            epart = __builtin_amdgcn_fdot2_f32_bf16(sh, dl, epart, false);
+            epart = __builtin_amdgcn_fdot2_f32_bf16(sl, dh, epart, false);
+          }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float rf = hi_lo(Rc.hi, Rc.lo, r), af = hi_lo(Ac.hi, Ac.lo, r);
+          const float ad = af * da[r];
+          // this wave's part of dL/dg before the decay factors: R^ o dr' + A^ o da'
+          f[r] = rf * dr[r] + ad;
+          carry[r] = -ad;
+          sig[r] = lw4[r] * kSigFromLw2;
+          const float gam = exp2_f(g4[r]), gpv = exp2_f(g4[r] - lw4[r]);
+          out_at(outs[O_DR], 4 * qd + r, ki) = __builtin_bit_cast(bf16_t, (__bf16)(dr[r] * gam));
+          out_at(outs[O_DA], 4 * qd + r, ki) = __builtin_bit_cast(bf16_t, (__bf16)(da[r] * gpv));
+        }
       }
       // suffix sums over the chunk's steps: in-lane over r, then over quads
-      f32x4 suf;
       suf[3] = f[3];
       suf[2] = f[2] + suf[3];
       suf[1] = f[1] + suf[2];
@@ -618,21 +635,20 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
       wave_lds_sync();
       float above = 0.f, etot = 0.f;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float fq = L.red[wave][0][q][t];
-        above += q > qd ? fq : 0.f;
-        etot += L.red[wave][1][q][t];
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const float fq = L.red[wave][0][q4][t];
+        above += q4 > qd ? fq : 0.f;
+        etot += L.red[wave][1][q4][t];
       }
+      // dlw = (R^ o dr' + A^ o da' suffix) - (K~ o dk' + B~ o db' suffix)
+      //       - a da + E: the gradient wave leaves its part, the set-up wave
+      //       keeps its own and combines after the next barrier
+      if (grad) {
+        L.kx[kb][lane] = f32x4{suf[0] + above - etot, suf[1] + above - etot,
+                               suf[2] + above - etot, suf[3] + above - etot};
+      } else {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float dlw = suf[r] + above - ad[r] + etot;
-        const float dwv = dlw * kWScale * sig[r] * (1.0f - sig[r]);
-        const int tr = 4 * qd + r;
-        out_at(L.outs[O_DK], tr, ki) = __builtin_bit_cast(bf16_t, (__bf16)dk[r]);
-        out_at(L.outs[O_DB], tr, ki) = __builtin_bit_cast(bf16_t, (__bf16)dbv[r]);
-        out_at(L.outs[O_DR], tr, ki) = __builtin_bit_cast(bf16_t, (__bf16)dr[r]);
-        out_at(L.outs[O_DA], tr, ki) = __builtin_bit_cast(bf16_t, (__bf16)da[r]);
-        out_at(L.outs[O_DW], tr, ki) = __builtin_bit_cast(bf16_t, (__bf16)dwv);
+        for (int r = 0; r < 4; ++r) carry[r] += suf[r] + above + etot;
       }
     }
   };
@@ -640,8 +656,10 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
   run_chunk(0, std::false_type{});
 
   lds_barrier();
-  flush(0);
-  if (p.ds0) {
+  if (!grad) finish(0);
+  lds_barrier();
+  if (!grad) flush(0);
+  if (grad && p.ds0) {
 #pragma unroll
     for (int ib = 0; ib < 4; ++ib)
       *reinterpret_cast<f32x4*>(p.ds0 + bh * (kHead * kHead) + jcol * kHead + 16 * ib + 4 * qd) = dS[ib];
