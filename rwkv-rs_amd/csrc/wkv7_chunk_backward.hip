@@ -26,22 +26,26 @@
 // (divide by the decay, kernel.rs:239-246); the other chunks read it from the
 // previous checkpoint.
 //
-// Work layout: one workgroup of four waves per (batch, head), chunks in
-// reverse order. Only the state gradient is carried from chunk to chunk; the
-// per-chunk set-up that does not depend on it (decays, decayed rows, their
-// step-by-step products, P) is computed one chunk ahead, next to the current
-// chunk's gradients, so each phase gives every wave independent streams:
-//   phase A: state-gradient chain and dV of chunk c (wave w: value columns
-//            16w..16w+15) | decays and decayed rows of chunk c-1 (wave w:
-//            keys 16w..16w+15) | step products of v, dy, sa of chunk c
-//   phase B: step products with dSA of chunk c | step products of the
-//            decayed rows of chunk c-1 and P = (I - A_ab)^-1 (wave 0)
-//   phase C: key-indexed gradients of chunk c (wave w: keys 16w..16w+15)
-// Within a phase each wave first issues all its LDS reads, then computes.
-// Inputs are staged through registers, loaded in phase A and written to LDS
-// in phase B: the rows only the decays read (x, r, k, a, b) in one buffer,
-// two chunks ahead; v, dy and the removal_state (split into bf16 hi/lo rows
-// once, when staged) in two, one chunk ahead.
+// Work layout: one workgroup of eight waves per (batch, head), two per SIMD,
+// chunks in reverse order. Waves 0-3 ("gradient waves", wave w owns value
+// tile w and key tile w) carry the state gradient; waves 4-7 ("set-up
+// waves", key tile w - 4) do the per-chunk work that does not depend on it,
+// one chunk ahead, so each SIMD interleaves two instruction streams:
+//   phase A: gradient waves: state-gradient chain and dV of chunk c; set-up
+//            waves: staging loads, the finished decay gradient of chunk c+1;
+//            all waves: decays and decayed rows of chunk c-1 (keys 8w..8w+7)
+//   phase B: gradient waves: step products of v, dy, sa and with dSA of
+//            chunk c; set-up waves: gradient flush of chunk c+1, staging
+//            stores, step products of the decayed rows of chunk c-1 and
+//            P = (I - A_ab)^-1 (wave 4)
+//   phase C: key-indexed gradients of chunk c, key tile w: dK, dB and their
+//            part of the decay gradient on the gradient wave, dR, dA and the
+//            rest on the set-up wave, which finishes dw after the barrier
+// Within a phase each wave first issues its LDS reads, then computes. Inputs
+// are staged through registers, loaded in phase A and written to LDS in
+// phase B: the rows only the decays read (x, r, k, a, b) in one buffer, two
+// chunks ahead; v, dy and the removal_state (split into bf16 hi/lo rows once,
+// when staged) in two, one chunk ahead.
 #include <type_traits>
 
 #include "wkv7_chunk.hpp"
@@ -136,24 +140,31 @@ __device__ __forceinline__ Split8 row_pair(const bf16_t (*hi)[64], const bf16_t 
 }
 __device__ __forceinline__ float hi_lo(bf16x4 h, bf16x4 l, int r) { return (float)h[r] + (float)l[r]; }
 
-// ---- set-up of one chunk, step 1: decays and decayed rows, keys 16 wave ..
-struct DecayIn { uint2 x; bf16x4 a, r, k, b; };
-__device__ __forceinline__ DecayIn decay_load(const bf16_t (*dec)[kL][64], int wave, int t, int qd) {
-  const int c0 = 16 * wave + 4 * qd;
-  return DecayIn{*reinterpret_cast<const uint2*>(tile_at(dec[I_X], t, c0)), read4(dec[I_A], t, c0),
-                 read4(dec[I_R], t, c0), read4(dec[I_K], t, c0), read4(dec[I_B], t, c0)};
+// ---- set-up of one chunk, step 1: decays and decayed rows. Each of the 8
+// waves takes keys 8 w .. 8 w + 7, two per lane (keys 8 w + 2 qd, + 1).
+struct DecayIn { uint32_t x, a, r, k, b; };   // two bf16 each
+__device__ __forceinline__ uint32_t read2(const bf16_t (*tile)[64], int row, int c) {
+  return *reinterpret_cast<const uint32_t*>(tile_at(tile, row, c));
 }
+__device__ __forceinline__ void write2(bf16_t (*tile)[64], int row, int c, uint32_t v) {
+  *reinterpret_cast<uint32_t*>(tile_at(tile, row, c)) = v;
+}
+__device__ __forceinline__ DecayIn decay_load(const bf16_t (*dec)[kL][64], int wave, int t, int qd) {
+  const int c0 = 8 * wave + 2 * qd;
+  return DecayIn{read2(dec[I_X], t, c0), read2(dec[I_A], t, c0), read2(dec[I_R], t, c0),
+                 read2(dec[I_K], t, c0), read2(dec[I_B], t, c0)};
+}
+__device__ __forceinline__ float bf_lo(uint32_t u) { return __uint_as_float(u << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
 __device__ __forceinline__ void setup_decays(Prep& P, const DecayIn& in, int wave, int t, int qd) {
-  const int c0 = 16 * wave + 4 * qd;
+  const int c0 = 8 * wave + 2 * qd;
   // plain float arrays around the cross-lane (DPP) operations: this compiler
   // folds DPP builtins whose source is an element of an ext_vector value into
   // a single one (all elements get element 0's)
-  const uint2 xr = in.x;
-  const float xs[4] = {__uint_as_float(xr.x << 16), __uint_as_float(xr.x & 0xffff0000u),
-                       __uint_as_float(xr.y << 16), __uint_as_float(xr.y & 0xffff0000u)};
-  float g2[4], lw2[4], gam[4], gin[4], gpv[4], gL[4];
+  const float xs[2] = {bf_lo(in.x), bf_hi(in.x)};
+  float g2[2], lw2[2], gam[2], gin[2], gpv[2], gL[2];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
+  for (int e = 0; e < 2; ++e) {
     lw2[e] = log2_decay(xs[e]);
     g2[e] = row_scan16(lw2[e]);
     gam[e] = exp2_f(g2[e]);
@@ -162,27 +173,28 @@ __device__ __forceinline__ void setup_decays(Prep& P, const DecayIn& in, int wav
         __builtin_bit_cast(int, 1.0f), __builtin_bit_cast(int, gam[e]), 0x111, 0xf, 0xf, false));
     gL[e] = row_last16(gam[e]);
   }
-  const f32x4 gamv = {gam[0], gam[1], gam[2], gam[3]};
-  const f32x4 ginv = {gin[0], gin[1], gin[2], gin[3]};
-  const f32x4 gpvv = {gpv[0], gpv[1], gpv[2], gpv[3]};
-  const Split4 ah = split4(widen4(in.a) * gpvv);
-  const Split4 rh = split4(widen4(in.r) * gamv);
-  const Split4 kt = split4(widen4(in.k) * ginv);
-  const Split4 bt = split4(widen4(in.b) * ginv);
-  write4(P.rows[T_AH], t, c0, ah.hi);
-  write4(P.rows[T_AL], t, c0, ah.lo);
-  write4(P.rows[T_RH], t, c0, rh.hi);
-  write4(P.rows[T_RL], t, c0, rh.lo);
-  write4(P.rows[T_KH], t, c0, kt.hi);
-  write4(P.rows[T_KL], t, c0, kt.lo);
-  write4(P.rows[T_BH], t, c0, bt.hi);
-  write4(P.rows[T_BL], t, c0, bt.lo);
+  uint32_t hi, lo;
+  split2(bf_lo(in.a) * gpv[0], bf_hi(in.a) * gpv[1], hi, lo);
+  write2(P.rows[T_AH], t, c0, hi);
+  write2(P.rows[T_AL], t, c0, lo);
+  split2(bf_lo(in.r) * gam[0], bf_hi(in.r) * gam[1], hi, lo);
+  write2(P.rows[T_RH], t, c0, hi);
+  write2(P.rows[T_RL], t, c0, lo);
+  split2(bf_lo(in.k) * gin[0], bf_hi(in.k) * gin[1], hi, lo);
+  write2(P.rows[T_KH], t, c0, hi);
+  write2(P.rows[T_KL], t, c0, lo);
+  split2(bf_lo(in.b) * gin[0], bf_hi(in.b) * gin[1], hi, lo);
+  write2(P.rows[T_BH], t, c0, hi);
+  write2(P.rows[T_BL], t, c0, lo);
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
+  for (int e = 0; e < 2; ++e) {
     P.gT[c0 + e][t] = g2[e];
     P.lwT[c0 + e][t] = lw2[e];
   }
-  if (t == 0) *reinterpret_cast<f32x4*>(&P.gl[c0]) = f32x4{gL[0], gL[1], gL[2], gL[3]};
+  if (t == 0) {
+    P.gl[c0] = gL[0];
+    P.gl[c0 + 1] = gL[1];
+  }
 }
 
 // ---- set-up step 2: one step-by-step product of decayed rows per wave.
@@ -340,7 +352,7 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
     stage_grad(pr, last & 1);
   }
   lds_barrier();
-  if (!grad) setup_decays(L.prep[last & 1], decay_load(L.dec, wq, t, qd), wq, t, qd);
+  setup_decays(L.prep[last & 1], decay_load(L.dec, wave, t, qd), wave, t, qd);
   lds_barrier();
   if (!grad) {
     if (last >= 1) stage_dec(fetch(last - 1, last));
@@ -441,6 +453,7 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
         }
       *reinterpret_cast<bf16x4*>(xdsa_at(L.xdsa[0], jcol, qd)) = dsas.hi;
       *reinterpret_cast<bf16x4*>(xdsa_at(L.xdsa[1], jcol, qd)) = dsas.lo;
+      if constexpr (kFull) setup_decays(Pn, decay_load(L.dec, wave, t, qd), wave, t, qd);
     } else {
       if (c < last) finish(c + 1);
       if constexpr (kFull) {
@@ -448,7 +461,7 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
         // the reversal of chunk 0 reads them)
         pre = fetch(c >= 2 ? c - 2 : 0, c - 1);
         load_s0(c, S0row);
-        setup_decays(Pn, decay_load(L.dec, wq, t, qd), wq, t, qd);
+        setup_decays(Pn, decay_load(L.dec, wave, t, qd), wave, t, qd);
       }
     }
     lds_barrier();
