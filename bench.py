@@ -18,7 +18,10 @@ matrix-core ones, which form the fp32 products from split bf16 MFMAs), and
 the CPU baseline (the oracle's reference-order fp32 restatement,
 OpenMP over (batch, head) pairs, timed on a bounded sample of the same
 workload on the host cores). config cfg3 is the batched decode step (T=1),
-which is HBM-bound.
+which is HBM-bound. config cfg4 is a whole RWKV-7 0.1B training step (12
+cells, C=768, vocab 65536, B=16, T=512) with the WKV7 operator on the HIP
+kernels and every other op in PyTorch; it reports the step time and the
+WKV7 share.
 """
 
 from __future__ import annotations
@@ -50,6 +53,7 @@ CONFIGS = {
     "cfg1": dict(B=8, T=4096, H=32, io="bf16", s0_std=0.1),
     "cfg2": dict(B=4, T=4096, H=64, io="bf16", s0_std=None),
     "cfg3": dict(B=256, T=1, H=40, io="bf16", s0_std=0.1),
+    "cfg4": dict(B=16, T=512, H=12, io="bf16", vocab=65536, cells=12),
 }
 
 
@@ -330,6 +334,58 @@ def bench_decode(cfg, steps, warmup, probe=False):
     }
 
 
+def bench_lm(cfg, steps, warmup):
+    """config[4]: one RWKV-7 0.1B training step (forward, loss, backward, Adam
+    update) on the host framework with the WKV7 operator on the HIP kernels;
+    reports the step time and the share of it spent in the WKV7 launches,
+    from timing events recorded around each launch on the launch stream."""
+    import torch
+    model_mod = importlib.import_module("rwkv-rs_amd.model")
+    wkv7 = importlib.import_module("rwkv-rs_amd.wkv7")
+    B, T, H = cfg["B"], cfg["T"], cfg["H"]
+    C, V, L = H * N_HEAD, cfg["vocab"], cfg["cells"]
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(0x5EED0004)
+    model = model_mod.AutoRegressiveModel(V, L, C, H, N_HEAD).to(dev).init_random(0.02, gen)
+    opt = model_mod.make_optimizer(model)
+    tokens = torch.randint(0, V, (B, T + 1), device=dev, generator=gen)
+    inputs, targets = tokens[:, :-1].contiguous(), tokens[:, 1:].contiguous()
+    for _ in range(warmup):
+        loss = model_mod.train_step(model, opt, inputs, targets)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    log = []
+    t0 = time.perf_counter()
+    e0.record(stream)
+    with wkv7.kernel_events(log):
+        for _ in range(steps):
+            loss = model_mod.train_step(model, opt, inputs, targets)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    step_ms = e0.elapsed_time(e1) / steps
+    fwd_ms = sum(a.elapsed_time(b) for n, a, b in log if n == "forward") / steps
+    bwd_ms = sum(a.elapsed_time(b) for n, a, b in log if n == "backward") / steps
+    ms_per_step = wall * 1e3 / steps
+    return {
+        "metric": "RWKV-7 0.1B train step tokens/s (B=16, T=512) + WKV7 share",
+        "value": B * T / (ms_per_step * 1e-3), "unit": "tokens/s", "n_gpus": 1,
+        "steps": steps, "warmup": warmup, "ms_per_step": ms_per_step,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "rwkv7_0.1b_train_step", "batch": B, "context_len": T,
+                   "num_cells": L, "embedded_dim": C, "num_heads": H, "head_size": N_HEAD,
+                   "vocab": V, "wkv7_io_dtype": "bf16", "matmul": "bf16 autocast",
+                   "optimizer": "AdamW(0.9, 0.99, eps 1e-16)"},
+        "gpu_step_ms": step_ms,
+        "wkv7_fwd_ms_per_step": fwd_ms, "wkv7_bwd_ms_per_step": bwd_ms,
+        "wkv7_share": (fwd_ms + bwd_ms) / step_ms,
+        "wkv7_launches_per_step": len(log) / steps,
+        "final_loss": float(loss),
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -351,7 +407,9 @@ def main():
               file=sys.stderr)
         sys.exit(2)
     cfg = CONFIGS[args.config]
-    if args.config == "cfg3":
+    if args.config == "cfg4":
+        out = bench_lm(cfg, args.steps, args.warmup)
+    elif args.config == "cfg3":
         out = bench_decode(cfg, args.steps, args.warmup, probe=args.copy_probe)
     else:
         out = bench_train(cfg, args.steps, args.warmup,

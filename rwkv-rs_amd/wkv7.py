@@ -25,8 +25,9 @@ outputs are allocated here like its ``empty_device`` (wkv7_common/host.rs:114-13
 
 from __future__ import annotations
 
+import contextlib
 from dataclasses import dataclass
-from typing import Optional
+from typing import List, Optional, Tuple
 
 import torch
 
@@ -141,6 +142,40 @@ def _state(t: Optional[torch.Tensor], shape, device) -> Optional[torch.Tensor]:
     return t.to(device=device, dtype=torch.float32).contiguous()
 
 
+# --------------------------------------------------------------- kernel timing
+_event_log: Optional[List[Tuple[str, "torch.cuda.Event", "torch.cuda.Event"]]] = None
+
+
+@contextlib.contextmanager
+def kernel_events(log: list):
+    """Record a (name, start, end) pair of timing events on the launch stream
+    around every forward and backward call into the library while the block
+    runs; ``name`` is "forward" or "backward". The caller synchronises and
+    reads ``start.elapsed_time(end)``. Used to report the operator's share of
+    a model step."""
+    global _event_log
+    prev, _event_log = _event_log, log
+    try:
+        yield log
+    finally:
+        _event_log = prev
+
+
+def _mark(name: str, device: torch.device):
+    if _event_log is None:
+        return None
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(torch.cuda.current_stream(device))
+    _event_log.append((name, start, end))
+    return end
+
+
+def _close(end, device: torch.device) -> None:
+    if end is not None:
+        end.record(torch.cuda.current_stream(device))
+
+
 def _check_chunk(T: int, chunk_len: int) -> None:
     # wkv7_common/host.rs:109-112 (the reference panics with this message)
     if chunk_len <= 0 or T % chunk_len != 0:
@@ -159,10 +194,12 @@ def _forward(w, r, k, v, a, b, initial_state, chunk_len, use_initial_state, retu
     output = torch.empty_like(w)
     final_state = (torch.empty((B, H, N, N), dtype=torch.float32, device=dev)
                    if return_final_state else None)
+    end = _mark("forward", dev)
     _native.call("wkv7_forward", _ptr(w), _ptr(r), _ptr(k), _ptr(v), _ptr(a), _ptr(b), _ptr(s0),
                  B, T, H, N, chunk_len, _dtype_code(w), int(use_initial_state),
                  int(return_final_state), _ptr(state), _ptr(removal_state), _ptr(output),
                  _ptr(final_state), _stream(dev))
+    _close(end, dev)
     return state, removal_state, output, final_state
 
 
@@ -178,11 +215,13 @@ def _backward(w, r, k, v, a, b, state, removal_state, output_grad, final_state_g
     grads = [torch.empty_like(w) for _ in range(6)]
     ds0 = (torch.empty((B, H, N, N), dtype=torch.float32, device=dev)
            if write_initial_state_grad else None)
+    end = _mark("backward", dev)
     _native.call("wkv7_backward", _ptr(w), _ptr(r), _ptr(k), _ptr(v), _ptr(a), _ptr(b),
                  _ptr(state), _ptr(removal_state), _ptr(output_grad), _ptr(dsT),
                  B, T, H, N, chunk_len, _dtype_code(w), int(use_final_state_grad),
                  int(write_initial_state_grad), *(_ptr(g) for g in grads), _ptr(ds0),
                  _stream(dev))
+    _close(end, dev)
     return grads, ds0
 
 
