@@ -334,7 +334,7 @@ def bench_decode(cfg, steps, warmup, probe=False):
     }
 
 
-def bench_lm(cfg, steps, warmup):
+def bench_lm(cfg, steps, warmup, neighbor_ops="hip"):
     """config[4]: one RWKV-7 0.1B training step (forward, loss, backward, Adam
     update) on the host framework with the WKV7 operator on the HIP kernels;
     reports the step time and the share of it spent in the WKV7 launches,
@@ -346,7 +346,8 @@ def bench_lm(cfg, steps, warmup):
     C, V, L = H * N_HEAD, cfg["vocab"], cfg["cells"]
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev).manual_seed(0x5EED0004)
-    model = model_mod.AutoRegressiveModel(V, L, C, H, N_HEAD).to(dev).init_random(0.02, gen)
+    model = model_mod.AutoRegressiveModel(V, L, C, H, N_HEAD, neighbor_ops=neighbor_ops)
+    model = model.to(dev).init_random(0.02, gen)
     opt = model_mod.make_optimizer(model)
     tokens = torch.randint(0, V, (B, T + 1), device=dev, generator=gen)
     inputs, targets = tokens[:, :-1].contiguous(), tokens[:, 1:].contiguous()
@@ -377,6 +378,7 @@ def bench_lm(cfg, steps, warmup):
         "config": {"workload": "rwkv7_0.1b_train_step", "batch": B, "context_len": T,
                    "num_cells": L, "embedded_dim": C, "num_heads": H, "head_size": N_HEAD,
                    "vocab": V, "wkv7_io_dtype": "bf16", "matmul": "bf16 autocast",
+                   "neighbor_ops": neighbor_ops,
                    "optimizer": "AdamW(0.9, 0.99, eps 1e-16)"},
         "gpu_step_ms": step_ms,
         "wkv7_fwd_ms_per_step": fwd_ms, "wkv7_bwd_ms_per_step": bwd_ms,
@@ -393,6 +395,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="cfg1", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--neighbor-ops", default="hip", choices=("hip", "torch"),
+                    help="cfg4: the ops beside the operator as fused kernels or torch ops")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also launch one plain copy of known size (counter calibration)")
     ap.add_argument("--pmc-summary", nargs="+", metavar="DIR",
@@ -408,7 +412,7 @@ def main():
         sys.exit(2)
     cfg = CONFIGS[args.config]
     if args.config == "cfg4":
-        out = bench_lm(cfg, args.steps, args.warmup)
+        out = bench_lm(cfg, args.steps, args.warmup, args.neighbor_ops)
     elif args.config == "cfg3":
         out = bench_decode(cfg, args.steps, args.warmup, probe=args.copy_probe)
     else:

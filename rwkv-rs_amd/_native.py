@@ -1,4 +1,5 @@
-"""ctypes binding of libwkv7_hip.so, the C ABI declared in include/wkv7.h.
+"""ctypes binding of libwkv7_hip.so, the C ABI declared in include/wkv7.h and
+include/rwkv_neighbors.h.
 
 The library is built in-tree by rwkv-rs_amd/build.py. Loading fails loudly when
 it is missing: there is no fallback implementation.
@@ -31,6 +32,9 @@ EXPORTS = (
     "wkv7_statepass_forward", "wkv7_statepass_backward",
     "wkv7_statetune_forward", "wkv7_statetune_backward",
     "wkv7_infer_forward",
+    "rwkv_token_shift_mix_workspace_bytes", "rwkv_token_shift_mix_forward",
+    "rwkv_token_shift_mix_backward", "rwkv_gated_readout_workspace_bytes",
+    "rwkv_gated_readout_forward", "rwkv_gated_readout_backward",
 )
 
 _P = ctypes.c_void_p
@@ -51,6 +55,15 @@ _SIGNATURES = {
     "wkv7_statetune_forward": ([_P] * 7 + [_I64] * 5 + [_INT] + [_P] * 4, _INT),
     "wkv7_statetune_backward": ([_P] * 9 + [_I64] * 5 + [_INT] + [_P] * 8, _INT),
     "wkv7_infer_forward": ([_P] * 10 + [_I64] * 5 + [_INT] * 2 + [_P] * 2, _INT),
+    "rwkv_token_shift_mix_workspace_bytes": ([_I64] * 4, _I64),
+    "rwkv_token_shift_mix_forward": ([_P] * 5 + [_I64] * 5 + [_INT] * 2 + [_P] * 4, _INT),
+    "rwkv_token_shift_mix_backward": ([_P] * 5 + [_I64] * 5 + [_INT] * 2 + [_P] * 6 + [_I64, _P],
+                                      _INT),
+    "rwkv_gated_readout_workspace_bytes": ([_I64] * 3, _I64),
+    "rwkv_gated_readout_forward": ([_P] * 8 + [ctypes.c_float] + [_I64] * 3 + [_INT] * 2
+                                   + [_P] * 2, _INT),
+    "rwkv_gated_readout_backward": ([_P] * 8 + [ctypes.c_float] + [_I64] * 3 + [_INT] * 2
+                                    + [_P] * 10 + [_I64, _P], _INT),
 }
 
 _lib = None

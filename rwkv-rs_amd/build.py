@@ -1,4 +1,5 @@
-"""Build libwkv7_hip.so (the gfx950 kernels and their C ABI) in-tree.
+"""Build libwkv7_hip.so (the gfx950 kernels and their C ABI: include/wkv7.h
+and include/rwkv_neighbors.h) in-tree.
 
     python rwkv-rs_amd/build.py          # or __graft_entry__.build()
 
@@ -19,7 +20,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libwkv7_hip.so")
 SOURCES = ["wkv7_api.cpp", "wkv7_forward.hip", "wkv7_backward.hip", "wkv7_infer.hip",
-           "wkv7_chunk_forward.hip", "wkv7_chunk_backward.hip"]
+           "wkv7_chunk_forward.hip", "wkv7_chunk_backward.hip",
+           "neighbors_api.cpp", "neighbors.hip"]
 ARCH = "gfx950"
 
 

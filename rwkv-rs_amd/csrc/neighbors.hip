@@ -1,0 +1,611 @@
+// Kernels beside the WKV7 operator in a time mixer, fused per side.
+//
+// Before the operator -- the token shift and its channel mixes
+// (token_shift_diff/kernel.rs:17-64 followed by addcmul5 / addcmul,
+// addcmul/kernel.rs:4-53, as WeightPrepare::forward and ChannelMixer::forward
+// call them, weight_prepare.rs:221-268, channel_mixer/mod.rs:96-106):
+//   prev_t = x_{t-1} if step t-1 is valid, else the external shift (t = 0 too)
+//   diff_t = prev_t - x_t (0 at a masked step)
+//   mix_i  = x_t + diff_t * scale_i[channel]            for i < num_mixes
+// and its backward (token_shift_diff/backward.rs:44-101, addcmul/backward.rs:
+// 34-58): with dd_t = sum_i g_i scale_i + g_diff and masked mdd_t = m_t dd_t,
+//   dx_t     = sum_i g_i - mdd_t + m_t mdd_{t+1}          (t + 1 < T)
+//   dshift_b = sum_t m_t (1 - m_{t-1}) mdd_t               (m_{-1} = 0)
+//   dscale_i = sum_{b,t} g_i diff_t
+// The difference stays in fp32 between the shift and the mixes.
+//
+// After the operator -- the gated readout (gated_readout.rs:110-148):
+//   out = (GroupNorm_h(y) + (sum_n r k bonus_h) v) * gate
+// with one group per head (64 channels, biased variance, eps), and its
+// backward, which recomputes the row statistics instead of storing them.
+//
+// All of these move a few bytes per flop: they are HBM-bound element-wise
+// passes. Each thread owns 4 consecutive channels (one 8- or 16-byte access
+// per tensor and row) and walks a short run of rows; the column sums of the
+// backward (scale, weight, bias and bonus gradients) are reduced within a
+// block, written as one partial per block to a workspace and summed in a
+// fixed order by a second kernel, so results do not depend on scheduling.
+#include <type_traits>
+
+#include "neighbors_launch.hpp"
+
+namespace rwkv_nb {
+namespace {
+
+struct F4 {
+  float v[4];
+};
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __builtin_bit_cast(float, static_cast<uint32_t>(b) << 16);
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+}
+
+template <bool BF>
+__device__ __forceinline__ F4 load4(const void* base, int64_t i) {
+  F4 o;
+  if constexpr (BF) {
+    const uint2 raw = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + i);
+    o.v[0] = bf16_to_f32(raw.x & 0xffffu);
+    o.v[1] = bf16_to_f32(raw.x >> 16);
+    o.v[2] = bf16_to_f32(raw.y & 0xffffu);
+    o.v[3] = bf16_to_f32(raw.y >> 16);
+  } else {
+    const float4 f = *reinterpret_cast<const float4*>(static_cast<const float*>(base) + i);
+    o.v[0] = f.x;
+    o.v[1] = f.y;
+    o.v[2] = f.z;
+    o.v[3] = f.w;
+  }
+  return o;
+}
+
+template <bool BF>
+__device__ __forceinline__ void store4(void* base, int64_t i, const F4& x) {
+  if constexpr (BF) {
+    uint2 raw;
+    raw.x = f32_to_bf16(x.v[0]) | (static_cast<uint32_t>(f32_to_bf16(x.v[1])) << 16);
+    raw.y = f32_to_bf16(x.v[2]) | (static_cast<uint32_t>(f32_to_bf16(x.v[3])) << 16);
+    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(base) + i) = raw;
+  } else {
+    *reinterpret_cast<float4*>(static_cast<float*>(base) + i) =
+        make_float4(x.v[0], x.v[1], x.v[2], x.v[3]);
+  }
+}
+
+template <bool BF>
+__device__ __forceinline__ float load1(const void* base, int64_t i) {
+  if constexpr (BF)
+    return bf16_to_f32(static_cast<const uint16_t*>(base)[i]);
+  else
+    return static_cast<const float*>(base)[i];
+}
+
+__device__ __forceinline__ F4 zero4() { return F4{{0.f, 0.f, 0.f, 0.f}}; }
+
+// sum over the 16 lanes of a row group
+__device__ __forceinline__ float sum16(float x) {
+  x += __shfl_xor(x, 8);
+  x += __shfl_xor(x, 4);
+  x += __shfl_xor(x, 2);
+  x += __shfl_xor(x, 1);
+  return x;
+}
+
+// ------------------------------------------------------------ token shift mix
+// slot of row b in the full-batch shift buffers; -1 when a batch id is out
+// of range (such a row reads a zero shift and writes no shift or gradient)
+__device__ __forceinline__ int64_t slot_of(const ShiftMixArgs& a, int64_t b) {
+  const int64_t slot = a.batch_ids ? a.batch_ids[b] : b;
+  return (slot >= 0 && slot < a.full_batch) ? slot : -1;
+}
+
+template <bool XB>
+__device__ __forceinline__ F4 external_shift(const ShiftMixArgs& a, int64_t b, int64_t c) {
+  if (!a.shift) return zero4();
+  const int64_t slot = slot_of(a, b);
+  return slot >= 0 ? load4<XB>(a.shift, slot * a.C + c) : zero4();
+}
+
+template <bool XB>
+__device__ __forceinline__ bool valid(const ShiftMixArgs& a, int64_t r) {
+  return !a.mask || load1<XB>(a.mask, r) != 0.f;
+}
+
+// KM: the largest mix count an instantiation serves (1, 6 or 8), so that
+// its per-thread arrays hold only as many mixes as the call can have
+template <bool XB, bool OB, int KM>
+__global__ __launch_bounds__(256) void shift_mix_forward_kernel(ShiftMixArgs a) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t C = a.C;
+  const int64_t c = (static_cast<int64_t>(blockIdx.y) * 64 + lane) * 4;
+  const int64_t rows = a.batch * a.T;
+  const int64_t r0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * kMixRowsPerWave;
+  const int64_t r1 = r0 + kMixRowsPerWave < rows ? r0 + kMixRowsPerWave : rows;
+  if (c >= C || r0 >= r1) return;
+  F4 mu[KM];
+#pragma unroll
+  for (int i = 0; i < KM; ++i)
+    mu[i] = i < a.num_mixes ? load4<false>(a.scales, i * C + c) : zero4();
+  int64_t b = r0 / a.T, t = r0 - b * a.T;
+  F4 xprev = zero4();
+  bool have_prev = false;
+  for (int64_t r = r0; r < r1; ++r) {
+    const F4 xt = load4<XB>(a.x, r * C + c);
+    const bool cur_valid = valid<XB>(a, r);
+    F4 prev;
+    if (t > 0 && valid<XB>(a, r - 1))
+      prev = have_prev ? xprev : load4<XB>(a.x, (r - 1) * C + c);
+    else
+      prev = external_shift<XB>(a, b, c);
+    F4 d;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) d.v[j] = cur_valid ? prev.v[j] - xt.v[j] : 0.f;
+#pragma unroll
+    for (int i = 0; i < KM; ++i) {
+      if (i < a.num_mixes) {
+        F4 o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o.v[j] = xt.v[j] + d.v[j] * mu[i].v[j];
+        store4<OB>(a.mixes[i], r * C + c, o);
+      }
+    }
+    if (a.diff) store4<OB>(a.diff, r * C + c, d);
+    xprev = xt;
+    have_prev = true;
+    if (++t == a.T) {
+      t = 0;
+      ++b;
+      have_prev = false;
+    }
+  }
+}
+
+// next_shift[slot(b)] = x at the last valid step of row b, else the external
+// shift; a separate launch, so next_shift may be the shift buffer itself
+template <bool XB>
+__global__ __launch_bounds__(256) void shift_next_kernel(ShiftMixArgs a) {
+  const int64_t c = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
+  const int64_t b = blockIdx.y;
+  if (c >= a.C) return;
+  int64_t t = a.T - 1;
+  if (a.mask)
+    while (t >= 0 && load1<XB>(a.mask, b * a.T + t) == 0.f) --t;
+  const F4 val = t >= 0 ? load4<XB>(a.x, (b * a.T + t) * a.C + c) : external_shift<XB>(a, b, c);
+  const int64_t slot = slot_of(a, b);
+  if (slot >= 0) store4<XB>(a.next_shift, slot * a.C + c, val);
+}
+
+// dd = sum_i g_i scale_i + g_diff at row r
+template <bool OB, int KM>
+__device__ __forceinline__ F4 diff_grad_at(const ShiftMixArgs& a, const F4 (&mu)[KM],
+                                           int64_t r, int64_t c) {
+  F4 dd = a.diff_grad ? load4<OB>(a.diff_grad, r * a.C + c) : zero4();
+#pragma unroll
+  for (int i = 0; i < KM; ++i) {
+    if (i < a.num_mixes) {
+      const F4 g = load4<OB>(a.mix_grads[i], r * a.C + c);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) dd.v[j] += g.v[j] * mu[i].v[j];
+    }
+  }
+  return dd;
+}
+
+template <bool XB, bool OB, int KM>
+__global__ __launch_bounds__(256) void shift_mix_backward_kernel(ShiftMixArgs a) {
+  __shared__ float red[4][KM][kMixColsPerBlock];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t C = a.C;
+  const int64_t c = (static_cast<int64_t>(blockIdx.y) * 64 + lane) * 4;
+  const int64_t rows = a.batch * a.T;
+  const int64_t r0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * kMixRowsPerWave;
+  const int64_t r1 = r0 + kMixRowsPerWave < rows ? r0 + kMixRowsPerWave : rows;
+  const bool active = c < C;
+  F4 mu[KM], acc[KM];
+#pragma unroll
+  for (int i = 0; i < KM; ++i) {
+    mu[i] = (active && i < a.num_mixes) ? load4<false>(a.scales, i * C + c) : zero4();
+    acc[i] = zero4();
+  }
+  if (active && r0 < r1) {
+    const int64_t rl = r1 - 1;
+    int64_t b = rl / a.T, t = rl - b * a.T;
+    // masked diff gradient of the step after the run, when it is in the same sequence
+    F4 mdd_next = zero4();
+    if (t + 1 < a.T) {
+      const float m = a.mask ? load1<XB>(a.mask, r1) : 1.f;
+      const F4 dd = diff_grad_at<OB, KM>(a, mu, r1, c);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) mdd_next.v[j] = m * dd.v[j];
+    }
+    F4 xt = load4<XB>(a.x, rl * C + c);
+    for (int64_t r = rl; r >= r0; --r) {
+      const float m = a.mask ? load1<XB>(a.mask, r) : 1.f;
+      // the forward's difference at this step, for the scale gradients
+      const F4 xp = t > 0 ? load4<XB>(a.x, (r - 1) * C + c) : zero4();
+      const F4 prev = (t > 0 && valid<XB>(a, r - 1)) ? xp : external_shift<XB>(a, b, c);
+      F4 d;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) d.v[j] = m != 0.f ? prev.v[j] - xt.v[j] : 0.f;
+      // each mix gradient is read once and folded into dd, their sum and
+      // the scale gradients
+      F4 dd = a.diff_grad ? load4<OB>(a.diff_grad, r * C + c) : zero4();
+      F4 gs = zero4();
+#pragma unroll
+      for (int i = 0; i < KM; ++i) {
+        if (i < a.num_mixes) {
+          const F4 g = load4<OB>(a.mix_grads[i], r * C + c);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            dd.v[j] += g.v[j] * mu[i].v[j];
+            gs.v[j] += g.v[j];
+            acc[i].v[j] += g.v[j] * d.v[j];
+          }
+        }
+      }
+      const bool has_next = t + 1 < a.T;
+      F4 mdd, dx;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        mdd.v[j] = m * dd.v[j];
+        dx.v[j] = gs.v[j] - mdd.v[j] + (has_next ? m * mdd_next.v[j] : 0.f);
+      }
+      store4<XB>(a.x_grad, r * C + c, dx);
+      mdd_next = mdd;
+      if (t > 0) {
+        xt = xp;
+        --t;
+      } else {
+        t = a.T - 1;
+        --b;
+        if (r - 1 >= r0) xt = load4<XB>(a.x, (r - 1) * C + c);
+      }
+    }
+  }
+  // block partial of the scale gradients: the four waves hold the same channels
+#pragma unroll
+  for (int i = 0; i < KM; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) red[wave][i][lane * 4 + j] = acc[i].v[j];
+  __syncthreads();
+  if (wave == 0 && active) {
+#pragma unroll
+    for (int i = 0; i < KM; ++i) {
+      if (i < a.num_mixes) {
+        F4 s;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          s.v[j] = red[0][i][lane * 4 + j] + red[1][i][lane * 4 + j] +
+                   red[2][i][lane * 4 + j] + red[3][i][lane * 4 + j];
+        store4<false>(a.workspace, (static_cast<int64_t>(blockIdx.x) * a.num_mixes + i) * C + c, s);
+      }
+    }
+  }
+}
+
+// the external shift's gradient: the masked diff gradient at every valid step
+// whose previous step is not valid (t = 0 included); rows of the full batch
+// that no batch id names are zero (filled before)
+template <bool XB, bool OB, int KM>
+__global__ __launch_bounds__(256) void shift_grad_kernel(ShiftMixArgs a) {
+  const int64_t c = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
+  const int64_t b = blockIdx.y;
+  if (c >= a.C) return;
+  F4 mu[KM];
+#pragma unroll
+  for (int i = 0; i < KM; ++i)
+    mu[i] = i < a.num_mixes ? load4<false>(a.scales, i * a.C + c) : zero4();
+  F4 acc = zero4();
+  for (int64_t t = 0; t < a.T; ++t) {
+    const int64_t r = b * a.T + t;
+    const float m = a.mask ? load1<XB>(a.mask, r) : 1.f;
+    const bool start = m != 0.f && (t == 0 || !valid<XB>(a, r - 1));
+    if (start) {
+      const F4 dd = diff_grad_at<OB, KM>(a, mu, r, c);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc.v[j] += m * m * dd.v[j];
+    }
+    if (!a.mask) break;  // without a mask only t = 0 starts a run
+  }
+  const int64_t slot = slot_of(a, b);
+  if (slot >= 0) store4<false>(a.shift_grad, slot * a.C + c, acc);
+}
+
+__global__ __launch_bounds__(256) void fill_zero_kernel(float* p, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0.f;
+}
+
+// out_q[c] = sum over row blocks of ws[rb][q][c]: 16 waves split the row
+// blocks (wave w takes w, w + 16, ...), each sums its share in order, then
+// the 16 partial sums are added in wave order, so the result is the same on
+// every run
+constexpr int kSumWaves = 16;
+
+struct ColumnSumArgs {
+  const float* ws;
+  int64_t row_blocks, Q, C;
+  float* out[kMaxMixes];
+};
+
+__global__ __launch_bounds__(64 * kSumWaves) void column_sum_kernel(ColumnSumArgs a) {
+  __shared__ float red[kSumWaves][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * 64 + lane;
+  const int q = blockIdx.y;
+  float s = 0.f;
+  if (c < a.C)
+    for (int64_t rb = wave; rb < a.row_blocks; rb += kSumWaves)
+      s += a.ws[(rb * a.Q + q) * a.C + c];
+  red[wave][lane] = s;
+  __syncthreads();
+  if (wave == 0 && c < a.C) {
+    float tot = 0.f;
+#pragma unroll
+    for (int w = 0; w < kSumWaves; ++w) tot += red[w][lane];
+#pragma unroll
+    for (int i = 0; i < kMaxMixes; ++i)
+      if (i == q) a.out[i][c] = tot;
+  }
+}
+
+// -------------------------------------------------------------- gated readout
+template <bool OPB>
+__device__ __forceinline__ void readout_row(const ReadoutArgs& a, int64_t idx, const F4& rk,
+                                            F4& y, F4& r, F4& k, F4& v, float& rstd, F4& yh,
+                                            float& s) {
+  y = load4<OPB>(a.y, idx);
+  r = load4<OPB>(a.r, idx);
+  k = load4<OPB>(a.k, idx);
+  v = load4<OPB>(a.v, idx);
+  const float mean = sum16(y.v[0] + y.v[1] + y.v[2] + y.v[3]) * (1.f / 64.f);
+  float d2 = 0.f, bon = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    yh.v[j] = y.v[j] - mean;
+    d2 += yh.v[j] * yh.v[j];
+    bon += r.v[j] * k.v[j] * rk.v[j];
+  }
+  rstd = rsqrtf(sum16(d2) * (1.f / 64.f) + a.eps);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) yh.v[j] *= rstd;
+  s = sum16(bon);
+}
+
+template <bool OPB, bool ACTB>
+__global__ __launch_bounds__(256) void readout_forward_kernel(ReadoutArgs a) {
+  const int grp = threadIdx.x >> 4, l = threadIdx.x & 15;
+  const int64_t C = a.H * 64;
+  const int64_t cc = static_cast<int64_t>(blockIdx.y) * 64 + l * 4;
+  const F4 gw = load4<false>(a.weight, cc), gb = load4<false>(a.bias, cc);
+  const F4 rk = load4<false>(a.bonus, cc);
+  const int64_t r0 = (static_cast<int64_t>(blockIdx.x) * 16 + grp) * kReadoutRowsPerGroup;
+  for (int i = 0; i < kReadoutRowsPerGroup; ++i) {
+    const int64_t row = r0 + i;
+    if (row >= a.rows) break;  // uniform over the 16 lanes of the group
+    const int64_t idx = row * C + cc;
+    F4 y, r, k, v, yh;
+    float rstd, s;
+    readout_row<OPB>(a, idx, rk, y, r, k, v, rstd, yh, s);
+    const F4 g = load4<ACTB>(a.gate, idx);
+    F4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o.v[j] = (yh.v[j] * gw.v[j] + gb.v[j] + s * v.v[j]) * g.v[j];
+    store4<ACTB>(a.out, idx, o);
+  }
+}
+
+template <bool OPB, bool ACTB>
+__global__ __launch_bounds__(256) void readout_backward_kernel(ReadoutArgs a) {
+  __shared__ float red[16][kReadoutSums][64];
+  const int grp = threadIdx.x >> 4, l = threadIdx.x & 15;
+  const int64_t C = a.H * 64;
+  const int64_t cc = static_cast<int64_t>(blockIdx.y) * 64 + l * 4;
+  const F4 gw = load4<false>(a.weight, cc), gb = load4<false>(a.bias, cc);
+  const F4 rk = load4<false>(a.bonus, cc);
+  F4 aw = zero4(), ab = zero4(), ak = zero4();
+  const int64_t r0 = (static_cast<int64_t>(blockIdx.x) * 16 + grp) * kReadoutRowsPerGroup;
+  for (int i = 0; i < kReadoutRowsPerGroup; ++i) {
+    const int64_t row = r0 + i;
+    if (row >= a.rows) break;  // uniform over the 16 lanes of the group
+    const int64_t idx = row * C + cc;
+    F4 y, r, k, v, yh;
+    float rstd, s;
+    readout_row<OPB>(a, idx, rk, y, r, k, v, rstd, yh, s);
+    const F4 g = load4<ACTB>(a.gate, idx);
+    const F4 dout = load4<ACTB>(a.out_grad, idx);
+    F4 dz, dg, dv, dyh;
+    float ds = 0.f, m1 = 0.f, m2 = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float z = yh.v[j] * gw.v[j] + gb.v[j] + s * v.v[j];
+      dz.v[j] = dout.v[j] * g.v[j];
+      dg.v[j] = dout.v[j] * z;
+      aw.v[j] += dz.v[j] * yh.v[j];
+      ab.v[j] += dz.v[j];
+      dv.v[j] = dz.v[j] * s;
+      ds += dz.v[j] * v.v[j];
+      dyh.v[j] = dz.v[j] * gw.v[j];
+      m1 += dyh.v[j];
+      m2 += dyh.v[j] * yh.v[j];
+    }
+    ds = sum16(ds);
+    m1 = sum16(m1) * (1.f / 64.f);
+    m2 = sum16(m2) * (1.f / 64.f);
+    F4 dr, dk, dy;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      dr.v[j] = ds * k.v[j] * rk.v[j];
+      dk.v[j] = ds * r.v[j] * rk.v[j];
+      ak.v[j] += ds * r.v[j] * k.v[j];
+      dy.v[j] = rstd * (dyh.v[j] - m1 - yh.v[j] * m2);
+    }
+    store4<ACTB>(a.gate_grad, idx, dg);
+    store4<OPB>(a.v_grad, idx, dv);
+    store4<OPB>(a.r_grad, idx, dr);
+    store4<OPB>(a.k_grad, idx, dk);
+    store4<OPB>(a.y_grad, idx, dy);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    red[grp][0][l * 4 + j] = aw.v[j];
+    red[grp][1][l * 4 + j] = ab.v[j];
+    red[grp][2][l * 4 + j] = ak.v[j];
+  }
+  __syncthreads();
+  if (threadIdx.x < kReadoutSums * 64) {
+    const int q = threadIdx.x >> 6, n = threadIdx.x & 63;
+    float s = 0.f;
+    for (int g = 0; g < 16; ++g) s += red[g][q][n];
+    a.workspace[(static_cast<int64_t>(blockIdx.x) * kReadoutSums + q) * C +
+                static_cast<int64_t>(blockIdx.y) * 64 + n] = s;
+  }
+}
+
+template <typename K>
+hipError_t launch(K kernel, dim3 grid, dim3 block, hipStream_t s) {
+  hipLaunchKernelGGL(kernel, grid, block, 0, s);
+  return hipGetLastError();
+}
+
+template <typename K, typename A>
+hipError_t launch(K kernel, dim3 grid, dim3 block, hipStream_t s, const A& args) {
+  hipLaunchKernelGGL(kernel, grid, block, 0, s, args);
+  return hipGetLastError();
+}
+
+hipError_t column_sum(const float* ws, int64_t row_blocks, int64_t Q, int64_t C,
+                      float* const* outs, hipStream_t s) {
+  ColumnSumArgs c{};
+  c.ws = ws;
+  c.row_blocks = row_blocks;
+  c.Q = Q;
+  c.C = C;
+  for (int i = 0; i < Q; ++i) c.out[i] = outs[i];
+  const dim3 grid(static_cast<unsigned>((C + 63) / 64), static_cast<unsigned>(Q));
+  return launch(column_sum_kernel, grid, dim3(64 * kSumWaves), s, c);
+}
+
+hipError_t fill_zero(float* p, int64_t n, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(fill_zero_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256),
+                     0, s, p, n);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+namespace {
+
+// one instantiation per (x dtype, output dtype, mix-count class)
+template <template <bool, bool, int> class Kern>
+hipError_t dispatch(const ShiftMixArgs& a, dim3 grid, dim3 block, hipStream_t s) {
+  const int km = a.num_mixes <= 1 ? 1 : a.num_mixes <= 6 ? 6 : 8;
+  auto go = [&](auto xb, auto ob) -> hipError_t {
+    constexpr bool XB = decltype(xb)::value, OB = decltype(ob)::value;
+    if (km == 1) return launch(Kern<XB, OB, 1>::fn, grid, block, s, a);
+    if (km == 6) return launch(Kern<XB, OB, 6>::fn, grid, block, s, a);
+    return launch(Kern<XB, OB, 8>::fn, grid, block, s, a);
+  };
+  using T = std::true_type;
+  using F = std::false_type;
+  if (a.x_bf16) return a.out_bf16 ? go(T{}, T{}) : go(T{}, F{});
+  return a.out_bf16 ? go(F{}, T{}) : go(F{}, F{});
+}
+
+template <bool XB, bool OB, int KM>
+struct MixForward {
+  static constexpr auto fn = shift_mix_forward_kernel<XB, OB, KM>;
+};
+template <bool XB, bool OB, int KM>
+struct MixBackward {
+  static constexpr auto fn = shift_mix_backward_kernel<XB, OB, KM>;
+};
+template <bool XB, bool OB, int KM>
+struct ShiftGrad {
+  static constexpr auto fn = shift_grad_kernel<XB, OB, KM>;
+};
+
+}  // namespace
+
+hipError_t launch_shift_mix_forward(const ShiftMixArgs& a, hipStream_t s) {
+  const int64_t rows = a.batch * a.T;
+  const unsigned gx = static_cast<unsigned>((a.C + kMixColsPerBlock - 1) / kMixColsPerBlock);
+  if (rows > 0) {
+    const dim3 grid(static_cast<unsigned>(mix_row_blocks(rows)), gx);
+    const hipError_t e = dispatch<MixForward>(a, grid, dim3(256), s);
+    if (e != hipSuccess) return e;
+  }
+  if (a.next_shift && a.batch > 0) {
+    const dim3 grid(gx, static_cast<unsigned>(a.batch));
+    return a.x_bf16 ? launch(shift_next_kernel<true>, grid, dim3(64), s, a)
+                    : launch(shift_next_kernel<false>, grid, dim3(64), s, a);
+  }
+  return hipSuccess;
+}
+
+hipError_t launch_shift_mix_backward(const ShiftMixArgs& a, hipStream_t s) {
+  const int64_t rows = a.batch * a.T;
+  const unsigned gx = static_cast<unsigned>((a.C + kMixColsPerBlock - 1) / kMixColsPerBlock);
+  hipError_t e = hipSuccess;
+  if (rows > 0) {
+    const int64_t rb = mix_row_blocks(rows);
+    e = dispatch<MixBackward>(a, dim3(static_cast<unsigned>(rb), gx), dim3(256), s);
+    if (e != hipSuccess) return e;
+    if (a.num_mixes > 0) {
+      float* outs[kMaxMixes];
+      for (int i = 0; i < a.num_mixes; ++i) outs[i] = a.scales_grad + i * a.C;
+      e = column_sum(a.workspace, rb, a.num_mixes, a.C, outs, s);
+      if (e != hipSuccess) return e;
+    }
+  } else if (a.num_mixes > 0) {
+    e = fill_zero(a.scales_grad, a.num_mixes * a.C, s);
+    if (e != hipSuccess) return e;
+  }
+  if (a.shift_grad) {
+    e = fill_zero(a.shift_grad, a.full_batch * a.C, s);
+    if (e != hipSuccess) return e;
+    if (rows > 0)
+      e = dispatch<ShiftGrad>(a, dim3(gx, static_cast<unsigned>(a.batch)), dim3(64), s);
+  }
+  return e;
+}
+
+hipError_t launch_readout_forward(const ReadoutArgs& a, hipStream_t s) {
+  if (a.rows == 0) return hipSuccess;
+  const dim3 grid(static_cast<unsigned>(readout_row_blocks(a.rows)), static_cast<unsigned>(a.H));
+  if (a.op_bf16)
+    return a.act_bf16 ? launch(readout_forward_kernel<true, true>, grid, dim3(256), s, a)
+                      : launch(readout_forward_kernel<true, false>, grid, dim3(256), s, a);
+  return a.act_bf16 ? launch(readout_forward_kernel<false, true>, grid, dim3(256), s, a)
+                    : launch(readout_forward_kernel<false, false>, grid, dim3(256), s, a);
+}
+
+hipError_t launch_readout_backward(const ReadoutArgs& a, hipStream_t s) {
+  const int64_t C = a.H * 64;
+  float* outs[kReadoutSums] = {a.weight_grad, a.bias_grad, a.bonus_grad};
+  if (a.rows == 0) {
+    for (float* p : outs) {
+      const hipError_t e = fill_zero(p, C, s);
+      if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+  }
+  const int64_t rb = readout_row_blocks(a.rows);
+  const dim3 grid(static_cast<unsigned>(rb), static_cast<unsigned>(a.H));
+  hipError_t e;
+  if (a.op_bf16)
+    e = a.act_bf16 ? launch(readout_backward_kernel<true, true>, grid, dim3(256), s, a)
+                   : launch(readout_backward_kernel<true, false>, grid, dim3(256), s, a);
+  else
+    e = a.act_bf16 ? launch(readout_backward_kernel<false, true>, grid, dim3(256), s, a)
+                   : launch(readout_backward_kernel<false, false>, grid, dim3(256), s, a);
+  if (e != hipSuccess) return e;
+  return column_sum(a.workspace, rb, kReadoutSums, C, outs, s);
+}
+
+}  // namespace rwkv_nb

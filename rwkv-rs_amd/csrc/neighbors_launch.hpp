@@ -1,0 +1,70 @@
+// Launchers of the kernels that neighbour the WKV7 operator in a time mixer:
+// the token shift with its channel mixes before it, and the gated readout
+// (GroupNorm, bonus, gate) after it. The C ABI (neighbors_api.cpp) checks
+// every argument before it calls these.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace rwkv_nb {
+
+constexpr int kMaxMixes = 8;        // channel mixes of one token shift
+constexpr int kMixRowsPerWave = 8;  // rows (batch, step) one wave walks
+constexpr int kMixRowsPerBlock = 4 * kMixRowsPerWave;
+constexpr int kMixColsPerBlock = 256;  // 64 lanes x 4 channels
+constexpr int kReadoutRowsPerGroup = 4;  // rows one 16-lane group walks
+constexpr int kReadoutRowsPerBlock = 16 * kReadoutRowsPerGroup;
+constexpr int kReadoutSums = 3;     // group-norm weight, bias, bonus
+
+struct ShiftMixArgs {
+  const void* x;             // [rows, C] (rows = batch * T), dtype x_bf16
+  const void* shift;         // [full_batch, C] or null (zeros)
+  const int32_t* batch_ids;  // [batch] or null (identity)
+  const void* mask;          // [batch, T] in x's dtype, or null (all valid)
+  const float* scales;       // [num_mixes, C]
+  int64_t batch, T, C, full_batch;
+  int num_mixes;
+  bool x_bf16, out_bf16;
+  void* mixes[kMaxMixes];    // forward: [rows, C] each, out dtype
+  void* diff;                // forward: [rows, C] out dtype, or null
+  void* next_shift;          // forward: [full_batch, C] x dtype, or null
+  const void* mix_grads[kMaxMixes];  // backward: [rows, C] out dtype
+  const void* diff_grad;     // backward: [rows, C] out dtype, or null
+  void* x_grad;              // backward: [rows, C] x dtype
+  float* shift_grad;         // backward: [full_batch, C] or null
+  float* scales_grad;        // backward: [num_mixes, C]
+  float* workspace;          // backward: [row_blocks, num_mixes, C]
+};
+
+struct ReadoutArgs {
+  const void *y, *r, *k, *v;  // [rows, H, 64], operand dtype
+  const void* gate;           // [rows, H * 64], activation dtype
+  const float* bonus;         // [H, 64]
+  const float* weight;        // [H * 64]
+  const float* bias;          // [H * 64]
+  float eps;
+  int64_t rows, H;
+  bool op_bf16, act_bf16;
+  void* out;                  // forward: [rows, H * 64], activation dtype
+  const void* out_grad;       // backward: [rows, H * 64], activation dtype
+  void *y_grad, *r_grad, *k_grad, *v_grad;  // backward: operand dtype
+  void* gate_grad;            // backward: activation dtype
+  float *bonus_grad, *weight_grad, *bias_grad;  // backward
+  float* workspace;           // backward: [row_blocks, 3, H * 64]
+};
+
+inline int64_t mix_row_blocks(int64_t rows) {
+  return (rows + kMixRowsPerBlock - 1) / kMixRowsPerBlock;
+}
+inline int64_t readout_row_blocks(int64_t rows) {
+  return (rows + kReadoutRowsPerBlock - 1) / kReadoutRowsPerBlock;
+}
+
+hipError_t launch_shift_mix_forward(const ShiftMixArgs& a, hipStream_t s);
+hipError_t launch_shift_mix_backward(const ShiftMixArgs& a, hipStream_t s);
+hipError_t launch_readout_forward(const ReadoutArgs& a, hipStream_t s);
+hipError_t launch_readout_backward(const ReadoutArgs& a, hipStream_t s);
+
+}  // namespace rwkv_nb

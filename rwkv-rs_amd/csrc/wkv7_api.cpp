@@ -79,13 +79,17 @@ int check_shape(int64_t B, int64_t T, int64_t H, int64_t N, int64_t C, int dtype
 
 int check_flag(int f) { return (f == 0 || f == 1) ? WKV7_OK : WKV7_ERR_FLAGS; }
 
+}  // namespace
+
+namespace wkv7 {
 int hip_status(hipError_t e) {
   if (e == hipSuccess) return WKV7_OK;
   g_last_hip_error = static_cast<int>(e);
   return WKV7_ERR_HIP;
 }
+}  // namespace wkv7
 
-}  // namespace
+using wkv7::hip_status;
 
 extern "C" {
 

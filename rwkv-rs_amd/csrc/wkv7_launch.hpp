@@ -68,4 +68,8 @@ hipError_t launch_backward_chunked(const BackwardDesc& d, hipStream_t stream);
 hipError_t launch_backward(const BackwardDesc& d, hipStream_t stream);
 hipError_t launch_infer(const InferDesc& d, hipStream_t stream);
 
+// WKV7_OK for hipSuccess; otherwise records e for wkv7_last_hip_error() on
+// the calling thread and returns WKV7_ERR_HIP
+int hip_status(hipError_t e);
+
 }  // namespace wkv7

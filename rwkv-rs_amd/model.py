@@ -22,6 +22,15 @@ passes its ``K: Wkv7Kernel<B>`` type parameter:
   followed by the optimizer update (Adam betas (0.9, 0.99), eps 1e-16,
   training.rs:164-177)
 
+The ops on either side of the operator run, by default
+(``neighbor_ops="hip"``), as the fused kernels of ``neighbors``: the token
+shift with the five mixes and the readout gate's mix in one pass, the
+GroupNorm + bonus + gate readout in another (the gate's mix, x + diff *
+param_gate, moves from GatedReadout into that first pass). With
+``neighbor_ops="torch"`` they are the plain torch formulations below, kept as
+the readable mirror of the reference and as the reference the fused kernels
+are tested against.
+
 Weights are random N(0, 0.02) (normalisation layers start at one and zero);
 the reference's shape-aware initialiser is not needed to time or check a step.
 Matrix products run in bfloat16 under autocast with float32 master weights;
@@ -38,6 +47,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from . import neighbors as _nb
 from . import wkv7 as _wkv7
 
 CHUNK_LEN = 16                 # time_mixer/mod.rs:190
@@ -85,6 +95,23 @@ def infer_time_mixer_lora_ranks(num_cells: int, embedded_dim: int, head_size: in
         infer_lora_rank_from_formula(1.7 * root * factor),
         infer_lora_rank_from_formula(5.0 * root),
     )
+
+
+NEIGHBOR_OPS = ("hip", "torch")
+
+
+def _check_neighbor_ops(neighbor_ops: str) -> str:
+    if neighbor_ops not in NEIGHBOR_OPS:
+        raise ValueError(f"neighbor_ops must be one of {NEIGHBOR_OPS}, got {neighbor_ops!r}")
+    return neighbor_ops
+
+
+def _matmul_dtype(x: torch.Tensor) -> torch.dtype:
+    """The dtype a matrix product reading x computes in: autocast's, else x's."""
+    dt = x.device.type
+    if torch.is_autocast_enabled(dt):
+        return torch.get_autocast_dtype(dt)
+    return x.dtype
 
 
 # ------------------------------------------------------------- element-wise ops
@@ -204,6 +231,7 @@ class WeightPrepareOutput:
     value: torch.Tensor
     removal_key_normalized: torch.Tensor
     replacement: torch.Tensor
+    gate_input: Optional[torch.Tensor] = None   # the readout gate's mix, when fused here
 
     def reshape_to_wkv7_input(self, shape, dtype: Optional[torch.dtype] = None):
         """weight_prepare.rs:346-356, plus the cast to the operator's dtype."""
@@ -221,7 +249,7 @@ class WeightPrepare(nn.Module):
     """modules/time_mixer/weight_prepare.rs:28-131"""
 
     def __init__(self, num_cells, embedded_dim, num_heads, head_size, ranks: LoRARanks,
-                 cell_id: int):
+                 cell_id: int, neighbor_ops: str = "hip"):
         super().__init__()
         C = embedded_dim
         self.param_receptance = _param(1, 1, C)
@@ -239,15 +267,34 @@ class WeightPrepare(nn.Module):
         self.param_key_removal = _param(1, 1, C)
         self.param_key_replacement = _param(1, 1, C)
         self.num_heads, self.head_size, self.cell_id = num_heads, head_size, cell_id
+        self.neighbor_ops = _check_neighbor_ops(neighbor_ops)
 
     def forward(self, embedded_context, value_from_first_cell, embedded_token_shift=None,
-                context_mask=None) -> WeightPrepareOutput:
-        """weight_prepare.rs:210-330"""
-        diff, next_shift = token_shift_diff(embedded_context, embedded_token_shift, context_mask)
+                context_mask=None, gate_scale: Optional[torch.Tensor] = None
+                ) -> WeightPrepareOutput:
+        """weight_prepare.rs:210-330. With the HIP neighbour ops the token shift
+        and the five mixes are one kernel, which also forms the readout gate's
+        mix x + diff * ``gate_scale`` (gated_readout.rs:122) when it is given;
+        the difference itself is then not materialised."""
         B, T, C = embedded_context.shape
-        xr, xw, xk, xv, xa = addcmul5(embedded_context, diff, self.param_receptance,
-                                      self.param_weight_decay, self.param_key,
-                                      self.param_value, self.param_learning_rate)
+        scales = [self.param_receptance, self.param_weight_decay, self.param_key,
+                  self.param_value, self.param_learning_rate]
+        gate_input = None
+        if self.neighbor_ops == "hip":
+            want_next = embedded_token_shift is not None
+            res = _nb.token_shift_mix(
+                embedded_context, scales + ([gate_scale] if gate_scale is not None else []),
+                embedded_token_shift, None, context_mask, _matmul_dtype(embedded_context),
+                return_next_token_shift=want_next)
+            mixes, next_shift = res if want_next else (res, None)
+            xr, xw, xk, xv, xa = mixes[:5]
+            if gate_scale is not None:
+                gate_input = mixes[5]
+            diff = None
+        else:
+            diff, next_shift = token_shift_diff(embedded_context, embedded_token_shift,
+                                                context_mask)
+            xr, xw, xk, xv, xa = addcmul5(embedded_context, diff, *scales)
         receptance = self.projection_receptance(xr)
         key_precursor = self.projection_key(xk)
         value_precursor = self.projection_value(xv)
@@ -269,14 +316,14 @@ class WeightPrepare(nn.Module):
         replacement = -removal_key_normalized * learning_rate
         return WeightPrepareOutput(diff, next_shift, value_from_first_cell, receptance,
                                    weight_decay, replacement_key, value,
-                                   removal_key_normalized, replacement)
+                                   removal_key_normalized, replacement, gate_input)
 
 
 class GatedReadout(nn.Module):
     """modules/time_mixer/gated_readout.rs:13-80"""
 
     def __init__(self, num_cells, embedded_dim, num_heads, head_size, ranks: LoRARanks,
-                 cell_id: int):
+                 cell_id: int, neighbor_ops: str = "hip"):
         super().__init__()
         C = embedded_dim
         self.param_gate = _param(1, 1, C)
@@ -284,12 +331,23 @@ class GatedReadout(nn.Module):
         self.param_receptance_key_bonus = _param(num_heads, C // num_heads)
         self.group_norm = nn.GroupNorm(num_heads, C, eps=GROUP_NORM_EPS)
         self.projection_output = _linear(C, C)
+        self.neighbor_ops = _check_neighbor_ops(neighbor_ops)
 
     def forward(self, embedded_context, token_shifted_diff, wkv7_forward_output,
-                receptance, replacement_key, value) -> torch.Tensor:
-        """gated_readout.rs:110-148; the last four operands are [B, T, H, N]."""
+                receptance, replacement_key, value,
+                gate_input: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """gated_readout.rs:110-148; the operator's output and operands are
+        [B, T, H, N]. ``gate_input`` is x + diff * param_gate when the token
+        shift kernel already formed it."""
         B, T, C = embedded_context.shape
-        gate = self.param_output_gate_lora(embedded_context + token_shifted_diff * self.param_gate)
+        if gate_input is None:
+            gate_input = embedded_context + token_shifted_diff * self.param_gate
+        gate = self.param_output_gate_lora(gate_input)
+        if self.neighbor_ops == "hip":
+            out = _nb.gated_readout(wkv7_forward_output, receptance, replacement_key, value,
+                                    gate, self.param_receptance_key_bonus,
+                                    self.group_norm.weight, self.group_norm.bias, GROUP_NORM_EPS)
+            return self.projection_output(out)
         # the operator's output comes back in its operand dtype; the norm runs
         # in the residual stream's
         y = wkv7_forward_output.to(embedded_context.dtype).reshape(B * T, C)
@@ -315,13 +373,14 @@ class TimeMixer(nn.Module):
     """modules/time_mixer/mod.rs:86-141"""
 
     def __init__(self, num_cells, embedded_dim, num_heads, head_size, cell_id: int,
-                 wkv7_dtype: torch.dtype = torch.bfloat16):
+                 wkv7_dtype: torch.dtype = torch.bfloat16, neighbor_ops: str = "hip"):
         super().__init__()
         ranks = infer_time_mixer_lora_ranks(num_cells, embedded_dim, head_size)
         self.weight_prepare = WeightPrepare(num_cells, embedded_dim, num_heads, head_size, ranks,
-                                            cell_id)
+                                            cell_id, neighbor_ops)
         self.gated_readout = GatedReadout(num_cells, embedded_dim, num_heads, head_size, ranks,
-                                          cell_id)
+                                          cell_id, neighbor_ops)
+        self.neighbor_ops = _check_neighbor_ops(neighbor_ops)
         self.num_heads, self.head_size, self.cell_id = num_heads, head_size, cell_id
         self.wkv7_dtype = wkv7_dtype
 
@@ -332,13 +391,14 @@ class TimeMixer(nn.Module):
         B, T, _ = io.embedded_context.shape
         x = apply_context_mask(io.embedded_context, io.context_mask)
         v_first = apply_context_mask(io.value_from_first_cell, io.context_mask)
-        wp = self.weight_prepare(x, v_first, io.embedded_token_shift, io.context_mask)
+        gate_scale = self.gated_readout.param_gate if self.neighbor_ops == "hip" else None
+        wp = self.weight_prepare(x, v_first, io.embedded_token_shift, io.context_mask, gate_scale)
         shape = (B, T, self.num_heads, self.head_size)
         wkv_in = wp.reshape_to_wkv7_input(shape, self.wkv7_dtype)
         out = kernel.forward(wkv_in, io.state, io.batch_ids, io.elapsed_t, CHUNK_LEN,
                              io.context_mask)
         y = self.gated_readout(x, wp.token_shifted_diff, out.output, wkv_in.receptance,
-                               wkv_in.replacement_key, wkv_in.value)
+                               wkv_in.replacement_key, wkv_in.value, wp.gate_input)
         return TimeMixerIO(
             embedded_context=apply_context_mask(y, io.context_mask),
             batch_ids=io.batch_ids, elapsed_t=io.elapsed_t, context_mask=io.context_mask,
@@ -350,18 +410,26 @@ class TimeMixer(nn.Module):
 class ChannelMixer(nn.Module):
     """modules/channel_mixer/mod.rs:20-121"""
 
-    def __init__(self, num_cells, embedded_dim, cell_id: int):
+    def __init__(self, num_cells, embedded_dim, cell_id: int, neighbor_ops: str = "hip"):
         super().__init__()
         self.key = _linear(embedded_dim, embedded_dim * 4)
         self.value = _linear(embedded_dim * 4, embedded_dim)
         self.token_shift_diff_scale = _param(1, 1, embedded_dim)
+        self.neighbor_ops = _check_neighbor_ops(neighbor_ops)
 
     def forward(self, embedded_context, embedded_token_shift=None, context_mask=None):
         """channel_mixer/mod.rs:83-121; returns (output, next_token_shift or None)."""
         return_shift = embedded_token_shift is not None
         x = apply_context_mask(embedded_context, context_mask)
-        diff, next_shift = token_shift_diff(x, embedded_token_shift, context_mask)
-        k = torch.relu(self.key(addcmul(x, diff, self.token_shift_diff_scale))) ** 2
+        if self.neighbor_ops == "hip":
+            res = _nb.token_shift_mix(x, [self.token_shift_diff_scale], embedded_token_shift, None,
+                                      context_mask, _matmul_dtype(x),
+                                      return_next_token_shift=return_shift)
+            (mixed,), next_shift = res if return_shift else (res, None)
+        else:
+            diff, next_shift = token_shift_diff(x, embedded_token_shift, context_mask)
+            mixed = addcmul(x, diff, self.token_shift_diff_scale)
+        k = torch.relu(self.key(mixed)) ** 2
         out = apply_context_mask(self.value(k), context_mask)
         return out, (next_shift if return_shift else None)
 
@@ -371,13 +439,13 @@ class CausalCell(nn.Module):
     added to the residual stream."""
 
     def __init__(self, num_cells, embedded_dim, num_heads, head_size, cell_id: int,
-                 wkv7_dtype: torch.dtype = torch.bfloat16):
+                 wkv7_dtype: torch.dtype = torch.bfloat16, neighbor_ops: str = "hip"):
         super().__init__()
         self.pre_layer_norm_for_time_mix = nn.LayerNorm(embedded_dim)
         self.pre_layer_norm_for_channel_mix = nn.LayerNorm(embedded_dim)
         self.time_mixer = TimeMixer(num_cells, embedded_dim, num_heads, head_size, cell_id,
-                                    wkv7_dtype)
-        self.channel_mixer = ChannelMixer(num_cells, embedded_dim, cell_id)
+                                    wkv7_dtype, neighbor_ops)
+        self.channel_mixer = ChannelMixer(num_cells, embedded_dim, cell_id, neighbor_ops)
 
     def forward(self, x, batch_ids, elapsed_t, value_from_first_cell, state, shift_time,
                 shift_channel, context_mask, kernel):
@@ -396,10 +464,10 @@ class MultiCausalCells(nn.Module):
     precursor feeds every later cell's value residual."""
 
     def __init__(self, num_cells, embedded_dim, num_heads, head_size,
-                 wkv7_dtype: torch.dtype = torch.bfloat16):
+                 wkv7_dtype: torch.dtype = torch.bfloat16, neighbor_ops: str = "hip"):
         super().__init__()
         self.cells = nn.ModuleList(
-            CausalCell(num_cells, embedded_dim, num_heads, head_size, i, wkv7_dtype)
+            CausalCell(num_cells, embedded_dim, num_heads, head_size, i, wkv7_dtype, neighbor_ops)
             for i in range(num_cells))
 
     def forward(self, x, batch_ids, kernel, elapsed_t=None, context_mask=None,
@@ -432,13 +500,15 @@ class AutoRegressiveModel(nn.Module):
     cells, layer norm, unembedding, l2wrap and mean cross entropy."""
 
     def __init__(self, vocab_size: int, num_cells: int, embedded_dim: int, num_heads: int,
-                 head_size: int = 64, wkv7_dtype: torch.dtype = torch.bfloat16):
+                 head_size: int = 64, wkv7_dtype: torch.dtype = torch.bfloat16,
+                 neighbor_ops: str = "hip"):
         super().__init__()
         if embedded_dim != num_heads * head_size:
             raise ValueError("embedded_dim must equal num_heads * head_size")
         self.embed = nn.Embedding(vocab_size, embedded_dim)
         self.layer_norm_for_first_cell = nn.LayerNorm(embedded_dim)
-        self.cells = MultiCausalCells(num_cells, embedded_dim, num_heads, head_size, wkv7_dtype)
+        self.cells = MultiCausalCells(num_cells, embedded_dim, num_heads, head_size, wkv7_dtype,
+                                      neighbor_ops)
         self.layer_norm_for_unembed = nn.LayerNorm(embedded_dim)
         self.unembed = _linear(embedded_dim, vocab_size)
         self.vocab_size = vocab_size

@@ -48,10 +48,12 @@ class TorchKernel:
         return wk.KernelOutput(output=y, next_state=state)
 
 
-def tiny_model(seed=0, cells=2, heads=2, vocab=97, std=0.02, wkv7_dtype=torch.float32):
+def tiny_model(seed=0, cells=2, heads=2, vocab=97, std=0.02, wkv7_dtype=torch.float32,
+               neighbor_ops="torch"):
     m = _model_mod()
     torch.manual_seed(seed)
-    model = m.AutoRegressiveModel(vocab, cells, heads * 64, heads, 64, wkv7_dtype=wkv7_dtype)
+    model = m.AutoRegressiveModel(vocab, cells, heads * 64, heads, 64, wkv7_dtype=wkv7_dtype,
+                                  neighbor_ops=neighbor_ops)
     g = torch.Generator().manual_seed(seed)
     return model.init_random(std, g)
 

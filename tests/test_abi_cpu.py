@@ -1,4 +1,5 @@
-"""CPU-only checks of the C ABI (include/wkv7.h): the library loads, exports
+"""CPU-only checks of the C ABI (include/wkv7.h, include/rwkv_neighbors.h):
+the library loads, exports
 every declared entry point, and rejects bad calls on the host with the right
 status before any HIP call. No kernel is launched here: every call either
 fails validation or has nothing to do."""
@@ -12,6 +13,7 @@ import pytest
 from conftest import REPO, load_pkg
 
 HEADER = os.path.join(REPO, "include", "wkv7.h")
+NEIGHBORS_HEADER = os.path.join(REPO, "include", "rwkv_neighbors.h")
 
 
 @pytest.fixture(scope="module")
@@ -21,21 +23,24 @@ def native():
     return n
 
 
-def declared_functions():
-    text = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:int|int64_t|const char \*)\s*(wkv7_\w+)\s*\(", text, re.M)))
+def declared_functions(header=HEADER, prefix="wkv7_"):
+    text = open(header).read()
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|const char \*)\s*(" + prefix + r"\w+)\s*\(",
+                                 text, re.M)))
 
 
 def test_header_declares_expected_entry_points():
     names = declared_functions()
     assert len(names) == 13, names
+    assert len(declared_functions(NEIGHBORS_HEADER, "rwkv_")) == 6
 
 
 def test_library_exports_every_declared_symbol(native):
     lib = native.lib()
-    for name in declared_functions():
+    declared = declared_functions() + declared_functions(NEIGHBORS_HEADER, "rwkv_")
+    for name in declared:
         assert hasattr(lib, name), name
-    assert set(declared_functions()) == set(native.EXPORTS)
+    assert set(declared) == set(native.EXPORTS)
 
 
 def test_version_and_strings(native):

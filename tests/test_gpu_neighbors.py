@@ -1,0 +1,187 @@
+"""GPU parity of the fused neighbour kernels (include/rwkv_neighbors.h)
+against float64 PyTorch on the CPU of the same ops, forward and backward:
+
+* token shift + mixes against ``model.token_shift_diff`` + ``addcmul`` (the
+  torch mirror of token_shift_diff/kernel.rs:17-64 and addcmul/kernel.rs),
+  with and without masks, external shifts and slot-mapped batch ids; fp32
+  results within 1e-5 relative L2, bf16 outputs within bf16 rounding (8e-3);
+* the gated readout against GroupNorm + bonus + gate written with torch ops
+  (gated_readout.rs:126-145), same bars;
+* the whole language model with the fused ops against the same model with
+  the torch formulations (same weights and tokens): loss and every
+  parameter gradient within 1e-4 in fp32.
+"""
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from conftest import announce, load_pkg, rel_l2
+from model_helpers import _model_mod, loss_and_grads, tiny_model, tokens
+
+pytestmark = pytest.mark.gpu
+
+F32_TOL = 1e-5
+BF16_TOL = 8e-3
+
+
+def _nb():
+    return load_pkg().neighbors
+
+
+def _err(got, want):
+    return rel_l2(got.detach().double().cpu().numpy(), want.detach().double().cpu().numpy())
+
+
+# ---------------------------------------------------------------- token shift
+SHIFT_CASES = [
+    dict(B=2, T=33, C=64, K=5, mask=False, shift=False, ids=False, xdt="f32", odt="f32"),
+    dict(B=3, T=17, C=192, K=6, mask=True, shift=True, ids=True, xdt="f32", odt="f32"),
+    dict(B=2, T=40, C=768, K=6, mask=False, shift=False, ids=False, xdt="f32", odt="bf16"),
+    dict(B=2, T=9, C=260, K=5, mask=True, shift=False, ids=False, xdt="f32", odt="f32"),
+    dict(B=4, T=1, C=128, K=1, mask=False, shift=True, ids=True, xdt="f32", odt="f32"),
+    dict(B=2, T=16, C=128, K=6, mask=True, shift=True, ids=False, xdt="bf16", odt="bf16"),
+    dict(B=16, T=512, C=768, K=6, mask=False, shift=False, ids=False, xdt="f32", odt="bf16"),
+]
+DT = {"f32": torch.float32, "bf16": torch.bfloat16}
+
+
+def _shift_case_id(c):
+    return "B{B}T{T}C{C}K{K}{m}{s}{i}_{xdt}_{odt}".format(
+        m="_mask" if c["mask"] else "", s="_shift" if c["shift"] else "",
+        i="_ids" if c["ids"] else "", **c)
+
+
+@pytest.mark.parametrize("case", SHIFT_CASES, ids=_shift_case_id)
+def test_token_shift_mix_matches_torch(case):
+    m = _model_mod()
+    nb = _nb()
+    B, T, C, K = case["B"], case["T"], case["C"], case["K"]
+    xdt, odt = DT[case["xdt"]], DT[case["odt"]]
+    g = torch.Generator().manual_seed(B * 1000 + T * 10 + C)
+    x = torch.randn(B, T, C, generator=g).to(xdt)
+    scales = [torch.rand(1, 1, C, generator=g) for _ in range(K)]
+    full = B + 3 if case["ids"] else B
+    ids = torch.randperm(full, generator=g)[:B] if case["ids"] else None
+    shift = torch.randn(full, C, generator=g).to(xdt) if case["shift"] else None
+    mask = None
+    if case["mask"]:
+        mask = (torch.rand(B, T, generator=g) > 0.3).float()
+        mask[0, :3] = 0.0
+        if B > 2:
+            mask[2] = 0.0                 # a row with no valid step
+        x = x * mask.unsqueeze(2).to(xdt)
+    grads = [torch.randn(B, T, C, generator=g).to(odt) for _ in range(K)]
+
+    # float64 torch on the CPU
+    x64 = x.double().requires_grad_(True)
+    sc64 = [s.double().requires_grad_(True) for s in scales]
+    sh64 = shift.double().requires_grad_(True) if shift is not None else None
+    rows = sh64[ids] if (sh64 is not None and ids is not None) else sh64
+    diff, nxt = m.token_shift_diff(x64, rows, mask.double() if mask is not None else None)
+    want = [m.addcmul(x64, diff, s) for s in sc64]
+    loss = sum((w * gg.double()).sum() for w, gg in zip(want, grads))
+    loss.backward()
+    want_next = None
+    if shift is not None:
+        want_next = shift.double().clone()
+        if ids is not None:
+            want_next[ids] = nxt.detach()
+        else:
+            want_next = nxt.detach()
+
+    dev = torch.device("cuda:0")
+    xg = x.to(dev).requires_grad_(True)
+    scg = [s.to(dev).requires_grad_(True) for s in scales]
+    shg = shift.to(dev).requires_grad_(True) if shift is not None else None
+    announce("token_shift_mix", _shift_case_id(case))
+    res = nb.token_shift_mix(xg, scg, shg, ids.to(dev) if ids is not None else None,
+                             mask.to(dev) if mask is not None else None, odt,
+                             return_next_token_shift=shift is not None)
+    mixes, got_next = res if shift is not None else (res, None)
+    sum((mx.float() * gg.to(dev).float()).sum() for mx, gg in zip(mixes, grads)).backward()
+    torch.cuda.synchronize()
+
+    out_tol = BF16_TOL if odt == torch.bfloat16 else F32_TOL
+    for i in range(K):
+        assert mixes[i].dtype == odt
+        assert _err(mixes[i], want[i]) <= out_tol, ("mix", i)
+    grad_tol = BF16_TOL if xdt == torch.bfloat16 else F32_TOL
+    assert _err(xg.grad, x64.grad) <= grad_tol
+    for i in range(K):
+        assert _err(scg[i].grad, sc64[i].grad) <= F32_TOL, ("scale", i)
+    if shift is not None:
+        assert _err(shg.grad, sh64.grad) <= grad_tol
+        assert _err(got_next, want_next) == 0.0        # a copy of x or of the shift
+
+
+# --------------------------------------------------------------- gated readout
+READOUT_CASES = [
+    dict(B=2, T=24, H=3, op="f32", act="f32"),
+    dict(B=2, T=16, H=12, op="bf16", act="bf16"),
+    dict(B=1, T=70, H=4, op="bf16", act="f32"),
+    dict(B=16, T=512, H=12, op="bf16", act="bf16"),
+]
+
+
+@pytest.mark.parametrize("case", READOUT_CASES,
+                         ids=lambda c: "B{B}T{T}H{H}_{op}_{act}".format(**c))
+def test_gated_readout_matches_torch(case):
+    nb = _nb()
+    B, T, H = case["B"], case["T"], case["H"]
+    C = H * 64
+    opd, actd = DT[case["op"]], DT[case["act"]]
+    g = torch.Generator().manual_seed(B * 100 + T + H)
+    y, r, k, v = (torch.randn(B, T, H, 64, generator=g).to(opd) for _ in range(4))
+    y = (y.float() * 3.0 + 0.5).to(opd)           # a non-trivial mean and scale per group
+    gate = torch.rand(B, T, C, generator=g).to(actd)
+    bonus = torch.randn(H, 64, generator=g) * 0.1
+    weight = 1.0 + 0.1 * torch.randn(C, generator=g)
+    bias = 0.1 * torch.randn(C, generator=g)
+    dout = torch.randn(B, T, C, generator=g).to(actd)
+
+    ins64 = [t.double().requires_grad_(True) for t in (y, r, k, v, gate, bonus, weight, bias)]
+    y64, r64, k64, v64, g64, bo64, w64, b64 = ins64
+    yn = F.group_norm(y64.reshape(B * T, C), H, w64, b64, 64e-5).reshape(B, T, C)
+    bon = ((r64 * k64 * bo64).sum(-1, keepdim=True) * v64).reshape(B, T, C)
+    want = (yn + bon) * g64
+    (want * dout.double()).sum().backward()
+
+    dev = torch.device("cuda:0")
+    ins = [t.to(dev).requires_grad_(True) for t in (y, r, k, v, gate, bonus, weight, bias)]
+    announce("gated_readout", case)
+    out = nb.gated_readout(*ins, eps=64e-5)
+    (out.float() * dout.to(dev).float()).sum().backward()
+    torch.cuda.synchronize()
+    assert out.dtype == actd
+    assert _err(out, want) <= (BF16_TOL if actd == torch.bfloat16 else F32_TOL)
+    names = ("y", "r", "k", "v", "gate", "bonus", "weight", "bias")
+    for n, a, b in zip(names, ins, ins64):
+        tol = F32_TOL
+        if n in ("y", "r", "k", "v") and opd == torch.bfloat16:
+            tol = BF16_TOL
+        if n == "gate" and actd == torch.bfloat16:
+            tol = BF16_TOL
+        assert _err(a.grad, b.grad) <= tol, n
+
+
+# ------------------------------------------------------------ the whole model
+def test_model_fused_neighbours_match_torch_ops():
+    wk = load_pkg().wkv7
+    dev = torch.device("cuda:0")
+    fused = tiny_model(std=0.2, neighbor_ops="hip").to(dev)
+    plain = tiny_model(std=0.2, neighbor_ops="torch").to(dev)
+    plain.load_state_dict(fused.state_dict())
+    inputs, targets = (t.to(dev) for t in tokens(2, 64, 97))
+    announce("model", "neighbor_ops=torch")
+    l0, g0 = loss_and_grads(plain, wk.KernelPretrain, inputs, targets)
+    announce("model", "neighbor_ops=hip")
+    l1, g1 = loss_and_grads(fused, wk.KernelPretrain, inputs, targets)
+    torch.cuda.synchronize()
+    assert abs(l1 - l0) <= 1e-5 * abs(l0), (l0, l1)
+    assert g0.keys() == g1.keys()
+    errs = {n: _err(g1[n], g0[n]) for n in g0}
+    worst = max(errs, key=errs.get)
+    print(f"[fused neighbours] loss {l0:.6f} vs {l1:.6f}; worst grad {worst} {errs[worst]:.3e}")
+    assert errs[worst] <= 1e-4, (worst, errs[worst])

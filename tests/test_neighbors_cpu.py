@@ -1,0 +1,129 @@
+"""CPU-only checks of the neighbour ops' C ABI (include/rwkv_neighbors.h):
+workspace sizes, and host-side rejection of bad calls with the right status
+before any HIP call (no kernel is launched: every call here fails
+validation)."""
+
+import ctypes
+
+import pytest
+
+from conftest import load_pkg
+
+FAKE = 0x10000   # 64 KiB-aligned addresses that are never dereferenced
+F32, BF16 = 0, 1
+
+
+@pytest.fixture(scope="module")
+def lib():
+    n = load_pkg()._native
+    return n.lib()
+
+
+def ptrs(*addrs):
+    arr = (ctypes.c_void_p * max(len(addrs), 1))()
+    for i, a in enumerate(addrs):
+        arr[i] = a
+    return arr
+
+
+def mix_fwd(lib, **over):
+    a = dict(x=FAKE, shift=None, ids=None, mask=None, scales=FAKE * 2, K=2, B=2, T=8, C=64,
+             full=2, dtype=F32, out=F32, mixes=ptrs(FAKE * 10, FAKE * 20), diff=None, nxt=None)
+    a.update(over)
+    return lib.rwkv_token_shift_mix_forward(a["x"], a["shift"], a["ids"], a["mask"], a["scales"],
+                                            a["K"], a["B"], a["T"], a["C"], a["full"], a["dtype"],
+                                            a["out"], a["mixes"], a["diff"], a["nxt"], None)
+
+
+def test_token_shift_mix_workspace_bytes(lib):
+    f = lib.rwkv_token_shift_mix_workspace_bytes
+    # 32 rows per block: 8192 rows -> 256 blocks x 6 mixes x 768 channels x 4 B
+    assert f(6, 16, 512, 768) == 256 * 6 * 768 * 4
+    assert f(5, 1, 33, 64) == 2 * 5 * 64 * 4
+    assert f(1, 0, 5, 64) == 0
+    assert f(9, 1, 1, 64) == -1
+    assert f(1, 1, 1, 6) == -1
+    assert f(1, -1, 1, 64) == -1
+
+
+def test_token_shift_mix_forward_validation(lib):
+    assert mix_fwd(lib, dtype=2) == 5
+    assert mix_fwd(lib, out=7) == 5
+    assert mix_fwd(lib, K=9) == 2
+    assert mix_fwd(lib, C=6) == 2
+    assert mix_fwd(lib, B=-1) == 2
+    assert mix_fwd(lib, B=70000, full=70000) == 2
+    assert mix_fwd(lib, x=None) == 1
+    assert mix_fwd(lib, scales=None) == 1
+    assert mix_fwd(lib, mixes=ptrs(FAKE * 10, 0)) == 1
+    assert mix_fwd(lib, x=FAKE + 4) == 6                     # fp32 needs 16 bytes
+    assert mix_fwd(lib, mixes=ptrs(FAKE * 10, FAKE * 20 + 8)) == 6
+    assert mix_fwd(lib, full=1) == 2                         # no batch ids: full batch >= batch
+    assert mix_fwd(lib, mixes=ptrs(FAKE * 10, FAKE * 10)) == 7   # two outputs alias
+    assert mix_fwd(lib, mixes=ptrs(FAKE, FAKE * 20)) == 7        # an output overlaps x
+
+
+def test_token_shift_mix_backward_validation(lib):
+    def bwd(**over):
+        a = dict(x=FAKE, K=2, B=2, T=8, C=64, grads=ptrs(FAKE * 10, FAKE * 20), dx=FAKE * 30,
+                 dsc=FAKE * 40, ws=FAKE * 50, wsb=1 << 20)
+        a.update(over)
+        return lib.rwkv_token_shift_mix_backward(a["x"], None, None, None, FAKE * 2, a["K"],
+                                                 a["B"], a["T"], a["C"], 2, F32, F32, a["grads"],
+                                                 None, a["dx"], None, a["dsc"], a["ws"], a["wsb"],
+                                                 None)
+    assert bwd(ws=None) == 2
+    assert bwd(wsb=16) == 2
+    assert bwd(dx=None) == 1
+    assert bwd(dsc=None) == 1
+    assert bwd(grads=ptrs(FAKE * 10, 0)) == 1
+    assert bwd(dx=FAKE * 10) == 7                            # gradient output over a gradient input
+
+
+def ro_fwd(lib, **over):
+    a = dict(y=FAKE, r=FAKE * 2, k=FAKE * 3, v=FAKE * 4, g=FAKE * 5, bonus=FAKE * 6,
+             w=FAKE * 7, b=FAKE * 8, eps=64e-5, rows=16, H=2, N=64, dtype=BF16, act=F32,
+             out=FAKE * 20)
+    a.update(over)
+    return lib.rwkv_gated_readout_forward(a["y"], a["r"], a["k"], a["v"], a["g"], a["bonus"],
+                                          a["w"], a["b"], a["eps"], a["rows"], a["H"], a["N"],
+                                          a["dtype"], a["act"], a["out"], None)
+
+
+def test_gated_readout_workspace_bytes(lib):
+    f = lib.rwkv_gated_readout_workspace_bytes
+    # 64 rows per block: 8192 rows -> 128 blocks x 3 sums x 768 channels x 4 B
+    assert f(8192, 12, 64) == 128 * 3 * 768 * 4
+    assert f(65, 1, 64) == 2 * 3 * 64 * 4
+    assert f(0, 4, 64) == 0
+    assert f(10, 4, 32) == -1
+    assert f(10, 0, 64) == -1
+
+
+def test_gated_readout_validation(lib):
+    assert ro_fwd(lib, N=32) == 4
+    assert ro_fwd(lib, dtype=3) == 5
+    assert ro_fwd(lib, H=0) == 2
+    assert ro_fwd(lib, rows=-1) == 2
+    assert ro_fwd(lib, eps=-1.0) == 2
+    assert ro_fwd(lib, eps=float("nan")) == 2
+    assert ro_fwd(lib, y=None) == 1
+    assert ro_fwd(lib, bonus=None) == 1
+    assert ro_fwd(lib, out=None) == 1
+    assert ro_fwd(lib, y=FAKE + 2) == 6                      # bf16 needs 8 bytes
+    assert ro_fwd(lib, g=FAKE * 5 + 8) == 6                  # fp32 needs 16 bytes
+    assert ro_fwd(lib, out=FAKE * 5) == 7                    # output over the gate
+    # nothing to do, nothing required but the parameters
+    assert ro_fwd(lib, rows=0, y=None, r=None, k=None, v=None, g=None, out=None) == 0
+
+
+def test_hip_neighbour_ops_refuse_cpu_tensors():
+    import torch
+    nb = load_pkg().neighbors
+    x = torch.zeros(1, 4, 8)
+    with pytest.raises(ValueError):
+        nb.token_shift_mix(x, [torch.zeros(8)])
+    y = torch.zeros(1, 4, 1, 64)
+    with pytest.raises(ValueError):
+        nb.gated_readout(y, y, y, y, torch.zeros(1, 4, 64), torch.zeros(1, 64), torch.zeros(64),
+                         torch.zeros(64))
