@@ -7,6 +7,7 @@ C ABI (include/wkv7.h) that mirrors rwkv-nn's Burn WKV7 operator traits.
 * ``neighbors`` -- the fused ops on either side of the operator (token shift
   + channel mixes, gated readout; include/rwkv_neighbors.h)
 * ``model``     -- an RWKV-7 language-model training step that calls ``wkv7``
+* ``weights``   -- RWKV-7 release checkpoints (.pth) mapped onto ``model``
 """
 
 import importlib
@@ -15,6 +16,6 @@ from . import synthetic  # noqa: F401
 
 
 def __getattr__(name):
-    if name in ("wkv7", "_native", "build", "model", "neighbors"):
+    if name in ("wkv7", "_native", "build", "model", "neighbors", "weights"):
         return importlib.import_module(f"{__name__}.{name}")
     raise AttributeError(name)
