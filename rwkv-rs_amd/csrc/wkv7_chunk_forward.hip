@@ -9,17 +9,23 @@
 // 37 small matrix products per chunk instead of 16 rank-2 updates with
 // reductions.
 //
-// Work layout: one workgroup of four waves per (batch, head). Steps are taken
-// four chunks (64 steps) at a time:
-//   phase 1  wave w prepares chunk w of the batch on its own: decays, the four
-//            16x16 step-by-step products, P on the matrix cores, W and U,
-//            and leaves every operand phase 2 needs in LDS, already in
-//            fragment order (one 16-byte or 8-byte load per lane);
-//   phase 2  the four chunks in order; wave w owns value columns 16w..16w+15
-//            of the state (state rows are independent in the forward) and
-//            computes SA, Y and the next state for them.
-// The raw inputs of the next batch stream into LDS (global_load_lds) during
-// phase 2.
+// Work layout: one workgroup of eight waves per (batch, head), two per SIMD,
+// in two groups that run concurrently and hand chunks over through LDS:
+//   prep waves 4-7  wave 4 + s prepares chunks c = s, s + 4, ... on its own:
+//                   stages the chunk's raw rows in its LDS region (loaded
+//                   into registers during the previous chunk), forms the
+//                   decays, the four 16x16 step-by-step products, P on the
+//                   matrix cores, W and U, and writes every operand the chain
+//                   needs to slot s, in fragment order (one 16-byte or 8-byte
+//                   load per lane); then it marks the slot ready;
+//   chain waves 0-3 take the chunks in order; wave w owns value columns
+//                   16w..16w+15 of the state (state rows are independent in
+//                   the forward), loads chunk c's operands from slot c % 4,
+//                   marks them taken, and computes SA, Y and the next state.
+// A prep wave overwrites its slot only after all four chain waves have taken
+// the chunk in it, so preparing chunk c overlaps the chain of chunks c-4 ..
+// c-1. The hand-over uses two LDS flags per slot and no barriers; every wait
+// is bounded, so a kernel whose flags went wrong ends instead of hanging.
 #include "wkv7_chunk.hpp"
 #include "wkv7_launch.hpp"
 
@@ -28,12 +34,17 @@ namespace {
 
 using namespace chunk;
 
-constexpr int kWaves = 4;
+constexpr int kChainWaves = 4;            // value tile = wave
+constexpr int kSlots = 4;                 // operand slots = prep waves
+constexpr int kWaves = kChainWaves + kSlots;
 constexpr int kBlock = 64 * kWaves;
-constexpr int kBatch = 4;                 // chunks per batch, one per wave
 constexpr int kVecs = 6;                  // staged inputs: x, r, k, a, b, v
 enum { S_X, S_R, S_K, S_A, S_B, S_V };
-constexpr int kPieces = kVecs * kBatch * kL * 8 / kBlock;   // 16-byte loads per thread
+constexpr int kPieces = kVecs * kL * 8 / 64;   // 16-byte loads per prep lane and chunk
+// polls of a hand-over flag before a wave gives up (each poll sleeps ~64
+// cycles): about 0.1 s, far beyond any legitimate wait in a kernel that runs
+// for well under a millisecond
+constexpr int kSpinLimit = 1 << 22;
 
 // Phase-1 products of one chunk, each in the fragment order its phase-2
 // consumer loads (index [lane] last). K~ and B~ are kept without the chunk's
@@ -61,16 +72,16 @@ struct FwdChunkParams {
   int T, H, C;
 };
 
-// Phase 1 for one chunk, run by one wave. `stg` holds the chunk's raw rows;
-// after they are read, the chunk's x, r, k, a, b rows and the wave's scratch
-// `scr` are reused for the hi/lo rows of A^, K~ and B~, from which the
+// The preparation of one chunk, run by one wave. `stg` holds the chunk's raw
+// rows; after they are read, the chunk's x, r, k, a, b rows and the wave's
+// scratch `scr` are reused for the hi/lo rows of A^, K~ and B~, from which the
 // transposed fragments are read.
-__device__ __forceinline__ void prepare_chunk(bf16_t (*stg)[kBatch][kL][64], int q,
-                                              float (*scr)[kL][kL], ChunkOps& o, int lane) {
+__device__ __forceinline__ void prepare_chunk(bf16_t (*stg)[kL][64], float (*scr)[kL][kL],
+                                              ChunkOps& o, int lane) {
   const int t = lane & 15, qd = lane >> 4;
   // the lane's step row t, keys 32 m + 16 hh + 4 qd + c (c < 4), as raw bf16
   auto raw = [&](int vec, int m, int hh) -> uint2 {
-    return *reinterpret_cast<const uint2*>(tile_at(stg[vec][q], t, 32 * m + 16 * hh + 4 * qd));
+    return *reinterpret_cast<const uint2*>(tile_at(stg[vec], t, 32 * m + 16 * hh + 4 * qd));
   };
   auto widen = [](uint2 u) -> f32x4 {
     return f32x4{__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
@@ -138,7 +149,7 @@ __device__ __forceinline__ void prepare_chunk(bf16_t (*stg)[kBatch][kL][64], int
 
   // hi/lo rows of A^, K~, B~ into LDS (the chunk's raw rows are consumed),
   // then their transposed fragments (row = key, k = step) by transposed loads
-  bf16_t (*rows[6])[64] = {stg[S_X][q], stg[S_R][q], stg[S_K][q], stg[S_A][q], stg[S_B][q],
+  bf16_t (*rows[6])[64] = {stg[S_X], stg[S_R], stg[S_K], stg[S_A], stg[S_B],
                            reinterpret_cast<bf16_t (*)[64]>(&scr[0][0][0])};
 #pragma unroll
   for (int m = 0; m < 2; ++m)
@@ -184,7 +195,7 @@ __device__ __forceinline__ void prepare_chunk(bf16_t (*stg)[kBatch][kL][64], int
   const bf16x8 Ps = stack(P);
 #pragma unroll
   for (int vb = 0; vb < 4; ++vb) {
-    const bf16x4 vt = tr(stg[S_V][q], vb);
+    const bf16x4 vt = tr(stg[S_V], vb);
     o.v[vb][lane] = vt;
     const f32x4 X = mma_s2(ak, vt, f32x4{0.f, 0.f, 0.f, 0.f});
     o.u[vb][lane] = mma_s3(Ps, split4(X), f32x4{0.f, 0.f, 0.f, 0.f});
@@ -227,13 +238,53 @@ __device__ __forceinline__ ChainOps load_chain_ops(const ChunkOps& o, int jb, in
   return c;
 }
 
+// a prep wave's LDS: the raw rows of the chunk it prepares, then (reused)
+// the hi/lo rows of A^, K~, B~; 16-byte pieces of a row rotated by the step
+// index so that row and transposed reads spread over the banks
+struct PrepLds {
+  bf16_t stg[kVecs][kL][64];
+  float scr[2][kL][kL];
+};
+
+// hand-over flags: ready[s] = the chunk whose operands are in slot s,
+// taken[s][w] = the last chunk chain wave w loaded from slot s
+struct Flags {
+  int ready[kSlots];
+  int taken[kSlots][kChainWaves];
+};
+
+__device__ __forceinline__ int lds_load_flag(const int* f) {
+  return __atomic_load_n(f, __ATOMIC_RELAXED);
+}
+__device__ __forceinline__ void lds_store_flag(int* f, int v) {
+  __atomic_store_n(f, v, __ATOMIC_RELAXED);
+}
+// the wave's earlier LDS writes are complete before its later LDS accesses
+__device__ __forceinline__ void lds_release() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+}
+__device__ __forceinline__ void lds_acquire() {
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// A prep lane's share of a chunk's raw rows: piece k is row 8 k + lane / 8
+// of the chunk's 6 x 16 rows (vec k / 2, step 8 (k % 2) + lane / 8); LDS slot
+// lane % 8 of that row holds global 16-byte piece (slot - tile_rot(step)) % 8.
+// Kept as named values so that the compiler holds them in registers across
+// the preparation of a chunk.
+__device__ __forceinline__ const uint4* raw_piece(const FwdChunkParams& p, int64_t tok0,
+                                                  int64_t tstride, int c, int lane, int k) {
+  const int vec = k >> 1, step = 8 * (k & 1) + (lane >> 3);
+  const int oct = ((lane & 7) - tile_rot(step)) & 7;
+  return reinterpret_cast<const uint4*>(p.in[vec] + tok0 + (int64_t)(kL * c + step) * tstride +
+                                        8 * oct);
+}
+
 template <bool kHasS0>
 __global__ __launch_bounds__(kBlock, 1) void wkv7_fwd_chunk_kernel(const FwdChunkParams p) {
-  __shared__ ChunkOps ops[kBatch];
-  // raw inputs of a batch: [vec][chunk][step][64 bf16], 16-byte pieces of a
-  // row rotated by the step index so phase-1 reads spread over the banks
-  __shared__ __attribute__((aligned(16))) bf16_t stg[kVecs][kBatch][kL][64];
-  __shared__ __attribute__((aligned(16))) float scr[kWaves][2][kL][kL];
+  __shared__ ChunkOps ops[kSlots];
+  __shared__ __attribute__((aligned(16))) PrepLds prep[kSlots];
+  __shared__ Flags flags;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int t = lane & 15, qd = lane >> 4;
@@ -241,27 +292,54 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_fwd_chunk_kernel(const FwdChun
   const int64_t bh = (int64_t)b * H + h;
   const int64_t tstride = (int64_t)H * kHead;              // elements per step
   const int64_t tok0 = ((int64_t)b * T * H + h) * kHead;   // step 0 of (b, h)
-  const int nchunks = T / kL, nbatches = (nchunks + kBatch - 1) / kBatch;
+  const int nchunks = T / kL;
 
-  // ---- staging loads: thread tid moves pieces k = 0..kPieces-1 of a batch.
-  // Piece p = kBlock * k + tid is row p / 8 = (vec, chunk, step), slot p % 8,
-  // which holds global 16-byte piece (slot - tile_rot(step)) % 8 of the row.
-  const int st_t = (tid >> 3) & 15, st_slot = tid & 7;
-  const int st_oct = (st_slot - tile_rot(st_t)) & 7;
-  auto issue = [&](int n) {
-    const int nq = min(kBatch, nchunks - kBatch * n);
-#pragma unroll
-    for (int k = 0; k < kPieces; ++k) {
-      const int vec = k >> 1, q = 2 * (k & 1) + (tid >> 7);
-      if (q < nq) {
-        const bf16_t* src = p.in[vec] + tok0 + (int64_t)(kL * (kBatch * n + q) + st_t) * tstride + 8 * st_oct;
-        load_lds16(src, reinterpret_cast<char*>(&stg[0][0][0][0]) + (kBlock * k + 64 * wave) * 16);
+  if (tid < kSlots) flags.ready[tid] = -1;
+  if (tid < kSlots * kChainWaves) flags.taken[tid / kChainWaves][tid % kChainWaves] = tid / kChainWaves - kSlots;
+  __syncthreads();
+
+  if (wave >= kChainWaves) {
+    // ================================================= prep wave for slot s
+    const int s = wave - kChainWaves;
+    PrepLds& my = prep[s];
+    // The raw rows of the next chunk are loaded into registers while this one
+    // is prepared (one chunk of loads in flight hides their latency; LDS has no
+    // room for a second staging region per wave).
+    static_assert(kPieces == 12, "twelve 16-byte pieces per lane and chunk");
+    if (s >= nchunks) return;
+#define RWKV_RAW_LOAD(c) \
+  r0 = *raw_piece(p, tok0, tstride, c, lane, 0); r1 = *raw_piece(p, tok0, tstride, c, lane, 1); \
+  r2 = *raw_piece(p, tok0, tstride, c, lane, 2); r3 = *raw_piece(p, tok0, tstride, c, lane, 3); \
+  r4 = *raw_piece(p, tok0, tstride, c, lane, 4); r5 = *raw_piece(p, tok0, tstride, c, lane, 5); \
+  r6 = *raw_piece(p, tok0, tstride, c, lane, 6); r7 = *raw_piece(p, tok0, tstride, c, lane, 7); \
+  r8 = *raw_piece(p, tok0, tstride, c, lane, 8); r9 = *raw_piece(p, tok0, tstride, c, lane, 9); \
+  r10 = *raw_piece(p, tok0, tstride, c, lane, 10); r11 = *raw_piece(p, tok0, tstride, c, lane, 11);
+    uint4 r0, r1, r2, r3, r4, r5, r6, r7, r8, r9, r10, r11;
+    RWKV_RAW_LOAD(s)
+    for (int c = s; c < nchunks; c += kSlots) {
+      uint4* const dst = reinterpret_cast<uint4*>(&my.stg[0][0][0]) + lane;
+      dst[0] = r0; dst[64] = r1; dst[128] = r2; dst[192] = r3; dst[256] = r4; dst[320] = r5;
+      dst[384] = r6; dst[448] = r7; dst[512] = r8; dst[576] = r9; dst[640] = r10; dst[704] = r11;
+      // the last chunk reloads itself (harmless) so that the loads need no branch
+      const int cn = c + kSlots < nchunks ? c + kSlots : c;
+      RWKV_RAW_LOAD(cn)
+      // the slot is free once every chain wave has taken chunk c - kSlots
+      for (int w = 0; w < kChainWaves; ++w) {
+        for (int n = 0; n < kSpinLimit && lds_load_flag(&flags.taken[s][w]) < c - kSlots; ++n)
+          __builtin_amdgcn_s_sleep(1);
       }
+      lds_acquire();
+      prepare_chunk(my.stg, my.scr, ops[s], lane);
+      lds_release();
+      if (lane == 0) lds_store_flag(&flags.ready[s], c);
     }
-  };
+#undef RWKV_RAW_LOAD
+    return;
+  }
 
-  // ---- state: value tile jb = wave, key tiles ib = 0..3, result layout
-  // (rows = key i = 16 ib + 4 qd + r, columns = value j = 16 jb + t)
+  // ===================================================== chain wave: value tile jb
+  // state: key tiles ib = 0..3 in the result layout (rows = key i =
+  // 16 ib + 4 qd + r, columns = value j = 16 jb + t)
   const int jb = wave, jcol = 16 * jb + t;
   f32x4 S[4];
 #pragma unroll
@@ -274,55 +352,51 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_fwd_chunk_kernel(const FwdChun
   const uint32_t tok_row = (uint32_t)tstride;                       // one step
   const uint32_t tok_off = 4 * qd * tok_row + jcol;                  // row 4 qd, column jcol
   const uint32_t ck_off = 4 * qd * kHead + jcol;
+  const uint32_t yt_off = t * tok_row + 16 * jb + 4 * qd;            // row t, 4 values
 
-  issue(0);
-  for (int n = 0; n < nbatches; ++n) {
-    const int nq = min(kBatch, nchunks - kBatch * n);
-    // this batch's staging loads were followed by the previous batch's stores,
-    // at least 24 per chunk (sa 4, y 4, checkpoint 16); vector memory
-    // operations retire in order, so at most 20 outstanding means the loads
-    // have landed while the stores keep flying
-    if (n == 0) wait_vmcnt<0>();
-    else wait_vmcnt<20>();
-    lds_barrier();
-    if (wave < nq) prepare_chunk(stg, wave, scr[wave], ops[wave], lane);
-    lds_barrier();   // chunk operands visible; staging free
-    if (n + 1 < nbatches) issue(n + 1);
+  for (int cidx = 0; cidx < nchunks; ++cidx) {
+    const int slot = cidx % kSlots;
+    for (int n = 0; n < kSpinLimit && lds_load_flag(&flags.ready[slot]) < cidx; ++n)
+      __builtin_amdgcn_s_sleep(1);
+    lds_acquire();
+    const ChainOps cur = load_chain_ops(ops[slot], jb, lane);
+    // the operand loads have completed before the slot is handed back
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+    lds_release();
+    if (lane == 0) lds_store_flag(&flags.taken[slot][jb], cidx);
 
-    // =========================== phase 2: the state's chain, value tile jb
-    for (int q = 0; q < nq; ++q) {
-      const ChainOps cur = load_chain_ops(ops[q], jb, lane);
-      const int cidx = kBatch * n + q;
-      const Split8 Sx0 = split8(S[0], S[1]), Sx1 = split8(S[2], S[3]);
-      f32x4 sa = mma32x3(cur.w[0], Sx0, cur.u);
-      sa = mma32x3(cur.w[1], Sx1, sa);
-      f32x4 yv = mma32x3(cur.r[0], Sx0, f32x4{0.f, 0.f, 0.f, 0.f});
-      yv = mma32x3(cur.r[1], Sx1, yv);
-      yv = mma_s2(cur.ark, cur.v, yv);
-      const Split4 sas = split4(sa);
-      yv = mma_s3(cur.arb, sas, yv);
+    const Split8 Sx0 = split8(S[0], S[1]), Sx1 = split8(S[2], S[3]);
+    f32x4 sa = mma32x3(cur.w[0], Sx0, cur.u);
+    sa = mma32x3(cur.w[1], Sx1, sa);
+    // Y^T = S0 R^T + V^T A_rk^T + SA^T A_rb^T: the same registers with the
+    // operand roles swapped (a result tile as the A operand is its
+    // transpose), so each lane holds 4 consecutive values of one step
+    f32x4 yt = mma32x3(Sx0, cur.r[0], f32x4{0.f, 0.f, 0.f, 0.f});
+    yt = mma32x3(Sx1, cur.r[1], yt);
+    yt = mma32(twice(cur.v), cur.ark, yt);
+    const Split4 sas = split4(sa);
+    yt = mma32(cat8(sas.lo, bf16x4{0, 0, 0, 0}), cur.arb, yt);
+    yt = mma32(twice(sas.hi), cur.arb, yt);
 #pragma unroll
-      for (int ib = 0; ib < 4; ++ib) {
-        f32x4 s = mma_s2(cur.kt[ib], cur.v, S[ib]);
-        s = mma_s3(cur.bt[ib], sas, s);
-        S[ib] = s * cur.gl[ib];
-      }
-      // outputs: rows = steps 16 cidx + 4 qd + r, column = value jcol
-      const int64_t cbase = tok0 + (int64_t)kL * cidx * tstride;
-      float* const sa_c = p.sa + cbase;
-      bf16_t* const y_c = p.y + cbase;
+    for (int ib = 0; ib < 4; ++ib) {
+      f32x4 st = mma_s2(cur.kt[ib], cur.v, S[ib]);
+      st = mma_s3(cur.bt[ib], sas, st);
+      S[ib] = st * cur.gl[ib];
+    }
+    // outputs: sa rows = steps 16 cidx + 4 qd + r, column = value jcol;
+    // y at step 16 cidx + t, values 16 jb + 4 qd .. + 3 (one 8-byte store)
+    const int64_t cbase = tok0 + (int64_t)kL * cidx * tstride;
+    float* const sa_c = p.sa + cbase;
+    bf16_t* const y_c = p.y + cbase;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        sa_c[tok_off + r * tok_row] = sa[r];
-        y_c[tok_off + r * tok_row] = __builtin_bit_cast(bf16_t, (__bf16)yv[r]);
-      }
-      if ((kL * (cidx + 1)) % p.C == 0) {
-        float* const ck = p.ckpt + (bh * (T / p.C) + kL * (cidx + 1) / p.C - 1) * (kHead * kHead);
+    for (int r = 0; r < 4; ++r) sa_c[tok_off + r * tok_row] = sa[r];
+    *reinterpret_cast<bf16x4*>(y_c + yt_off) = to_bf16x4(yt);
+    if ((kL * (cidx + 1)) % p.C == 0) {
+      float* const ck = p.ckpt + (bh * (T / p.C) + kL * (cidx + 1) / p.C - 1) * (kHead * kHead);
 #pragma unroll
-        for (int ib = 0; ib < 4; ++ib)
+      for (int ib = 0; ib < 4; ++ib)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) ck[ck_off + (16 * ib + r) * kHead] = S[ib][r];
-      }
+        for (int r = 0; r < 4; ++r) ck[ck_off + (16 * ib + r) * kHead] = S[ib][r];
     }
   }
 
