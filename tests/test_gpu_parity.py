@@ -264,6 +264,42 @@ def test_full_size_config1_sampled_heads(wk, oracle):
         assert err < BF16_STATE_TOL, (bi, h, err)
 
 
+def test_full_size_config2_sampled_heads(wk, oracle):
+    # BASELINE config[2] at full size (B=4, T=4096, H=64, the 7B-class layer
+    # width, bf16, zero initial state) on the pretrain operator: two (b, h)
+    # pairs, first and last, against the oracle over all 4096 steps; and the
+    # statepass operator from an all-zero state gives the same outputs and
+    # gradients bit for bit (size-independent: the state loaded is zero).
+    announce("config[2] full size, sampled heads")
+    pkg = load_pkg()
+    B, T, H = 4, 4096, 64
+    t = pkg.synthetic.make_inputs_torch(B, T, H, seed=0x5EED0002, s0_std=None, dtype=torch.bfloat16)
+    ins = [t[n] for n in NAMES]
+    fwd = wk.wkv7_pretrain_forward(wk.Wkv7ForwardInput(
+        receptance=ins[1], weight_decay=ins[0], replacement_key=ins[2], value=ins[3],
+        removal_key_normalized=ins[4], replacement=ins[5]), 16)
+    bwd = wk.wkv7_pretrain_backward(*ins, fwd.state, fwd.removal_state, t["dy"], 16)
+    zero = torch.zeros(B, H, 64, 64, device=ins[0].device)
+    sp_f = wk.wkv7_statepass_forward(*ins, zero, 16)
+    sp_b = wk.wkv7_statepass_backward(*ins, sp_f.state, sp_f.removal_state, t["dy"], zero, 16)
+    torch.cuda.synchronize()
+    assert torch.equal(sp_f.output, fwd.output)
+    assert torch.equal(sp_f.state, fwd.state)
+    for gn in GRAD_NAMES:
+        assert torch.equal(getattr(sp_b, gn), getattr(bwd, gn)), gn
+    for bi, h in ((0, 0), (B - 1, H - 1)):
+        sl = lambda x: to_np(x[bi:bi + 1, :, h:h + 1])
+        ins_np = [sl(x) for x in ins]
+        of = oracle.forward_f32(*ins_np, chunk_len=16)
+        ob = oracle.backward_f32(*ins_np, of["state"], of["removal_state"], sl(t["dy"]), chunk_len=16)
+        assert rel_l2(sl(fwd.output), pkg.synthetic.bf16_round(of["output"])) < BF16_TOL
+        ck = to_np(fwd.state[bi:bi + 1, h:h + 1])
+        assert rel_l2(ck, of["state"]) < BF16_STATE_TOL
+        for gn in GRAD_NAMES:
+            err = rel_l2(sl(getattr(bwd, gn)), pkg.synthetic.bf16_round(ob[gn]))
+            assert err < BF16_TOL, (bi, h, gn, err)
+
+
 @pytest.mark.parametrize("case", [
     (1, 16, 1, None, 31),    # one chunk from a zero state
     (2, 64, 3, 0.1, 32),     # one full batch of four chunks
