@@ -21,7 +21,8 @@
 //   chain waves 0-3 take the chunks in order; wave w owns value columns
 //                   16w..16w+15 of the state (state rows are independent in
 //                   the forward), loads chunk c's operands from slot c % 4,
-//                   marks them taken, and computes SA, Y and the next state.
+//                   computes SA, Y and the next state, and marks the slot
+//                   taken once every operand has been used.
 // A prep wave overwrites its slot only after all four chain waves have taken
 // the chunk in it, so preparing chunk c overlaps the chain of chunks c-4 ..
 // c-1. The hand-over uses two LDS flags per slot and no barriers; every wait
@@ -353,6 +354,15 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_fwd_chunk_kernel(const FwdChun
   const uint32_t tok_off = 4 * qd * tok_row + jcol;                  // row 4 qd, column jcol
   const uint32_t ck_off = 4 * qd * kHead + jcol;
   const uint32_t yt_off = t * tok_row + 16 * jb + 4 * qd;            // row t, 4 values
+  // the checkpoint after chunk c (chunk_len is 16 here: one per chunk),
+  // transposed ([key][value]): rows = keys 16 ib + 4 qd + r, column jcol
+  auto store_ckpt = [&](int c, const f32x4 (&st)[4]) {
+    float* const ck = p.ckpt + (bh * nchunks + c) * (kHead * kHead);
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ck[ck_off + (16 * ib + r) * kHead] = st[ib][r];
+  };
 
   for (int cidx = 0; cidx < nchunks; ++cidx) {
     const int slot = cidx % kSlots;
@@ -360,12 +370,11 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_fwd_chunk_kernel(const FwdChun
       __builtin_amdgcn_s_sleep(1);
     lds_acquire();
     const ChainOps cur = load_chain_ops(ops[slot], jb, lane);
-    // the operand loads have completed before the slot is handed back
-    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
-    lds_release();
-    if (lane == 0) lds_store_flag(&flags.taken[slot][jb], cidx);
 
     const Split8 Sx0 = split8(S[0], S[1]), Sx1 = split8(S[2], S[3]);
+    // the previous chunk's checkpoint (the state this chunk starts from),
+    // stored here so that the stores overlap this chunk's products
+    if (cidx > 0) store_ckpt(cidx - 1, S);
     f32x4 sa = mma32x3(cur.w[0], Sx0, cur.u);
     sa = mma32x3(cur.w[1], Sx1, sa);
     // Y^T = S0 R^T + V^T A_rk^T + SA^T A_rb^T: the same registers with the
@@ -383,6 +392,11 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_fwd_chunk_kernel(const FwdChun
       st = mma_s3(cur.bt[ib], sas, st);
       S[ib] = st * cur.gl[ib];
     }
+    // every operand has been used, so its load has completed (the wait costs
+    // nothing here); the slot goes back to its prep wave
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+    lds_release();
+    if (lane == 0) lds_store_flag(&flags.taken[slot][jb], cidx);
     // outputs: sa rows = steps 16 cidx + 4 qd + r, column = value jcol;
     // y at step 16 cidx + t, values 16 jb + 4 qd .. + 3 (one 8-byte store)
     const int64_t cbase = tok0 + (int64_t)kL * cidx * tstride;
@@ -391,14 +405,8 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_fwd_chunk_kernel(const FwdChun
 #pragma unroll
     for (int r = 0; r < 4; ++r) sa_c[tok_off + r * tok_row] = sa[r];
     *reinterpret_cast<bf16x4*>(y_c + yt_off) = to_bf16x4(yt);
-    if ((kL * (cidx + 1)) % p.C == 0) {
-      float* const ck = p.ckpt + (bh * (T / p.C) + kL * (cidx + 1) / p.C - 1) * (kHead * kHead);
-#pragma unroll
-      for (int ib = 0; ib < 4; ++ib)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) ck[ck_off + (16 * ib + r) * kHead] = S[ib][r];
-    }
   }
+  if (nchunks > 0) store_ckpt(nchunks - 1, S);
 
   if (p.sT) {
 #pragma unroll
