@@ -34,8 +34,8 @@
 //   phase A: gradient waves: state-gradient chain and dV of chunk c; set-up
 //            waves: staging loads, the finished decay gradient of chunk c+1;
 //            all waves: decays and decayed rows of chunk c-1 (keys 8w..8w+7)
-//   phase B: gradient waves: step products of v, dy, sa and with dSA of
-//            chunk c; set-up waves: gradient flush of chunk c+1, staging
+//   phase B: gradient waves: gradient flush of chunk c+1, step products of
+//            v, dy, sa and with dSA of chunk c; set-up waves: staging
 //            stores, step products of the decayed rows of chunk c-1 and
 //            P = (I - A_ab)^-1 (wave 4)
 //   phase C: key-indexed gradients of chunk c, key tile w: dK, dB and their
@@ -310,7 +310,8 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
     }
   };
 
-  // the staged gradient tiles of chunk cc to memory (set-up waves): thread
+  // the staged gradient tiles of chunk cc to memory (gradient waves in the
+  // loop, whose phase B is the shorter one; set-up waves after it): thread
   // utid writes 16-byte pieces p = 256 k + utid (tile p / 128, row (p / 8) %
   // 16); tile 2 k + wq / 2 is wave-uniform, so the destination is picked by
   // scalar selects and stays a global pointer
@@ -480,6 +481,7 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
                   read_tr16(xdsa_at(L.xdsa[hl], 32 * m + 16 + 4 * qd + (t >> 2), t & 3)));
     };
     if (grad) {
+      if (c < last) flush(c + 1);
 #pragma unroll
       for (int r = 0; r < 4; ++r) out_at(outs[O_DV], 4 * qd + r, jcol) = __builtin_bit_cast(bf16_t, (__bf16)dv[r]);
       // step products of v, dy, sa (one per wave), as D = X1 Y1^T + X2 Y2^T:
@@ -530,7 +532,6 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
       for (int r = 0; r < 4; ++r) e[r] = sgn * (4 * qd + r - t) > 0 ? e[r] : 0.f;
       L.frag[G_BSAV + wq][lane] = stack_f(e);
     } else {
-      if (c < last) flush(c + 1);
       if constexpr (kFull) {
         stage_dec(pre);             // decay rows of chunk c - 2 (the decays of phase A are done)
         stage_grad(pre, sb ^ 1);    // gradient rows of chunk c - 1 (free buffer)
