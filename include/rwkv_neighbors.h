@@ -14,6 +14,11 @@
  *   modules/time_mixer/gated_readout.rs:126-145 (GroupNorm over
  *     heads, the r.k~.bonus term, the gate)                          rwkv_gated_readout_forward
  *   its autodiff backward (Burn's autodiff of the same ops)          rwkv_gated_readout_backward
+ *   modules/time_mixer/weight_prepare.rs:282-317 (learning rate,
+ *     replacement key, value residual, decay, normalized removal
+ *     key, replacement), with the LoRA biases of
+ *     layers/lora.rs:118-123                                          rwkv_weight_prepare_forward
+ *   its autodiff backward (Burn's autodiff of the same ops)          rwkv_weight_prepare_backward
  *
  * Token shift + mixes. x ("embedded_context") is [batch, context_len, C]
  * row-major in dtype; for each row b and step t
@@ -127,6 +132,72 @@ int rwkv_gated_readout_backward(const void *wkv7_output, const void *receptance,
                                 float *group_norm_weight_grad,
                                 float *group_norm_bias_grad, void *workspace,
                                 int64_t workspace_bytes, void *stream);
+
+/*
+ * End of the weight preparation. From the key and value projections
+ * ("precursors") and the three LoRA products before their bias
+ * (learning_rate_lora = act(x_a W_a) W_b, likewise weight_decay_lora and
+ * value_residual_lora), all [rows, H * 64] in dtype, and the fp32 [H * 64]
+ * parameters, per row and channel:
+ *   lr                     = sigmoid(learning_rate_lora + learning_rate_bias)
+ *   replacement_key        = key * (key_replacement * (lr - 1) + 1)
+ *   value                  = lerp(value_precursor, value_from_first_cell,
+ *                                 sigmoid(value_residual_lora + value_residual_bias))
+ *   weight_decay           = -softplus(-(weight_decay_lora + weight_decay_bias)) - 0.5
+ *   removal_key_normalized = -u,  u = rk / max(|rk|, 1e-12) over each head's 64
+ *                            channels, rk = key * key_removal
+ *   replacement            = u * lr
+ * written in out_dtype (the WKV7 operand dtype). The value residual is on
+ * when value_residual_bias is not NULL (every cell but the first); then
+ * value_from_first_cell and value_residual_lora are required, otherwise they
+ * must be NULL and value is the precursor. softplus(y) is y above 20.
+ *
+ * The backward takes the five outputs' gradients (out_dtype) and writes the
+ * inputs' gradients (dtype; the residual's only when it is on) and the fp32
+ * parameter gradients, summed over rows in a fixed order (workspace from
+ * rwkv_weight_prepare_workspace_bytes). It recomputes the forward.
+ */
+int64_t rwkv_weight_prepare_workspace_bytes(int64_t rows, int64_t num_heads,
+                                            int64_t head_size);
+
+int rwkv_weight_prepare_forward(const void *key_precursor, const void *value_precursor,
+                                const void *value_from_first_cell,
+                                const void *learning_rate_lora, const void *weight_decay_lora,
+                                const void *value_residual_lora,
+                                const float *learning_rate_bias,
+                                const float *weight_decay_bias,
+                                const float *value_residual_bias,
+                                const float *key_replacement, const float *key_removal,
+                                int64_t rows, int64_t num_heads, int64_t head_size,
+                                int dtype, int out_dtype, void *weight_decay,
+                                void *replacement_key, void *value,
+                                void *removal_key_normalized, void *replacement,
+                                void *stream);
+
+int rwkv_weight_prepare_backward(const void *key_precursor, const void *value_precursor,
+                                 const void *value_from_first_cell,
+                                 const void *learning_rate_lora,
+                                 const void *weight_decay_lora,
+                                 const void *value_residual_lora,
+                                 const float *learning_rate_bias,
+                                 const float *weight_decay_bias,
+                                 const float *value_residual_bias,
+                                 const float *key_replacement, const float *key_removal,
+                                 int64_t rows, int64_t num_heads, int64_t head_size,
+                                 int dtype, int out_dtype, const void *weight_decay_grad,
+                                 const void *replacement_key_grad, const void *value_grad,
+                                 const void *removal_key_normalized_grad,
+                                 const void *replacement_grad, void *key_precursor_grad,
+                                 void *value_precursor_grad,
+                                 void *value_from_first_cell_grad,
+                                 void *learning_rate_lora_grad,
+                                 void *weight_decay_lora_grad,
+                                 void *value_residual_lora_grad,
+                                 float *learning_rate_bias_grad,
+                                 float *weight_decay_bias_grad,
+                                 float *value_residual_bias_grad,
+                                 float *key_replacement_grad, float *key_removal_grad,
+                                 void *workspace, int64_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -35,6 +35,8 @@ EXPORTS = (
     "rwkv_token_shift_mix_workspace_bytes", "rwkv_token_shift_mix_forward",
     "rwkv_token_shift_mix_backward", "rwkv_gated_readout_workspace_bytes",
     "rwkv_gated_readout_forward", "rwkv_gated_readout_backward",
+    "rwkv_weight_prepare_workspace_bytes", "rwkv_weight_prepare_forward",
+    "rwkv_weight_prepare_backward",
 )
 
 _P = ctypes.c_void_p
@@ -64,6 +66,10 @@ _SIGNATURES = {
                                    + [_P] * 2, _INT),
     "rwkv_gated_readout_backward": ([_P] * 8 + [ctypes.c_float] + [_I64] * 3 + [_INT] * 2
                                     + [_P] * 10 + [_I64, _P], _INT),
+    "rwkv_weight_prepare_workspace_bytes": ([_I64] * 3, _I64),
+    "rwkv_weight_prepare_forward": ([_P] * 11 + [_I64] * 3 + [_INT] * 2 + [_P] * 6, _INT),
+    "rwkv_weight_prepare_backward": ([_P] * 11 + [_I64] * 3 + [_INT] * 2 + [_P] * 17
+                                     + [_I64, _P], _INT),
 }
 
 _lib = None

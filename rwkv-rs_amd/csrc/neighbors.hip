@@ -14,6 +14,17 @@
 //   dscale_i = sum_{b,t} g_i diff_t
 // The difference stays in fp32 between the shift and the mixes.
 //
+// Before the operator too -- the element-wise end of the weight preparation
+// (weight_prepare.rs:282-317), from the projections' and LoRAs' products
+// (the LoRA biases added here, layers/lora.rs:118-123):
+//   lr  = sigmoid(lr_lora + lr_bias)
+//   k~  = key * (key_replacement * (lr - 1) + 1)
+//   v   = lerp(value, value_first, sigmoid(vr_lora + vr_bias))   (not cell 0)
+//   w   = -softplus(-(wd_lora + wd_bias)) - 0.5
+//   u   = rk / max(|rk|_head, 1e-12), rk = key * key_removal
+//   a   = -u,  b = u * lr
+// and its backward, which recomputes the forward from the same inputs.
+//
 // After the operator -- the gated readout (gated_readout.rs:110-148):
 //   out = (GroupNorm_h(y) + (sum_n r k bonus_h) v) * gate
 // with one group per head (64 channels, biased variance, eps), and its
@@ -22,7 +33,8 @@
 // All of these move a few bytes per flop: they are HBM-bound element-wise
 // passes. Each thread owns 4 consecutive channels (one 8- or 16-byte access
 // per tensor and row) and walks a short run of rows; the column sums of the
-// backward (scale, weight, bias and bonus gradients) are reduced within a
+// backward (scale, weight, bias, bonus and the weight preparation's
+// per-channel gradients) are reduced within a
 // block, written as one partial per block to a workspace and summed in a
 // fixed order by a second kernel, so results do not depend on scheduling.
 #include <type_traits>
@@ -466,6 +478,190 @@ __global__ __launch_bounds__(256) void readout_backward_kernel(ReadoutArgs a) {
   }
 }
 
+// ------------------------------------------------- weight preparation, end
+constexpr float kNormEps = 1e-12f;       // F.normalize's eps (weight_prepare.rs:313)
+constexpr float kSoftplusLinear = 20.f;  // softplus(y) = y above this, as torch's
+
+__device__ __forceinline__ float sigmoid1(float x) { return 1.f / (1.f + expf(-x)); }
+
+__device__ __forceinline__ float softplus1(float y) {
+  return y > kSoftplusLinear ? y : log1pf(expf(y));
+}
+
+// softplus'(y)
+__device__ __forceinline__ float softplus_slope(float y) {
+  return y > kSoftplusLinear ? 1.f : sigmoid1(y);
+}
+
+// the forward of one row's four channels, kept for the backward
+struct PrepareRow {
+  F4 k;       // key precursor
+  F4 lr;      // learning rate
+  F4 alpha;   // key_replacement * (lr - 1) + 1
+  F4 wd;      // decay LoRA output with its bias
+  F4 u;       // normalized removal key (before the sign)
+  F4 v;       // value after the residual
+  F4 nu;      // value-residual gate (RES)
+  F4 vdiff;   // value_first - value (RES)
+  float den;  // max(|rk|, eps) of the row's head
+  bool clamped;
+};
+
+struct PrepareParams {
+  F4 lr_bias, wd_bias, vr_bias, ka, kk;
+};
+
+template <bool RES>
+__device__ __forceinline__ PrepareParams prepare_params(const PrepareArgs& a, int64_t cc) {
+  PrepareParams q;
+  q.lr_bias = load4<false>(a.lr_bias, cc);
+  q.wd_bias = load4<false>(a.wd_bias, cc);
+  q.vr_bias = RES ? load4<false>(a.vr_bias, cc) : zero4();
+  q.ka = load4<false>(a.key_replacement, cc);
+  q.kk = load4<false>(a.key_removal, cc);
+  return q;
+}
+
+template <bool IB, bool RES>
+__device__ __forceinline__ void prepare_row(const PrepareArgs& a, int64_t idx,
+                                            const PrepareParams& q, PrepareRow& p) {
+  p.k = load4<IB>(a.key, idx);
+  const F4 lr = load4<IB>(a.lr, idx), wd = load4<IB>(a.wd, idx), vp = load4<IB>(a.value, idx);
+  F4 vf = zero4(), vr = zero4();
+  if constexpr (RES) {
+    vf = load4<IB>(a.value_first, idx);
+    vr = load4<IB>(a.vr, idx);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    p.lr.v[j] = sigmoid1(lr.v[j] + q.lr_bias.v[j]);
+    p.alpha.v[j] = q.ka.v[j] * (p.lr.v[j] - 1.f) + 1.f;
+    p.wd.v[j] = wd.v[j] + q.wd_bias.v[j];
+    p.u.v[j] = p.k.v[j] * q.kk.v[j];
+    ss += p.u.v[j] * p.u.v[j];
+    if constexpr (RES) {
+      p.nu.v[j] = sigmoid1(vr.v[j] + q.vr_bias.v[j]);
+      p.vdiff.v[j] = vf.v[j] - vp.v[j];
+      p.v.v[j] = vp.v[j] + p.vdiff.v[j] * p.nu.v[j];
+    } else {
+      p.v.v[j] = vp.v[j];
+    }
+  }
+  const float n = sqrtf(sum16(ss));
+  p.clamped = !(n >= kNormEps);  // x / clamp_min(|x|, eps); no gradient through a clamped norm
+  p.den = p.clamped ? kNormEps : n;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) p.u.v[j] = p.u.v[j] / p.den;
+}
+
+template <bool IB, bool OB, bool RES>
+__global__ __launch_bounds__(256) void prepare_forward_kernel(PrepareArgs a) {
+  const int grp = threadIdx.x >> 4, l = threadIdx.x & 15;
+  const int64_t C = a.H * 64;
+  const int64_t cc = static_cast<int64_t>(blockIdx.y) * 64 + l * 4;
+  const PrepareParams q = prepare_params<RES>(a, cc);
+  const int64_t r0 = (static_cast<int64_t>(blockIdx.x) * 16 + grp) * kPrepareRowsPerGroup;
+  for (int i = 0; i < kPrepareRowsPerGroup; ++i) {
+    const int64_t row = r0 + i;
+    if (row >= a.rows) break;  // uniform over the 16 lanes of the group
+    const int64_t idx = row * C + cc;
+    PrepareRow p;
+    prepare_row<IB, RES>(a, idx, q, p);
+    F4 w, kt, na, b;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      w.v[j] = -softplus1(-p.wd.v[j]) - 0.5f;
+      kt.v[j] = p.k.v[j] * p.alpha.v[j];
+      na.v[j] = -p.u.v[j];
+      b.v[j] = p.u.v[j] * p.lr.v[j];
+    }
+    store4<OB>(a.weight_decay, idx, w);
+    store4<OB>(a.replacement_key, idx, kt);
+    store4<OB>(a.value_out, idx, p.v);
+    store4<OB>(a.removal, idx, na);
+    store4<OB>(a.replacement, idx, b);
+  }
+}
+
+template <bool IB, bool OB, bool RES>
+__global__ __launch_bounds__(256) void prepare_backward_kernel(PrepareArgs a) {
+  constexpr int Q = RES ? kPrepareSums : kPrepareSums - 1;
+  __shared__ float red[16][kPrepareSums][64];
+  const int grp = threadIdx.x >> 4, l = threadIdx.x & 15;
+  const int64_t C = a.H * 64;
+  const int64_t cc = static_cast<int64_t>(blockIdx.y) * 64 + l * 4;
+  const PrepareParams q = prepare_params<RES>(a, cc);
+  F4 acc[kPrepareSums];
+#pragma unroll
+  for (int s = 0; s < kPrepareSums; ++s) acc[s] = zero4();
+  const int64_t r0 = (static_cast<int64_t>(blockIdx.x) * 16 + grp) * kPrepareRowsPerGroup;
+  for (int i = 0; i < kPrepareRowsPerGroup; ++i) {
+    const int64_t row = r0 + i;
+    if (row >= a.rows) break;  // uniform over the 16 lanes of the group
+    const int64_t idx = row * C + cc;
+    PrepareRow p;
+    prepare_row<IB, RES>(a, idx, q, p);
+    const F4 gw = load4<OB>(a.weight_decay_grad, idx), gkt = load4<OB>(a.replacement_key_grad, idx);
+    const F4 gv = load4<OB>(a.value_out_grad, idx), ga = load4<OB>(a.removal_grad, idx);
+    const F4 gb = load4<OB>(a.replacement_grad, idx);
+    // a = -u and b = u lr: the gradient reaching u, and u . du over the head
+    F4 du;
+    float dot = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      du.v[j] = gb.v[j] * p.lr.v[j] - ga.v[j];
+      dot += p.u.v[j] * du.v[j];
+    }
+    dot = sum16(dot);
+    F4 dk, dlr, dwd, dvp, dvf, dvr;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      // u = rk / den: d rk = (du - u (u . du)) / |rk|, or du / eps when clamped
+      const float drk = p.clamped ? du.v[j] / kNormEps : (du.v[j] - p.u.v[j] * dot) / p.den;
+      const float dalpha = gkt.v[j] * p.k.v[j];
+      const float glr = gb.v[j] * p.u.v[j] + dalpha * q.ka.v[j];
+      dlr.v[j] = glr * p.lr.v[j] * (1.f - p.lr.v[j]);
+      dk.v[j] = gkt.v[j] * p.alpha.v[j] + drk * q.kk.v[j];
+      dwd.v[j] = gw.v[j] * softplus_slope(-p.wd.v[j]);
+      acc[PS_LR_BIAS].v[j] += dlr.v[j];
+      acc[PS_WD_BIAS].v[j] += dwd.v[j];
+      acc[PS_KEY_REPLACEMENT].v[j] += dalpha * (p.lr.v[j] - 1.f);
+      acc[PS_KEY_REMOVAL].v[j] += drk * p.k.v[j];
+      if constexpr (RES) {
+        const float nu = p.nu.v[j];
+        dvp.v[j] = gv.v[j] * (1.f - nu);
+        dvf.v[j] = gv.v[j] * nu;
+        dvr.v[j] = gv.v[j] * p.vdiff.v[j] * nu * (1.f - nu);
+        acc[PS_VR_BIAS].v[j] += dvr.v[j];
+      } else {
+        dvp.v[j] = gv.v[j];
+      }
+    }
+    store4<IB>(a.key_grad, idx, dk);
+    store4<IB>(a.value_grad, idx, dvp);
+    store4<IB>(a.lr_grad, idx, dlr);
+    store4<IB>(a.wd_grad, idx, dwd);
+    if constexpr (RES) {
+      store4<IB>(a.value_first_grad, idx, dvf);
+      store4<IB>(a.vr_grad, idx, dvr);
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < Q; ++s)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) red[grp][s][l * 4 + j] = acc[s].v[j];
+  __syncthreads();
+  // Q * 64 partials over the block's 256 threads
+  for (int e = threadIdx.x; e < Q * 64; e += 256) {
+    const int s = e >> 6, n = e & 63;
+    float t = 0.f;
+    for (int g = 0; g < 16; ++g) t += red[g][s][n];
+    a.workspace[(static_cast<int64_t>(blockIdx.x) * Q + s) * C +
+                static_cast<int64_t>(blockIdx.y) * 64 + n] = t;
+  }
+}
+
 template <typename K>
 hipError_t launch(K kernel, dim3 grid, dim3 block, hipStream_t s) {
   hipLaunchKernelGGL(kernel, grid, block, 0, s);
@@ -606,6 +802,56 @@ hipError_t launch_readout_backward(const ReadoutArgs& a, hipStream_t s) {
                    : launch(readout_backward_kernel<false, false>, grid, dim3(256), s, a);
   if (e != hipSuccess) return e;
   return column_sum(a.workspace, rb, kReadoutSums, C, outs, s);
+}
+
+namespace {
+
+// one instantiation per (input dtype, output dtype, residual or not)
+template <template <bool, bool, bool> class Kern>
+hipError_t dispatch_prepare(const PrepareArgs& a, dim3 grid, hipStream_t s) {
+  auto go = [&](auto ib, auto ob) -> hipError_t {
+    constexpr bool IB = decltype(ib)::value, OB = decltype(ob)::value;
+    return a.residual ? launch(Kern<IB, OB, true>::fn, grid, dim3(256), s, a)
+                         : launch(Kern<IB, OB, false>::fn, grid, dim3(256), s, a);
+  };
+  using T = std::true_type;
+  using F = std::false_type;
+  if (a.in_bf16) return a.out_bf16 ? go(T{}, T{}) : go(T{}, F{});
+  return a.out_bf16 ? go(F{}, T{}) : go(F{}, F{});
+}
+
+template <bool IB, bool OB, bool RES>
+struct PrepareForward {
+  static constexpr auto fn = prepare_forward_kernel<IB, OB, RES>;
+};
+template <bool IB, bool OB, bool RES>
+struct PrepareBackward {
+  static constexpr auto fn = prepare_backward_kernel<IB, OB, RES>;
+};
+
+}  // namespace
+
+hipError_t launch_prepare_forward(const PrepareArgs& a, hipStream_t s) {
+  if (a.rows == 0) return hipSuccess;
+  const dim3 grid(static_cast<unsigned>(prepare_row_blocks(a.rows)), static_cast<unsigned>(a.H));
+  return dispatch_prepare<PrepareForward>(a, grid, s);
+}
+
+hipError_t launch_prepare_backward(const PrepareArgs& a, hipStream_t s) {
+  const int64_t C = a.H * 64;
+  const int q = a.residual ? kPrepareSums : kPrepareSums - 1;
+  if (a.rows == 0) {
+    for (int i = 0; i < q; ++i) {
+      const hipError_t e = fill_zero(a.sums[i], C, s);
+      if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+  }
+  const int64_t rb = prepare_row_blocks(a.rows);
+  const hipError_t e =
+      dispatch_prepare<PrepareBackward>(a, dim3(static_cast<unsigned>(rb), static_cast<unsigned>(a.H)), s);
+  if (e != hipSuccess) return e;
+  return column_sum(a.workspace, rb, q, C, a.sums, s);
 }
 
 }  // namespace rwkv_nb

@@ -88,6 +88,57 @@ int check_readout(const void* y, const void* r, const void* k, const void* v, co
   return WKV7_OK;
 }
 
+// shared shape and pointer checks of the weight preparation's end; the
+// value residual is on exactly when its bias is given
+int check_prepare(const void* key, const void* value, const void* value_first, const void* lr,
+                  const void* wd, const void* vr, const float* lr_bias, const float* wd_bias,
+                  const float* vr_bias, const float* ka, const float* kk, int64_t rows, int64_t H,
+                  int64_t N, int dtype, int out_dtype) {
+  if (!valid_dtype(dtype) || !valid_dtype(out_dtype)) return WKV7_ERR_DTYPE;
+  if (N != 64) return WKV7_ERR_HEAD_SIZE;
+  if (rows < 0 || H <= 0 || H > kMaxGridY) return WKV7_ERR_SHAPE;
+  if (rwkv_nb::prepare_row_blocks(rows) > kMaxGridX) return WKV7_ERR_SHAPE;
+  if (!lr_bias || !wd_bias || !ka || !kk) return WKV7_ERR_NULL_POINTER;
+  const bool res = vr_bias != nullptr;
+  if (!res && (value_first || vr)) return WKV7_ERR_SHAPE;  // a residual input without its bias
+  if (rows > 0 && (!key || !value || !lr || !wd || (res && (!value_first || !vr))))
+    return WKV7_ERR_NULL_POINTER;
+  for (const void* p : {key, value, value_first, lr, wd, vr})
+    if (p && !aligned_for(p, dtype)) return WKV7_ERR_ALIGNMENT;
+  for (const float* p : {lr_bias, wd_bias, vr_bias, ka, kk})
+    if (p && !aligned_for(p, WKV7_DTYPE_F32)) return WKV7_ERR_ALIGNMENT;
+  return WKV7_OK;
+}
+
+int64_t prepare_workspace(int64_t rows, int64_t H) {
+  return rwkv_nb::prepare_row_blocks(rows) * rwkv_nb::kPrepareSums * H * 64 * 4;
+}
+
+rwkv_nb::PrepareArgs prepare_args(const void* key, const void* value, const void* value_first,
+                                  const void* lr, const void* wd, const void* vr,
+                                  const float* lr_bias, const float* wd_bias,
+                                  const float* vr_bias, const float* ka, const float* kk,
+                                  int64_t rows, int64_t H, int dtype, int out_dtype) {
+  rwkv_nb::PrepareArgs a{};
+  a.key = key;
+  a.value = value;
+  a.value_first = value_first;
+  a.lr = lr;
+  a.wd = wd;
+  a.vr = vr;
+  a.lr_bias = lr_bias;
+  a.wd_bias = wd_bias;
+  a.vr_bias = vr_bias;
+  a.key_replacement = ka;
+  a.key_removal = kk;
+  a.rows = rows;
+  a.H = H;
+  a.in_bf16 = dtype == WKV7_DTYPE_BF16;
+  a.out_bf16 = out_dtype == WKV7_DTYPE_BF16;
+  a.residual = vr_bias != nullptr;
+  return a;
+}
+
 int64_t readout_workspace(int64_t rows, int64_t H) {
   return rwkv_nb::readout_row_blocks(rows) * rwkv_nb::kReadoutSums * H * 64 * 4;
 }
@@ -344,6 +395,133 @@ int rwkv_gated_readout_backward(const void* wkv7_output, const void* receptance,
   a.bias_grad = group_norm_bias_grad;
   a.workspace = static_cast<float*>(workspace);
   return wkv7::hip_status(rwkv_nb::launch_readout_backward(a, static_cast<hipStream_t>(stream)));
+}
+
+int64_t rwkv_weight_prepare_workspace_bytes(int64_t rows, int64_t num_heads, int64_t head_size) {
+  if (rows < 0 || num_heads <= 0 || num_heads > kMaxGridY || head_size != 64) return -1;
+  return prepare_workspace(rows, num_heads);
+}
+
+int rwkv_weight_prepare_forward(const void* key_precursor, const void* value_precursor,
+                                const void* value_from_first_cell, const void* learning_rate_lora,
+                                const void* weight_decay_lora, const void* value_residual_lora,
+                                const float* learning_rate_bias, const float* weight_decay_bias,
+                                const float* value_residual_bias, const float* key_replacement,
+                                const float* key_removal, int64_t rows, int64_t num_heads,
+                                int64_t head_size, int dtype, int out_dtype, void* weight_decay,
+                                void* replacement_key, void* value, void* removal_key_normalized,
+                                void* replacement, void* stream) {
+  if (int rc = check_prepare(key_precursor, value_precursor, value_from_first_cell,
+                             learning_rate_lora, weight_decay_lora, value_residual_lora,
+                             learning_rate_bias, weight_decay_bias, value_residual_bias,
+                             key_replacement, key_removal, rows, num_heads, head_size, dtype,
+                             out_dtype))
+    return rc;
+  void* outs[] = {weight_decay, replacement_key, value, removal_key_normalized, replacement};
+  for (void* p : outs) {
+    if (rows > 0 && !p) return WKV7_ERR_NULL_POINTER;
+    if (p && !aligned_for(p, out_dtype)) return WKV7_ERR_ALIGNMENT;
+  }
+  const int64_t C = num_heads * 64, in = rows * C * esize(dtype), out = rows * C * esize(out_dtype);
+  std::vector<Range> o, i;
+  for (void* p : outs) o.push_back({p, out});
+  for (const void* p : {key_precursor, value_precursor, value_from_first_cell, learning_rate_lora,
+                        weight_decay_lora, value_residual_lora})
+    i.push_back({p, in});
+  for (const float* p : {learning_rate_bias, weight_decay_bias, value_residual_bias,
+                         key_replacement, key_removal})
+    i.push_back({p, C * 4});
+  if (any_overlap(o, i)) return WKV7_ERR_OVERLAP;
+  rwkv_nb::PrepareArgs a = prepare_args(
+      key_precursor, value_precursor, value_from_first_cell, learning_rate_lora,
+      weight_decay_lora, value_residual_lora, learning_rate_bias, weight_decay_bias,
+      value_residual_bias, key_replacement, key_removal, rows, num_heads, dtype, out_dtype);
+  a.weight_decay = weight_decay;
+  a.replacement_key = replacement_key;
+  a.value_out = value;
+  a.removal = removal_key_normalized;
+  a.replacement = replacement;
+  return wkv7::hip_status(rwkv_nb::launch_prepare_forward(a, static_cast<hipStream_t>(stream)));
+}
+
+int rwkv_weight_prepare_backward(
+    const void* key_precursor, const void* value_precursor, const void* value_from_first_cell,
+    const void* learning_rate_lora, const void* weight_decay_lora,
+    const void* value_residual_lora, const float* learning_rate_bias,
+    const float* weight_decay_bias, const float* value_residual_bias,
+    const float* key_replacement, const float* key_removal, int64_t rows, int64_t num_heads,
+    int64_t head_size, int dtype, int out_dtype, const void* weight_decay_grad,
+    const void* replacement_key_grad, const void* value_grad,
+    const void* removal_key_normalized_grad, const void* replacement_grad,
+    void* key_precursor_grad, void* value_precursor_grad, void* value_from_first_cell_grad,
+    void* learning_rate_lora_grad, void* weight_decay_lora_grad, void* value_residual_lora_grad,
+    float* learning_rate_bias_grad, float* weight_decay_bias_grad,
+    float* value_residual_bias_grad, float* key_replacement_grad, float* key_removal_grad,
+    void* workspace, int64_t workspace_bytes, void* stream) {
+  if (int rc = check_prepare(key_precursor, value_precursor, value_from_first_cell,
+                             learning_rate_lora, weight_decay_lora, value_residual_lora,
+                             learning_rate_bias, weight_decay_bias, value_residual_bias,
+                             key_replacement, key_removal, rows, num_heads, head_size, dtype,
+                             out_dtype))
+    return rc;
+  const bool res = value_residual_bias != nullptr;
+  if (!learning_rate_bias_grad || !weight_decay_bias_grad || !key_replacement_grad ||
+      !key_removal_grad || (res && !value_residual_bias_grad))
+    return WKV7_ERR_NULL_POINTER;
+  if (!res && (value_from_first_cell_grad || value_residual_lora_grad || value_residual_bias_grad))
+    return WKV7_ERR_SHAPE;
+  const void* grads_in[] = {weight_decay_grad, replacement_key_grad, value_grad,
+                            removal_key_normalized_grad, replacement_grad};
+  void* grads_out[] = {key_precursor_grad,    value_precursor_grad,   learning_rate_lora_grad,
+                       weight_decay_lora_grad, value_from_first_cell_grad, value_residual_lora_grad};
+  if (rows > 0) {
+    for (const void* p : grads_in)
+      if (!p) return WKV7_ERR_NULL_POINTER;
+    for (int k = 0; k < (res ? 6 : 4); ++k)
+      if (!grads_out[k]) return WKV7_ERR_NULL_POINTER;
+  }
+  const int64_t need = prepare_workspace(rows, num_heads);
+  if (need > 0 && (!workspace || workspace_bytes < need)) return WKV7_ERR_SHAPE;
+  for (const void* p : grads_in)
+    if (p && !aligned_for(p, out_dtype)) return WKV7_ERR_ALIGNMENT;
+  for (const void* p : grads_out)
+    if (p && !aligned_for(p, dtype)) return WKV7_ERR_ALIGNMENT;
+  float* sums[] = {learning_rate_bias_grad, weight_decay_bias_grad, key_replacement_grad,
+                   key_removal_grad, value_residual_bias_grad};
+  for (const float* p : sums)
+    if (p && !aligned_for(p, WKV7_DTYPE_F32)) return WKV7_ERR_ALIGNMENT;
+  if (workspace && !aligned_for(workspace, WKV7_DTYPE_F32)) return WKV7_ERR_ALIGNMENT;
+  const int64_t C = num_heads * 64, in = rows * C * esize(dtype), out = rows * C * esize(out_dtype);
+  std::vector<Range> o, i;
+  for (void* p : grads_out) o.push_back({p, in});
+  for (float* p : sums) o.push_back({p, C * 4});
+  o.push_back({workspace, need});
+  for (const void* p : {key_precursor, value_precursor, value_from_first_cell, learning_rate_lora,
+                        weight_decay_lora, value_residual_lora})
+    i.push_back({p, in});
+  for (const float* p : {learning_rate_bias, weight_decay_bias, value_residual_bias,
+                         key_replacement, key_removal})
+    i.push_back({p, C * 4});
+  for (const void* p : grads_in) i.push_back({p, out});
+  if (any_overlap(o, i)) return WKV7_ERR_OVERLAP;
+  rwkv_nb::PrepareArgs a = prepare_args(
+      key_precursor, value_precursor, value_from_first_cell, learning_rate_lora,
+      weight_decay_lora, value_residual_lora, learning_rate_bias, weight_decay_bias,
+      value_residual_bias, key_replacement, key_removal, rows, num_heads, dtype, out_dtype);
+  a.weight_decay_grad = weight_decay_grad;
+  a.replacement_key_grad = replacement_key_grad;
+  a.value_out_grad = value_grad;
+  a.removal_grad = removal_key_normalized_grad;
+  a.replacement_grad = replacement_grad;
+  a.key_grad = key_precursor_grad;
+  a.value_grad = value_precursor_grad;
+  a.value_first_grad = value_from_first_cell_grad;
+  a.lr_grad = learning_rate_lora_grad;
+  a.wd_grad = weight_decay_lora_grad;
+  a.vr_grad = value_residual_lora_grad;
+  for (int k = 0; k < rwkv_nb::kPrepareSums; ++k) a.sums[k] = sums[k];
+  a.workspace = static_cast<float*>(workspace);
+  return wkv7::hip_status(rwkv_nb::launch_prepare_backward(a, static_cast<hipStream_t>(stream)));
 }
 
 }  // extern "C"

@@ -1,6 +1,7 @@
 // Launchers of the kernels that neighbour the WKV7 operator in a time mixer:
-// the token shift with its channel mixes before it, and the gated readout
-// (GroupNorm, bonus, gate) after it. The C ABI (neighbors_api.cpp) checks
+// the token shift with its channel mixes and the element-wise end of the
+// weight preparation before it, and the gated readout (GroupNorm, bonus,
+// gate) after it. The C ABI (neighbors_api.cpp) checks
 // every argument before it calls these.
 #pragma once
 
@@ -17,6 +18,13 @@ constexpr int kMixColsPerBlock = 256;  // 64 lanes x 4 channels
 constexpr int kReadoutRowsPerGroup = 4;  // rows one 16-lane group walks
 constexpr int kReadoutRowsPerBlock = 16 * kReadoutRowsPerGroup;
 constexpr int kReadoutSums = 3;     // group-norm weight, bias, bonus
+constexpr int kPrepareRowsPerGroup = 4;  // rows one 16-lane group walks
+constexpr int kPrepareRowsPerBlock = 16 * kPrepareRowsPerGroup;
+// column sums of the weight-preparation backward, in workspace order: the
+// learning-rate, decay and value-residual LoRA biases, key replacement and
+// key removal (the value-residual slot only when the cell has one)
+enum { PS_LR_BIAS, PS_WD_BIAS, PS_KEY_REPLACEMENT, PS_KEY_REMOVAL, PS_VR_BIAS, kPrepareSums };
+static_assert(kPrepareSums <= kMaxMixes, "one column-sum launch serves at most kMaxMixes sums");
 
 struct ShiftMixArgs {
   const void* x;             // [rows, C] (rows = batch * T), dtype x_bf16
@@ -55,16 +63,41 @@ struct ReadoutArgs {
   float* workspace;           // backward: [row_blocks, 3, H * 64]
 };
 
+struct PrepareArgs {
+  const void *key, *value;    // [rows, H * 64] precursors, input dtype
+  const void* value_first;    // [rows, H * 64] or null (the first cell: no residual)
+  const void *lr, *wd;        // LoRA products before their bias, input dtype
+  const void* vr;             // the value-residual LoRA product; null iff value_first is
+  const float *lr_bias, *wd_bias, *vr_bias;          // [H * 64]; vr_bias null iff vr is
+  const float *key_replacement, *key_removal;        // [H * 64]
+  int64_t rows, H;
+  bool in_bf16, out_bf16;
+  bool residual;              // the cell has a value residual (vr_bias set; every cell but the first)
+  // forward outputs / backward output gradients, [rows, H * 64], out dtype
+  void *weight_decay, *replacement_key, *value_out, *removal, *replacement;
+  const void *weight_decay_grad, *replacement_key_grad, *value_out_grad, *removal_grad,
+      *replacement_grad;
+  // backward: input gradients (input dtype) and parameter gradients
+  void *key_grad, *value_grad, *value_first_grad, *lr_grad, *wd_grad, *vr_grad;
+  float* sums[kPrepareSums];  // [H * 64] each, in the order above
+  float* workspace;           // [row_blocks, sums used, H * 64]
+};
+
 inline int64_t mix_row_blocks(int64_t rows) {
   return (rows + kMixRowsPerBlock - 1) / kMixRowsPerBlock;
 }
 inline int64_t readout_row_blocks(int64_t rows) {
   return (rows + kReadoutRowsPerBlock - 1) / kReadoutRowsPerBlock;
 }
+inline int64_t prepare_row_blocks(int64_t rows) {
+  return (rows + kPrepareRowsPerBlock - 1) / kPrepareRowsPerBlock;
+}
 
 hipError_t launch_shift_mix_forward(const ShiftMixArgs& a, hipStream_t s);
 hipError_t launch_shift_mix_backward(const ShiftMixArgs& a, hipStream_t s);
 hipError_t launch_readout_forward(const ReadoutArgs& a, hipStream_t s);
 hipError_t launch_readout_backward(const ReadoutArgs& a, hipStream_t s);
+hipError_t launch_prepare_forward(const PrepareArgs& a, hipStream_t s);
+hipError_t launch_prepare_backward(const PrepareArgs& a, hipStream_t s);
 
 }  // namespace rwkv_nb

@@ -209,13 +209,17 @@ class LoRA(nn.Module):
         self.bias = _param(1, 1, embedded_dim) if has_bias else None
         self.activation = activation
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
+    def product(self, x: torch.Tensor) -> torch.Tensor:
+        """``act(x @ w_a) @ w_b``: the LoRA without its bias."""
         h = x @ self.w_a
         if self.activation == "sigmoid":
             h = torch.sigmoid(h)
         elif self.activation == "tanh":
             h = torch.tanh(h)
-        h = h @ self.w_b
+        return h @ self.w_b
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        h = self.product(x)
         return h + self.bias if self.bias is not None else h
 
 
@@ -270,12 +274,15 @@ class WeightPrepare(nn.Module):
         self.neighbor_ops = _check_neighbor_ops(neighbor_ops)
 
     def forward(self, embedded_context, value_from_first_cell, embedded_token_shift=None,
-                context_mask=None, gate_scale: Optional[torch.Tensor] = None
-                ) -> WeightPrepareOutput:
+                context_mask=None, gate_scale: Optional[torch.Tensor] = None,
+                operand_dtype: Optional[torch.dtype] = None) -> WeightPrepareOutput:
         """weight_prepare.rs:210-330. With the HIP neighbour ops the token shift
         and the five mixes are one kernel, which also forms the readout gate's
         mix x + diff * ``gate_scale`` (gated_readout.rs:122) when it is given;
-        the difference itself is then not materialised."""
+        the difference itself is then not materialised. Everything after the
+        projections and the LoRA products is a second kernel, which writes
+        the five WKV7 operands it forms in ``operand_dtype`` (default: the
+        products' dtype)."""
         B, T, C = embedded_context.shape
         scales = [self.param_receptance, self.param_weight_decay, self.param_key,
                   self.param_value, self.param_learning_rate]
@@ -300,6 +307,21 @@ class WeightPrepare(nn.Module):
         value_precursor = self.projection_value(xv)
         if self.cell_id == 0:
             value_from_first_cell = value_precursor
+        if self.neighbor_ops == "hip":
+            first = self.cell_id == 0
+            vr_lora = self.param_value_residual_lora
+            weight_decay, replacement_key, value, removal_key_normalized, replacement = \
+                _nb.weight_prepare_end(
+                    key_precursor, value_precursor, None if first else value_from_first_cell,
+                    self.param_learning_rate_lora.product(xa),
+                    self.param_weight_decay_lora.product(xw),
+                    None if first else vr_lora.product(xv),
+                    self.param_learning_rate_lora.bias, self.param_weight_decay_lora.bias,
+                    None if first else vr_lora.bias, self.param_key_replacement,
+                    self.param_key_removal, self.num_heads, operand_dtype)
+            return WeightPrepareOutput(diff, next_shift, value_from_first_cell, receptance,
+                                       weight_decay, replacement_key, value,
+                                       removal_key_normalized, replacement, gate_input)
         learning_rate = torch.sigmoid(self.param_learning_rate_lora(xa))
         alpha_modulated = self.param_key_replacement * (learning_rate - 1.0) + 1.0
         replacement_key = key_precursor * alpha_modulated
@@ -392,7 +414,8 @@ class TimeMixer(nn.Module):
         x = apply_context_mask(io.embedded_context, io.context_mask)
         v_first = apply_context_mask(io.value_from_first_cell, io.context_mask)
         gate_scale = self.gated_readout.param_gate if self.neighbor_ops == "hip" else None
-        wp = self.weight_prepare(x, v_first, io.embedded_token_shift, io.context_mask, gate_scale)
+        wp = self.weight_prepare(x, v_first, io.embedded_token_shift, io.context_mask, gate_scale,
+                                 self.wkv7_dtype)
         shape = (B, T, self.num_heads, self.head_size)
         wkv_in = wp.reshape_to_wkv7_input(shape, self.wkv7_dtype)
         out = kernel.forward(wkv_in, io.state, io.batch_ids, io.elapsed_t, CHUNK_LEN,

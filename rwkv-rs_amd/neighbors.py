@@ -8,6 +8,10 @@ kernels of include/rwkv_neighbors.h, as torch autograd Functions.
   28-58). ``WeightPrepare`` takes five mixes of one shift and the gated
   readout's gate input is a sixth (gated_readout.rs:122); ``ChannelMixer``
   takes one (channel_mixer/mod.rs:96-106).
+* ``weight_prepare_end`` -- the element-wise end of ``WeightPrepare``: the
+  learning rate, replacement key, value residual, decay, normalized removal
+  key and replacement from the projections and the LoRA products, with the
+  LoRA biases (weight_prepare.rs:282-317, layers/lora.rs:118-123), fused.
 * ``gated_readout`` -- GroupNorm over heads, the r.k~.bonus term and the gate
   (gated_readout.rs:126-145), fused; the output projection stays a GEMM.
 
@@ -210,3 +214,94 @@ def gated_readout(wkv7_output: torch.Tensor, receptance: torch.Tensor,
     if bonus.shape != (H, N) or w.shape != (H * N,) or b.shape != (H * N,):
         raise ValueError("parameter shapes must be [H, 64], [H * 64], [H * 64]")
     return _GatedReadout.apply(y, r, k, v, g, bonus, w, b, eps)
+
+
+class _WeightPrepareEnd(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, key, value, value_first, lr, wd, vr, lr_bias, wd_bias, vr_bias,
+                key_replacement, key_removal, num_heads, out_dtype):
+        B, T, C = key.shape
+        outs = [torch.empty((B, T, C), dtype=out_dtype, device=key.device) for _ in range(5)]
+        _native.call("rwkv_weight_prepare_forward", _ptr(key), _ptr(value), _ptr(value_first),
+                     _ptr(lr), _ptr(wd), _ptr(vr), _ptr(lr_bias), _ptr(wd_bias), _ptr(vr_bias),
+                     _ptr(key_replacement), _ptr(key_removal), B * T, num_heads, C // num_heads,
+                     _code(key.dtype), _code(out_dtype), *[_ptr(t) for t in outs],
+                     _stream(key.device))
+        ctx.save_for_backward(key, value, value_first, lr, wd, vr, lr_bias, wd_bias, vr_bias,
+                              key_replacement, key_removal)
+        ctx.num_heads, ctx.out_dtype = num_heads, out_dtype
+        return tuple(outs)
+
+    @staticmethod
+    def backward(ctx, *grads):
+        key, value, value_first, lr, wd, vr, lr_bias, wd_bias, vr_bias, ka, kk = ctx.saved_tensors
+        B, T, C = key.shape
+        H = ctx.num_heads
+        dev = key.device
+        g = [torch.zeros((B, T, C), dtype=ctx.out_dtype, device=dev) if d is None
+             else d.to(ctx.out_dtype).contiguous() for d in grads]
+        res = vr_bias is not None
+        dkey, dvalue, dlr, dwd = (torch.empty_like(t) for t in (key, value, lr, wd))
+        dvf = torch.empty_like(value_first) if res else None
+        dvr = torch.empty_like(vr) if res else None
+        dlr_b, dwd_b, dka, dkk = (torch.empty_like(t) for t in (lr_bias, wd_bias, ka, kk))
+        dvr_b = torch.empty_like(vr_bias) if res else None
+        nbytes = _native.lib().rwkv_weight_prepare_workspace_bytes(B * T, H, C // H)
+        ws = torch.empty(max(nbytes // 4, 1), dtype=torch.float32, device=dev)
+        _native.call("rwkv_weight_prepare_backward", _ptr(key), _ptr(value), _ptr(value_first),
+                     _ptr(lr), _ptr(wd), _ptr(vr), _ptr(lr_bias), _ptr(wd_bias), _ptr(vr_bias),
+                     _ptr(ka), _ptr(kk), B * T, H, C // H, _code(key.dtype),
+                     _code(ctx.out_dtype), *[_ptr(t) for t in g], _ptr(dkey), _ptr(dvalue),
+                     _ptr(dvf), _ptr(dlr), _ptr(dwd), _ptr(dvr), _ptr(dlr_b), _ptr(dwd_b),
+                     _ptr(dvr_b), _ptr(dka), _ptr(dkk), _ptr(ws), nbytes, _stream(dev))
+        return (dkey, dvalue, dvf, dlr, dwd, dvr, dlr_b, dwd_b, dvr_b, dka, dkk, None, None)
+
+
+def weight_prepare_end(key_precursor: torch.Tensor, value_precursor: torch.Tensor,
+                       value_from_first_cell: Optional[torch.Tensor],
+                       learning_rate_lora: torch.Tensor, weight_decay_lora: torch.Tensor,
+                       value_residual_lora: Optional[torch.Tensor],
+                       learning_rate_bias: torch.Tensor, weight_decay_bias: torch.Tensor,
+                       value_residual_bias: Optional[torch.Tensor],
+                       key_replacement: torch.Tensor, key_removal: torch.Tensor,
+                       num_heads: int, out_dtype: Optional[torch.dtype] = None):
+    """The tail of WeightPrepare::forward (weight_prepare.rs:282-317) on one
+    kernel: returns ``(weight_decay, replacement_key, value,
+    removal_key_normalized, replacement)`` as [B, T, C] in ``out_dtype``
+    (default: the inputs' dtype).
+
+    The [B, T, C] inputs share one dtype: the key and value projections and
+    the three LoRA products before their bias (``LoRA.product``). The biases
+    and ``key_replacement`` / ``key_removal`` are fp32 with C elements (any
+    shape). The value residual (``value_from_first_cell``,
+    ``value_residual_lora`` and its bias) is given for every cell but the
+    first, or not at all."""
+    key = _gpu(key_precursor, "key_precursor")
+    if key.dim() != 3:
+        raise ValueError("key_precursor must be [B, T, C]")
+    B, T, C = key.shape
+    if num_heads <= 0 or C != num_heads * 64:
+        raise ValueError("C must be num_heads * 64")
+    res = (value_from_first_cell, value_residual_lora, value_residual_bias)
+    if any(t is None for t in res) and not all(t is None for t in res):
+        raise ValueError("the value residual needs value_from_first_cell, value_residual_lora "
+                         "and value_residual_bias together")
+    acts = [key] + [None if t is None else _gpu(t, "activation") for t in
+                    (value_precursor, value_from_first_cell, learning_rate_lora,
+                     weight_decay_lora, value_residual_lora)]
+    for t in acts:
+        if t is not None and (t.shape != key.shape or t.dtype != key.dtype):
+            raise ValueError("the [B, T, C] inputs must share one shape and dtype")
+    params = []
+    for t in (learning_rate_bias, weight_decay_bias, value_residual_bias, key_replacement,
+              key_removal):
+        if t is None:
+            params.append(None)
+            continue
+        t = _gpu(t, "parameter")
+        if t.dtype != torch.float32 or t.numel() != C:
+            raise ValueError("biases and key_replacement / key_removal must be fp32 with C elements")
+        params.append(t.reshape(C))
+    out_dtype = key.dtype if out_dtype is None else out_dtype
+    _code(out_dtype)
+    return _WeightPrepareEnd.apply(*acts, *params, num_heads, out_dtype)

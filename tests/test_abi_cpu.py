@@ -32,7 +32,7 @@ def declared_functions(header=HEADER, prefix="wkv7_"):
 def test_header_declares_expected_entry_points():
     names = declared_functions()
     assert len(names) == 13, names
-    assert len(declared_functions(NEIGHBORS_HEADER, "rwkv_")) == 6
+    assert len(declared_functions(NEIGHBORS_HEADER, "rwkv_")) == 9
 
 
 def test_library_exports_every_declared_symbol(native):

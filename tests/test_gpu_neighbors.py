@@ -7,6 +7,10 @@ against float64 PyTorch on the CPU of the same ops, forward and backward:
   results within 1e-5 relative L2, bf16 outputs within bf16 rounding (8e-3);
 * the gated readout against GroupNorm + bonus + gate written with torch ops
   (gated_readout.rs:126-145), same bars;
+* the end of the weight preparation (learning rate, replacement key, value
+  residual, decay, normalized removal key, replacement) against the same ops
+  in torch (weight_prepare.rs:282-317), with and without the residual, with a
+  head whose removal key is zero (the clamped norm), same bars;
 * the whole language model with the fused ops against the same model with
   the torch formulations (same weights and tokens): loss and every
   parameter gradient within 1e-4 in fp32.
@@ -163,6 +167,76 @@ def test_gated_readout_matches_torch(case):
             tol = BF16_TOL
         if n == "gate" and actd == torch.bfloat16:
             tol = BF16_TOL
+        assert _err(a.grad, b.grad) <= tol, n
+
+
+# ------------------------------------------------------- weight preparation end
+PREPARE_CASES = [
+    dict(B=2, T=24, H=2, res=True, idt="f32", odt="f32", zero_head=False),
+    dict(B=1, T=40, H=3, res=False, idt="f32", odt="f32", zero_head=True),
+    dict(B=2, T=16, H=12, res=True, idt="bf16", odt="bf16", zero_head=False),
+    dict(B=3, T=9, H=4, res=False, idt="bf16", odt="f32", zero_head=False),
+    dict(B=2, T=17, H=2, res=True, idt="f32", odt="bf16", zero_head=True),
+    dict(B=16, T=512, H=12, res=True, idt="bf16", odt="bf16", zero_head=False),
+]
+
+
+def _prepare_case_id(c):
+    return "B{B}T{T}H{H}{r}{z}_{idt}_{odt}".format(
+        r="_res" if c["res"] else "", z="_zerohead" if c["zero_head"] else "", **c)
+
+
+def _torch_prepare_end(k, vp, vf, lr, wd, vr, blr, bwd, bvr, ka, kk, H):
+    """weight_prepare.rs:282-317 with the LoRA biases added (lora.rs:118-123),
+    as torch ops."""
+    B, T, C = k.shape
+    learning_rate = torch.sigmoid(lr + blr)
+    kt = k * (ka * (learning_rate - 1.0) + 1.0)
+    v = vp if vf is None else torch.lerp(vp, vf, torch.sigmoid(vr + bvr))
+    w = -F.softplus(-(wd + bwd)) - 0.5
+    a = -F.normalize((k * kk).reshape(B, T, H, 64), p=2.0, dim=-1, eps=1e-12).reshape(B, T, C)
+    return w, kt, v, a, -a * learning_rate
+
+
+@pytest.mark.parametrize("case", PREPARE_CASES, ids=_prepare_case_id)
+def test_weight_prepare_end_matches_torch(case):
+    nb = _nb()
+    B, T, H, res = case["B"], case["T"], case["H"], case["res"]
+    C = H * 64
+    idt, odt = DT[case["idt"]], DT[case["odt"]]
+    g = torch.Generator().manual_seed(B * 100 + T + 7 * H)
+    acts = [torch.randn(B, T, C, generator=g).to(idt) for _ in range(6)]
+    acts[4] = (acts[4].float() * 3.0).to(idt)       # decay LoRA: both softplus regimes
+    params = [0.5 * torch.randn(C, generator=g) for _ in range(5)]
+    params[1] = params[1] - 25.0 * (torch.rand(C, generator=g) > 0.9)   # softplus's linear part
+    if case["zero_head"]:
+        params[4][64:128] = 0.0                       # key_removal: head 1's norm is clamped
+    if not res:
+        acts[2] = acts[5] = params[2] = None
+    grads = [torch.randn(B, T, C, generator=g).to(odt) for _ in range(5)]
+
+    ins64 = [None if t is None else t.double().requires_grad_(True) for t in acts + params]
+    want = _torch_prepare_end(*ins64, H)
+    sum((w * gg.double()).sum() for w, gg in zip(want, grads)).backward()
+
+    dev = torch.device("cuda:0")
+    ins = [None if t is None else t.to(dev).requires_grad_(True) for t in acts + params]
+    announce("weight_prepare_end", _prepare_case_id(case))
+    outs = nb.weight_prepare_end(*ins, H, odt)
+    sum((o.float() * gg.to(dev).float()).sum() for o, gg in zip(outs, grads)).backward()
+    torch.cuda.synchronize()
+
+    names = ("weight_decay", "replacement_key", "value", "removal", "replacement")
+    for n, o, w in zip(names, outs, want):
+        assert o.dtype == odt
+        assert _err(o, w) <= (BF16_TOL if odt == torch.bfloat16 else F32_TOL), n
+    in_names = ("key", "value", "value_first", "lr", "wd", "vr", "lr_bias", "wd_bias",
+                "vr_bias", "key_replacement", "key_removal")
+    for i, (n, a, b) in enumerate(zip(in_names, ins, ins64)):
+        if a is None:
+            continue
+        # bf16 gradients round once; gradients from bf16 output gradients carry their rounding
+        tol = BF16_TOL if (idt == torch.bfloat16 and i < 6) or odt == torch.bfloat16 else F32_TOL
         assert _err(a.grad, b.grad) <= tol, n
 
 

@@ -117,6 +117,76 @@ def test_gated_readout_validation(lib):
     assert ro_fwd(lib, rows=0, y=None, r=None, k=None, v=None, g=None, out=None) == 0
 
 
+def prep_fwd(lib, **over):
+    a = dict(k=FAKE, v=FAKE * 2, vf=FAKE * 3, lr=FAKE * 4, wd=FAKE * 5, vr=FAKE * 6,
+             blr=FAKE * 7, bwd=FAKE * 8, bvr=FAKE * 9, ka=FAKE * 10, kk=FAKE * 11, rows=16, H=2,
+             N=64, dtype=BF16, out=BF16, outs=(FAKE * 20, FAKE * 21, FAKE * 22, FAKE * 23,
+                                             FAKE * 24))
+    a.update(over)
+    return lib.rwkv_weight_prepare_forward(a["k"], a["v"], a["vf"], a["lr"], a["wd"], a["vr"],
+                                           a["blr"], a["bwd"], a["bvr"], a["ka"], a["kk"],
+                                           a["rows"], a["H"], a["N"], a["dtype"], a["out"],
+                                           *a["outs"], None)
+
+
+def test_weight_prepare_workspace_bytes(lib):
+    f = lib.rwkv_weight_prepare_workspace_bytes
+    # 64 rows per block: 8192 rows -> 128 blocks x 5 sums x 768 channels x 4 B
+    assert f(8192, 12, 64) == 128 * 5 * 768 * 4
+    assert f(65, 1, 64) == 2 * 5 * 64 * 4
+    assert f(0, 4, 64) == 0
+    assert f(10, 4, 32) == -1
+    assert f(-1, 4, 64) == -1
+    assert f(10, 0, 64) == -1
+
+
+def test_weight_prepare_forward_validation(lib):
+    assert prep_fwd(lib, dtype=2) == 5
+    assert prep_fwd(lib, out=9) == 5
+    assert prep_fwd(lib, N=32) == 4
+    assert prep_fwd(lib, H=0) == 2
+    assert prep_fwd(lib, rows=-1) == 2
+    assert prep_fwd(lib, k=None) == 1
+    assert prep_fwd(lib, kk=None) == 1
+    assert prep_fwd(lib, vf=None) == 1                      # residual on (its bias is given)
+    assert prep_fwd(lib, vr=None) == 1
+    assert prep_fwd(lib, bvr=None) == 2                     # residual inputs without their bias
+    assert prep_fwd(lib, bvr=None, vf=None, vr=None, outs=(0, 0, 0, 0, 0)) == 1
+    assert prep_fwd(lib, lr=FAKE * 4 + 2) == 6              # bf16 needs 8 bytes
+    assert prep_fwd(lib, ka=FAKE * 10 + 8) == 6             # fp32 parameters need 16 bytes
+    assert prep_fwd(lib, out=F32, outs=(FAKE * 20, FAKE * 21, FAKE * 22 + 8, FAKE * 23,
+                                        FAKE * 24)) == 6
+    assert prep_fwd(lib, outs=(FAKE * 20, FAKE * 20, FAKE * 22, FAKE * 23, FAKE * 24)) == 7
+    assert prep_fwd(lib, outs=(FAKE * 20, FAKE * 21, FAKE * 22, FAKE * 23, FAKE * 5)) == 7
+    # nothing to do: only the parameters are needed
+    assert prep_fwd(lib, rows=0, k=None, v=None, vf=None, lr=None, wd=None, vr=None,
+                    outs=(0, 0, 0, 0, 0)) == 0
+
+
+def test_weight_prepare_backward_validation(lib):
+    def bwd(**over):
+        a = dict(bvr=FAKE * 9, gin=[FAKE * (30 + i) for i in range(5)],
+                 gout=[FAKE * (40 + i) for i in range(6)], sums=[FAKE * (50 + i) for i in range(5)],
+                 ws=FAKE * 60, wsb=1 << 20, vf=FAKE * 3, vr=FAKE * 6)
+        a.update(over)
+        g = a["gout"]
+        return lib.rwkv_weight_prepare_backward(
+            FAKE, FAKE * 2, a["vf"], FAKE * 4, FAKE * 5, a["vr"], FAKE * 7, FAKE * 8, a["bvr"],
+            FAKE * 10, FAKE * 11, 16, 2, 64, BF16, BF16, *a["gin"], g[0], g[1], g[2], g[3], g[4],
+            g[5], a["sums"][0], a["sums"][1], a["sums"][2], a["sums"][3], a["sums"][4], a["ws"],
+            a["wsb"], None)
+    assert bwd(ws=None) == 2
+    assert bwd(wsb=64) == 2
+    assert bwd(gin=[FAKE * 30, 0, FAKE * 32, FAKE * 33, FAKE * 34]) == 1
+    assert bwd(gout=[FAKE * 40, FAKE * 41, FAKE * 42, FAKE * 43, 0, FAKE * 45]) == 1
+    assert bwd(sums=[FAKE * 50, FAKE * 51, FAKE * 52, FAKE * 53, 0]) == 1   # residual bias grad
+    assert bwd(sums=[FAKE * 50, 0, FAKE * 52, FAKE * 53, FAKE * 54]) == 1
+    # no residual: its gradient outputs must be absent too
+    assert bwd(bvr=None, vf=None, vr=None) == 2
+    assert bwd(gout=[FAKE * 40, FAKE * 30, FAKE * 42, FAKE * 43, FAKE * 44, FAKE * 45]) == 7
+    assert bwd(ws=FAKE * 50) == 7                           # workspace over a parameter gradient
+
+
 def test_hip_neighbour_ops_refuse_cpu_tensors():
     import torch
     nb = load_pkg().neighbors
