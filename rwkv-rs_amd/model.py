@@ -452,7 +452,12 @@ class ChannelMixer(nn.Module):
         else:
             diff, next_shift = token_shift_diff(x, embedded_token_shift, context_mask)
             mixed = addcmul(x, diff, self.token_shift_diff_scale)
-        k = torch.relu(self.key(mixed)) ** 2
+        # relu(.)^2 (channel_mixer/mod.rs:108) as a product: autocast runs pow
+        # in fp32 (a cast up, then one back for the value projection, and the
+        # same in the backward), a product stays in the matmul dtype; the
+        # square of a bf16 value is exact in fp32, so both round it once
+        r = torch.relu(self.key(mixed))
+        k = r * r
         out = apply_context_mask(self.value(k), context_mask)
         return out, (next_shift if return_shift else None)
 
