@@ -16,6 +16,6 @@ from . import synthetic  # noqa: F401
 
 
 def __getattr__(name):
-    if name in ("wkv7", "_native", "build", "model", "neighbors", "weights"):
+    if name in ("wkv7", "_native", "build", "model", "neighbors", "weights", "lm_loss"):
         return importlib.import_module(f"{__name__}.{name}")
     raise AttributeError(name)

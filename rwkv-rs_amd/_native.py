@@ -37,6 +37,7 @@ EXPORTS = (
     "rwkv_gated_readout_forward", "rwkv_gated_readout_backward",
     "rwkv_weight_prepare_workspace_bytes", "rwkv_weight_prepare_forward",
     "rwkv_weight_prepare_backward",
+    "rwkv_cross_entropy_l2wrap_forward", "rwkv_cross_entropy_l2wrap_backward",
 )
 
 _P = ctypes.c_void_p
@@ -70,6 +71,9 @@ _SIGNATURES = {
     "rwkv_weight_prepare_forward": ([_P] * 11 + [_I64] * 3 + [_INT] * 2 + [_P] * 6, _INT),
     "rwkv_weight_prepare_backward": ([_P] * 11 + [_I64] * 3 + [_INT] * 2 + [_P] * 17
                                      + [_I64, _P], _INT),
+    "rwkv_cross_entropy_l2wrap_forward": ([_P] * 2 + [_I64] * 2 + [_INT] + [_P] * 5, _INT),
+    "rwkv_cross_entropy_l2wrap_backward": ([_P] * 6 + [ctypes.c_float] + [_I64] * 2 + [_INT]
+                                           + [_P] * 2, _INT),
 }
 
 _lib = None

@@ -21,7 +21,7 @@ CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libwkv7_hip.so")
 SOURCES = ["wkv7_api.cpp", "wkv7_forward.hip", "wkv7_backward.hip", "wkv7_infer.hip",
            "wkv7_chunk_forward.hip", "wkv7_chunk_backward.hip",
-           "neighbors_api.cpp", "neighbors.hip"]
+           "neighbors_api.cpp", "neighbors.hip", "lm_loss_api.cpp", "lm_loss.hip"]
 ARCH = "gfx950"
 
 

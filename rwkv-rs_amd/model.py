@@ -47,6 +47,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from . import lm_loss as _loss
 from . import neighbors as _nb
 from . import wkv7 as _wkv7
 
@@ -540,6 +541,7 @@ class AutoRegressiveModel(nn.Module):
         self.layer_norm_for_unembed = nn.LayerNorm(embedded_dim)
         self.unembed = _linear(embedded_dim, vocab_size)
         self.vocab_size = vocab_size
+        self.neighbor_ops = _check_neighbor_ops(neighbor_ops)
 
     def init_random(self, std: float = 0.02, generator: Optional[torch.Generator] = None):
         """Every weight N(0, std); LayerNorm and GroupNorm weights one and biases zero."""
@@ -565,6 +567,8 @@ class AutoRegressiveModel(nn.Module):
         x, _, _, _ = self.cells(x, batch_ids, kernel)
         logits = self.unembed(self.layer_norm_for_unembed(x))
         n = B * T
+        if self.neighbor_ops == "hip":
+            return _loss.cross_entropy_l2wrap(logits.reshape(n, self.vocab_size), targets.reshape(n))
         logits = l2wrap(logits.reshape(n, self.vocab_size), n)
         return F.cross_entropy(logits.float(), targets.reshape(n))
 

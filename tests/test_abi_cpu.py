@@ -1,4 +1,5 @@
-"""CPU-only checks of the C ABI (include/wkv7.h, include/rwkv_neighbors.h):
+"""CPU-only checks of the C ABI (include/wkv7.h, include/rwkv_neighbors.h,
+include/rwkv_lm_loss.h):
 the library loads, exports
 every declared entry point, and rejects bad calls on the host with the right
 status before any HIP call. No kernel is launched here: every call either
@@ -14,6 +15,7 @@ from conftest import REPO, load_pkg
 
 HEADER = os.path.join(REPO, "include", "wkv7.h")
 NEIGHBORS_HEADER = os.path.join(REPO, "include", "rwkv_neighbors.h")
+LOSS_HEADER = os.path.join(REPO, "include", "rwkv_lm_loss.h")
 
 
 @pytest.fixture(scope="module")
@@ -33,11 +35,13 @@ def test_header_declares_expected_entry_points():
     names = declared_functions()
     assert len(names) == 13, names
     assert len(declared_functions(NEIGHBORS_HEADER, "rwkv_")) == 9
+    assert len(declared_functions(LOSS_HEADER, "rwkv_")) == 2
 
 
 def test_library_exports_every_declared_symbol(native):
     lib = native.lib()
-    declared = declared_functions() + declared_functions(NEIGHBORS_HEADER, "rwkv_")
+    declared = (declared_functions() + declared_functions(NEIGHBORS_HEADER, "rwkv_")
+                + declared_functions(LOSS_HEADER, "rwkv_"))
     for name in declared:
         assert hasattr(lib, name), name
     assert set(declared) == set(native.EXPORTS)

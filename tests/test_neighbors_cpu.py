@@ -187,6 +187,39 @@ def test_weight_prepare_backward_validation(lib):
     assert bwd(ws=FAKE * 50) == 7                           # workspace over a parameter gradient
 
 
+def test_cross_entropy_l2wrap_validation(lib):
+    def fwd(**over):
+        a = dict(x=FAKE, t=FAKE * 2, rows=4, V=64, dt=BF16, outs=(FAKE * 3, FAKE * 4, FAKE * 5,
+                                                                 FAKE * 6))
+        a.update(over)
+        return lib.rwkv_cross_entropy_l2wrap_forward(a["x"], a["t"], a["rows"], a["V"], a["dt"],
+                                                     *a["outs"], None)
+
+    def bwd(**over):
+        a = dict(x=FAKE, t=FAKE * 2, scale=1e-4, rows=4, V=64, dt=BF16, dx=FAKE * 9)
+        a.update(over)
+        return lib.rwkv_cross_entropy_l2wrap_backward(a["x"], a["t"], FAKE * 3, FAKE * 4, FAKE * 5,
+                                                      FAKE * 6, a["scale"], a["rows"], a["V"],
+                                                      a["dt"], a["dx"], None)
+    assert fwd(dt=4) == 5
+    assert fwd(V=0) == 2
+    assert fwd(rows=-1) == 2
+    assert fwd(rows=1 << 31) == 2
+    assert fwd(x=None) == 1
+    assert fwd(outs=(FAKE * 3, 0, FAKE * 5, FAKE * 6)) == 1
+    assert fwd(x=FAKE + 8) == 6                      # vector rows need 16 bytes
+    assert fwd(t=FAKE * 2 + 4) == 6
+    assert fwd(outs=(FAKE * 3, FAKE * 3, FAKE * 5, FAKE * 6)) == 7
+    assert fwd(outs=(FAKE * 3, FAKE * 4, FAKE * 5, FAKE)) == 7    # an output over the logits
+    assert fwd(rows=0, x=None, t=None, outs=(0, 0, 0, 0)) == 0
+    assert bwd(scale=float("nan")) == 2
+    assert bwd(dx=None) == 1
+    assert bwd(dx=FAKE * 9 + 8) == 6
+    assert bwd(V=63, dx=FAKE * 9 + 7) == 6           # element rows: bf16 needs 2 bytes
+    assert bwd(dx=FAKE) == 7                         # gradient over the logits
+    assert bwd(dx=FAKE * 5) == 7                     # gradient over a row array
+
+
 def test_hip_neighbour_ops_refuse_cpu_tensors():
     import torch
     nb = load_pkg().neighbors
