@@ -5,7 +5,7 @@
 A step is one forward and one backward pass of the WKV7 statepass operator
 (initial state in, final-state gradient zero, 16-step checkpoints) over one
 batch of synthetic operands, called through the C ABI with device-resident
-buffers allocated once. The default workload is BASELINE config[1]:
+buffers allocated once. The default workload is the headline one:
 B=8, T=4096, H=32, N=64, bf16 operands, fp32 state and arithmetic,
 initial state ~ N(0, 0.1).
 
@@ -406,8 +406,9 @@ def main():
         pmc_summary(args.pmc_summary)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: the WKV7 operator needs no collective and "
-              "this build runs on single-GPU boxes (see DESIGN.md for how it shards)",
+        print("bench.py measures one GPU only: the WKV7 operator needs no collective, and "
+              "this build runs one process on one GPU (sharding over (batch, head) pairs "
+              "across GPUs is not built)",
               file=sys.stderr)
         sys.exit(2)
     cfg = CONFIGS[args.config]

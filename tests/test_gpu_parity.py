@@ -2,7 +2,7 @@
 include/wkv7.h via the rwkv-rs_amd.wkv7 mirror) against the CPU oracle, which
 restates /root/reference/crates/rwkv-nn/src/kernels/wkv7_common/kernel.rs.
 
-Tolerances: fp32 inputs, relative L2 <= 1e-5 per
+Tolerances (the target's own): fp32 inputs, relative L2 <= 1e-5 per
 tensor; bf16 inputs with fp32 state, relative L2 <= 1e-2 per tensor. For bf16
 inputs the fp32 state-family outputs (checkpoints, removal_state, final state,
 initial-state gradient) are also held to 1e-4: the chunked matrix-core forward
@@ -236,7 +236,7 @@ def test_autograd_matches_direct_backward(wk):
 
 
 def test_full_size_config1_sampled_heads(wk, oracle):
-    # BASELINE config[1] at full size (B=8, T=4096, H=32, bf16, s0 ~ N(0, 0.1)):
+    # the headline workload at full size (B=8, T=4096, H=32, bf16, s0 ~ N(0, 0.1)):
     # two (b, h) pairs, first and last, checked against the oracle over all 4096
     # steps, and the checkpoint of the last chunk equals the transposed final state.
     announce("config[1] full size, sampled heads")
@@ -265,7 +265,7 @@ def test_full_size_config1_sampled_heads(wk, oracle):
 
 
 def test_full_size_config2_sampled_heads(wk, oracle):
-    # BASELINE config[2] at full size (B=4, T=4096, H=64, the 7B-class layer
+    # the 7B-class workload at full size (B=4, T=4096, H=64, the 7B-class layer
     # width, bf16, zero initial state) on the pretrain operator: two (b, h)
     # pairs, first and last, against the oracle over all 4096 steps; and the
     # statepass operator from an all-zero state gives the same outputs and
