@@ -102,3 +102,56 @@ def test_decode_matches_forward_step(wk):
                                 torch.zeros(4, dtype=torch.int32, device="cuda"))
     assert torch.equal(out.output, fwd.output)
     assert torch.equal(st, fwd.final_state)
+
+
+def test_decode_step_replays_from_a_captured_graph(wk):
+    """A serving loop captures its decode step once and replays it: the
+    entry point enqueues one kernel on the caller's stream and neither
+    allocates nor clears memory, so it can sit in a HIP graph. Four replays,
+    each after new tokens are copied into the captured inputs, against the
+    same step run eagerly on copies of the state; the step also advances
+    elapsed_t as a captured torch op (the host bookkeeping of
+    inferring.rs:61-87). Results must be identical."""
+    announce("infer graph capture")
+    pkg = load_pkg()
+    Ba, H, full = 4, 3, 6
+    dev = torch.device("cuda:0")
+    ids = torch.tensor([5, 0, 2, 3], dtype=torch.int32, device=dev)
+    gen = torch.Generator().manual_seed(41)
+    state = (torch.randn(full, H, 64, 64, generator=gen) * 0.1).to(dev)
+    elapsed = torch.randint(0, 100, (full,), generator=gen, dtype=torch.int32).to(dev)
+
+    def fresh(seed):
+        d = pkg.synthetic.make_inputs(Ba, 1, H, 64, seed=seed, bf16=True)
+        return [to_dev(d[n], torch.bfloat16) for n in NAMES]
+
+    static_in = fresh(50)
+
+    def step(ins, st, el):
+        out = wk.wkv7_infer_forward(*ins, ids, st, None, el, use_dither=True)
+        el[ids.long()] += 1
+        return out.output
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):             # warm-up off the capture, on copies
+        step(static_in, state.clone(), elapsed.clone())
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    st_graph, el_graph = state.clone(), elapsed.clone()
+    with torch.cuda.graph(g):
+        y_graph = step(static_in, st_graph, el_graph)
+    torch.cuda.synchronize()
+    # capture records the work without running it: the eager copies start here
+    st_eager, el_eager = state.clone(), elapsed.clone()
+    for rep in range(4):
+        new = fresh(60 + rep)
+        for dst, src in zip(static_in, new):
+            dst.copy_(src)
+        g.replay()
+        y_eager = step(new, st_eager, el_eager)
+        torch.cuda.synchronize()
+        assert torch.equal(y_graph, y_eager), rep
+        assert torch.equal(st_graph, st_eager), rep
+        assert torch.equal(el_graph, el_eager), rep
