@@ -259,3 +259,20 @@ def test_model_fused_neighbours_match_torch_ops():
     worst = max(errs, key=errs.get)
     print(f"[fused neighbours] loss {l0:.6f} vs {l1:.6f}; worst grad {worst} {errs[worst]:.3e}")
     assert errs[worst] <= 1e-4, (worst, errs[worst])
+
+
+def test_weight_prepare_end_with_no_rows():
+    """An empty batch: empty outputs, and parameter gradients that are zero
+    (written by the kernels, not left as allocated)."""
+    nb = _nb()
+    dev = torch.device("cuda:0")
+    H, C = 2, 128
+    acts = [torch.randn(1, 0, C, device=dev).requires_grad_(True) for _ in range(6)]
+    params = [torch.full((C,), float("nan"), device=dev).requires_grad_(True) for _ in range(5)]
+    announce("weight_prepare_end", "no rows")
+    outs = nb.weight_prepare_end(*acts, *params, H, torch.bfloat16)
+    assert all(o.shape == (1, 0, C) and o.dtype == torch.bfloat16 for o in outs)
+    sum(o.float().sum() for o in outs).backward()
+    torch.cuda.synchronize()
+    for p in params:
+        assert torch.equal(p.grad, torch.zeros(C, device=dev))
