@@ -125,15 +125,24 @@ def apply_context_mask(x: torch.Tensor, context_mask: Optional[torch.Tensor]) ->
 
 def token_shift_diff(embedded_context: torch.Tensor,
                      embedded_token_shift: Optional[torch.Tensor] = None,
-                     context_mask: Optional[torch.Tensor] = None):
+                     context_mask: Optional[torch.Tensor] = None,
+                     batch_ids: Optional[torch.Tensor] = None):
     """token_shift_diff/kernel.rs:17-64.
 
     ``diff[t] = prev[t] - x[t]`` where ``prev[t]`` is ``x[t-1]`` when step t-1
     is valid and the external shift otherwise (also at t = 0); masked steps
     give zero. The next shift is ``x`` at the last valid step, or the external
-    shift when no step is valid. Returns ``(token_shifted_diff,
-    next_token_shift)``."""
+    shift when no step is valid. With ``batch_ids`` the external shift is a
+    [full_batch, C] buffer whose row ``batch_ids[b]`` belongs to row b, and
+    the next shift is that buffer with those rows replaced. Returns
+    ``(token_shifted_diff, next_token_shift)``."""
     B, T, C = embedded_context.shape
+    if batch_ids is not None and embedded_token_shift is not None:
+        ids = batch_ids.to(device=embedded_token_shift.device, dtype=torch.long)
+        diff, rows = token_shift_diff(embedded_context, embedded_token_shift[ids], context_mask)
+        full = embedded_token_shift.clone()
+        full[ids] = rows.to(full.dtype)
+        return diff, full
     ext = (embedded_token_shift if embedded_token_shift is not None
            else embedded_context.new_zeros(B, C))
     if T == 0:
@@ -276,11 +285,14 @@ class WeightPrepare(nn.Module):
 
     def forward(self, embedded_context, value_from_first_cell, embedded_token_shift=None,
                 context_mask=None, gate_scale: Optional[torch.Tensor] = None,
-                operand_dtype: Optional[torch.dtype] = None) -> WeightPrepareOutput:
+                operand_dtype: Optional[torch.dtype] = None,
+                batch_ids: Optional[torch.Tensor] = None) -> WeightPrepareOutput:
         """weight_prepare.rs:210-330. With the HIP neighbour ops the token shift
         and the five mixes are one kernel, which also forms the readout gate's
         mix x + diff * ``gate_scale`` (gated_readout.rs:122) when it is given;
-        the difference itself is then not materialised. Everything after the
+        the difference itself is then not materialised. ``batch_ids`` maps
+        rows to the slots of a full-batch ``embedded_token_shift``
+        (weight_prepare.rs:224-229). Everything after the
         projections and the LoRA products is a second kernel, which writes
         the five WKV7 operands it forms in ``operand_dtype`` (default: the
         products' dtype)."""
@@ -292,7 +304,7 @@ class WeightPrepare(nn.Module):
             want_next = embedded_token_shift is not None
             res = _nb.token_shift_mix(
                 embedded_context, scales + ([gate_scale] if gate_scale is not None else []),
-                embedded_token_shift, None, context_mask, _matmul_dtype(embedded_context),
+                embedded_token_shift, batch_ids, context_mask, _matmul_dtype(embedded_context),
                 return_next_token_shift=want_next)
             mixes, next_shift = res if want_next else (res, None)
             xr, xw, xk, xv, xa = mixes[:5]
@@ -301,7 +313,7 @@ class WeightPrepare(nn.Module):
             diff = None
         else:
             diff, next_shift = token_shift_diff(embedded_context, embedded_token_shift,
-                                                context_mask)
+                                                context_mask, batch_ids)
             xr, xw, xk, xv, xa = addcmul5(embedded_context, diff, *scales)
         receptance = self.projection_receptance(xr)
         key_precursor = self.projection_key(xk)
@@ -416,7 +428,7 @@ class TimeMixer(nn.Module):
         v_first = apply_context_mask(io.value_from_first_cell, io.context_mask)
         gate_scale = self.gated_readout.param_gate if self.neighbor_ops == "hip" else None
         wp = self.weight_prepare(x, v_first, io.embedded_token_shift, io.context_mask, gate_scale,
-                                 self.wkv7_dtype)
+                                 self.wkv7_dtype, io.batch_ids)
         shape = (B, T, self.num_heads, self.head_size)
         wkv_in = wp.reshape_to_wkv7_input(shape, self.wkv7_dtype)
         out = kernel.forward(wkv_in, io.state, io.batch_ids, io.elapsed_t, CHUNK_LEN,
@@ -441,17 +453,19 @@ class ChannelMixer(nn.Module):
         self.token_shift_diff_scale = _param(1, 1, embedded_dim)
         self.neighbor_ops = _check_neighbor_ops(neighbor_ops)
 
-    def forward(self, embedded_context, embedded_token_shift=None, context_mask=None):
-        """channel_mixer/mod.rs:83-121; returns (output, next_token_shift or None)."""
+    def forward(self, embedded_context, embedded_token_shift=None, context_mask=None,
+                batch_ids=None):
+        """channel_mixer/mod.rs:83-121 (the token shift by slot, :84-88); returns
+        (output, next_token_shift or None)."""
         return_shift = embedded_token_shift is not None
         x = apply_context_mask(embedded_context, context_mask)
         if self.neighbor_ops == "hip":
-            res = _nb.token_shift_mix(x, [self.token_shift_diff_scale], embedded_token_shift, None,
-                                      context_mask, _matmul_dtype(x),
+            res = _nb.token_shift_mix(x, [self.token_shift_diff_scale], embedded_token_shift,
+                                      batch_ids, context_mask, _matmul_dtype(x),
                                       return_next_token_shift=return_shift)
             (mixed,), next_shift = res if return_shift else (res, None)
         else:
-            diff, next_shift = token_shift_diff(x, embedded_token_shift, context_mask)
+            diff, next_shift = token_shift_diff(x, embedded_token_shift, context_mask, batch_ids)
             mixed = addcmul(x, diff, self.token_shift_diff_scale)
         # relu(.)^2 (channel_mixer/mod.rs:108) as a product: autocast runs pow
         # in fp32 (a cast up, then one back for the value projection, and the
@@ -483,7 +497,7 @@ class CausalCell(nn.Module):
                                          shift_time, state), kernel)
         x = x + tm.embedded_context
         cm, next_shift_channel = self.channel_mixer(self.pre_layer_norm_for_channel_mix(x),
-                                                    shift_channel, context_mask)
+                                                    shift_channel, context_mask, batch_ids)
         x = x + cm
         return x, tm.value_from_first_cell, tm.state, tm.embedded_token_shift, next_shift_channel
 
@@ -558,6 +572,53 @@ class AutoRegressiveModel(nn.Module):
                     p.normal_(0.0, std, generator=generator)
         return self
 
+    def new_infer_state(self, full_batch_size: int, device=None) -> "InferState":
+        """Zeroed per-slot buffers for ``full_batch_size`` slots."""
+        device = device if device is not None else self.embed.weight.device
+        C = self.embed.weight.shape[1]
+        H = self.cells.cells[0].time_mixer.num_heads
+        N = self.cells.cells[0].time_mixer.head_size
+        n = len(self.cells.cells)
+
+        def z(*shape):
+            return torch.zeros(*shape, dtype=torch.float32, device=device)
+        return InferState([z(full_batch_size, C) for _ in range(n)],
+                          [z(full_batch_size, H, N, N) for _ in range(n)],
+                          [z(full_batch_size, C) for _ in range(n)],
+                          torch.zeros(full_batch_size, dtype=torch.int32, device=device))
+
+    @torch.no_grad()
+    def infer(self, contexts: torch.Tensor, batch_ids: torch.Tensor, infer_state: "InferState",
+              context_mask: Optional[torch.Tensor] = None, unembed_mode: str = "last"):
+        """model.rs:184-300: run ``contexts`` ([batch, T] token ids) through
+        the cells on the decode kernel, reading and updating the slots
+        ``batch_ids`` of ``infer_state`` in place (state, both token shifts),
+        with ``infer_state.elapsed_t`` as the dither's step count (the
+        caller advances it afterwards, ``InferState.advance``, as
+        inferring.rs:276 does). ``context_mask`` ([batch, T], 0/1) marks
+        valid steps; a masked step leaves its slot's state alone. Returns
+        the logits of the last step ([batch, 1, vocab], "last"), of every
+        step ("full") or None ("skip")."""
+        if unembed_mode not in UNEMBED_MODES:
+            raise ValueError(f"unembed_mode must be one of {UNEMBED_MODES}")
+        B, T = contexts.shape
+        if T == 0:
+            raise ValueError("contexts must be non-empty")
+        ops32 = self.cells.cells[0].time_mixer.wkv7_dtype == torch.float32
+        kernel = _wkv7.KernelInfer if ops32 else _DitheredInfer
+        x = self.layer_norm_for_first_cell(self.embed(contexts))
+        x, st, state, sc = self.cells(x, batch_ids, kernel, infer_state.elapsed_t, context_mask,
+                                      infer_state.shift_time, infer_state.state,
+                                      infer_state.shift_channel)
+        infer_state.shift_time[:] = st
+        infer_state.state[:] = state
+        infer_state.shift_channel[:] = sc
+        if unembed_mode == "skip":
+            return None
+        if unembed_mode == "last":
+            x = x[:, T - 1:]
+        return self.unembed(self.layer_norm_for_unembed(x))
+
     def forward(self, inputs: torch.Tensor, targets: torch.Tensor, kernel=None):
         """model.rs:121-176 with the pretrain kernel by default; returns the loss."""
         kernel = kernel if kernel is not None else _wkv7.KernelPretrain
@@ -571,6 +632,54 @@ class AutoRegressiveModel(nn.Module):
             return _loss.cross_entropy_l2wrap(logits.reshape(n, self.vocab_size), targets.reshape(n))
         logits = l2wrap(logits.reshape(n, self.vocab_size), n)
         return F.cross_entropy(logits.float(), targets.reshape(n))
+
+
+# ------------------------------------------------------------------ inference
+@dataclass
+class InferState:
+    """The per-slot buffers of a serving loop (examples/rwkv-lm/src/
+    inferring.rs:100-180): for each cell the time- and channel-mix token
+    shifts ([full_batch, C], fp32) and the WKV7 state ([full_batch, H, 64,
+    64], fp32), and each slot's elapsed_t (int32), the dither seed's step
+    count."""
+    shift_time: List[torch.Tensor]
+    state: List[torch.Tensor]
+    shift_channel: List[torch.Tensor]
+    elapsed_t: torch.Tensor
+
+    def advance(self, batch_ids: torch.Tensor, context_len: int,
+                context_mask: Optional[torch.Tensor] = None) -> None:
+        """inferring.rs:61-83: each slot's elapsed_t advances by its valid
+        (unmasked) steps, saturating at the int32 maximum, so a left-padded
+        prefill uses the dither seeds of the same prefill unpadded."""
+        ids = batch_ids.to(device=self.elapsed_t.device, dtype=torch.long)
+        if context_mask is None:
+            valid = torch.full((ids.numel(),), context_len, dtype=torch.int64,
+                               device=self.elapsed_t.device)
+        else:
+            valid = (context_mask != 0).sum(dim=1).to(self.elapsed_t.device)
+        total = (self.elapsed_t[ids].to(torch.int64) + valid).clamp(max=2 ** 31 - 1)
+        self.elapsed_t[ids] = total.to(torch.int32)
+
+    def reset_slot(self, slot: int) -> None:
+        """A new sequence in ``slot``: zero state and shifts, elapsed_t 0
+        (inferring.rs:455-465)."""
+        for t in self.shift_time + self.state + self.shift_channel:
+            t[slot].zero_()
+        self.elapsed_t[slot] = 0
+
+
+class _DitheredInfer:
+    """KernelInfer with the dither on: the reference dithers the decay when
+    the operands are not fp32 (wkv7_infer/host.rs:157)."""
+
+    @staticmethod
+    def forward(input, state, batch_ids, elapsed_t, chunk_len, context_mask):
+        return _wkv7.KernelInfer.forward(input, state, batch_ids, elapsed_t, chunk_len,
+                                         context_mask, use_dither=True)
+
+
+UNEMBED_MODES = ("skip", "last", "full")
 
 
 def make_optimizer(model: nn.Module, lr: float = 6e-4, weight_decay: float = 0.1):

@@ -206,3 +206,23 @@ def test_model_bf16_operands_without_autocast():
                               inputs, targets)
     assert abs(l16 - l32) <= 1e-2 * abs(l32)
     assert all(torch.isfinite(g).all() for g in g16.values())
+
+
+def test_token_shift_by_slot():
+    """token_shift_diff with batch_ids (weight_prepare.rs:224-229,
+    channel_mixer/mod.rs:84-99): rows read their slots of the full-batch
+    shift, the next shift replaces those slots and keeps the others."""
+    m = _model_mod()
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(2, 5, 8, generator=g)
+    full = torch.randn(4, 8, generator=g)
+    ids = torch.tensor([3, 0])
+    mask = torch.ones(2, 5)
+    mask[1, :2] = 0.0
+    diff, nxt = m.token_shift_diff(x, full, mask, ids)
+    want_diff, want_rows = m.token_shift_diff(x, full[ids], mask)
+    assert torch.equal(diff, want_diff)
+    assert torch.equal(nxt[ids], want_rows)
+    assert torch.equal(nxt[[1, 2]], full[[1, 2]])
+    assert torch.equal(m.token_shift_diff(x, full[:2], mask)[0],
+                       m.token_shift_diff(x, full[:2], mask, None)[0])
