@@ -47,6 +47,7 @@ int check_common(const void* logits, const int64_t* targets, int64_t rows, int64
   if (dtype != WKV7_DTYPE_F32 && dtype != WKV7_DTYPE_BF16) return WKV7_ERR_DTYPE;
   if (rows < 0 || rows > INT32_MAX) return WKV7_ERR_SHAPE;   // one block per row
   if (vocab <= 0 || vocab > INT32_MAX) return WKV7_ERR_SHAPE;
+  if (rows > 0 && vocab > INT64_MAX / 4 / rows) return WKV7_ERR_SHAPE;  // byte sizes fit int64
   if (rows > 0 && (!logits || !targets)) return WKV7_ERR_NULL_POINTER;
   if (!aligned(logits, row_alignment(vocab, dtype)) || !aligned(targets, 8))
     return WKV7_ERR_ALIGNMENT;

@@ -205,6 +205,7 @@ def test_cross_entropy_l2wrap_validation(lib):
     assert fwd(V=0) == 2
     assert fwd(rows=-1) == 2
     assert fwd(rows=1 << 31) == 2
+    assert fwd(rows=(1 << 31) - 1, V=(1 << 31) - 1) == 2    # bytes beyond int64
     assert fwd(x=None) == 1
     assert fwd(outs=(FAKE * 3, 0, FAKE * 5, FAKE * 6)) == 1
     assert fwd(x=FAKE + 8) == 6                      # vector rows need 16 bytes
