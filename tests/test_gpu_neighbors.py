@@ -276,3 +276,47 @@ def test_weight_prepare_end_with_no_rows():
     torch.cuda.synchronize()
     for p in params:
         assert torch.equal(p.grad, torch.zeros(C, device=dev))
+
+
+def test_parameter_gradients_are_bitwise_repeatable():
+    """The per-channel gradients are reduced without atomics, in a fixed
+    order: two runs of each fused backward at config[4]'s size give the same
+    bits."""
+    nb = _nb()
+    ll = load_pkg().lm_loss
+    dev = torch.device("cuda:0")
+    B, T, H = 16, 512, 12
+    C = H * 64
+    g = torch.Generator(device=dev).manual_seed(77)
+
+    def rnd(*shape, dtype=torch.float32):
+        return torch.randn(*shape, generator=g, device=dev).to(dtype)
+
+    x, y, r, k, v = rnd(B, T, C), *(rnd(B, T, H, 64, dtype=torch.bfloat16) for _ in range(4))
+    gate = rnd(B, T, C, dtype=torch.bfloat16)
+    acts = [rnd(B, T, C, dtype=torch.bfloat16) for _ in range(6)]
+    logits, targets = rnd(512, 65536, dtype=torch.bfloat16), torch.randint(0, 65536, (512,), device=dev)
+    grads_mix = [rnd(B, T, C, dtype=torch.bfloat16) for _ in range(6)]
+    dro, dpre = rnd(B, T, C, dtype=torch.bfloat16), [rnd(B, T, C, dtype=torch.bfloat16) for _ in range(5)]
+
+    def run():
+        scales = [torch.linspace(-1, 1, C, device=dev).requires_grad_(True) for _ in range(6)]
+        mixes = nb.token_shift_mix(x, scales, out_dtype=torch.bfloat16)
+        sum((m.float() * gm.float()).sum() for m, gm in zip(mixes, grads_mix)).backward()
+        params = [torch.full((C,), 0.5, device=dev).requires_grad_(True) for _ in range(3)]
+        bonus = torch.full((H, 64), 0.1, device=dev).requires_grad_(True)
+        out = nb.gated_readout(y, r, k, v, gate, bonus, params[0], params[1])
+        (out.float() * dro.float()).sum().backward()
+        pp = [torch.full((C,), 0.3, device=dev).requires_grad_(True) for _ in range(5)]
+        outs = nb.weight_prepare_end(*acts, *pp, H, torch.bfloat16)
+        sum((o.float() * d.float()).sum() for o, d in zip(outs, dpre)).backward()
+        lg = logits.clone().requires_grad_(True)
+        ll.cross_entropy_l2wrap(lg, targets).backward()
+        torch.cuda.synchronize()
+        return [s.grad for s in scales] + [bonus.grad, params[0].grad, params[1].grad] + \
+            [p.grad for p in pp] + [lg.grad]
+
+    announce("determinism", "token shift, readout, weight preparation, loss")
+    first, second = run(), run()
+    for i, (a, b) in enumerate(zip(first, second)):
+        assert torch.equal(a, b), i
