@@ -45,11 +45,17 @@ def test_decode_step_slot_mapped(wk, oracle, dtype, dither):
     np.testing.assert_array_equal(to_np(st_gpu)[untouched], state[untouched])
 
 
-def test_prefill_with_mask_matches_oracle(wk, oracle):
-    announce("infer prefill with mask")
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_prefill_with_mask_matches_oracle(wk, oracle, dtype):
+    # prefill (T > 1, the 16-step tile kernel) with a left-padded, ragged mask
+    # in the operand dtype; fp32 state, no dither (the reference's F = f32
+    # kernel, wkv7_infer/host.rs:157), bf16 operands carried as their exact
+    # fp32 values by the oracle
+    announce("infer prefill with mask", dtype)
     pkg = load_pkg()
     Ba, T, H, full = 3, 37, 2, 4
-    d = pkg.synthetic.make_inputs(Ba, T, H, 64, seed=33)
+    bf16 = dtype == torch.bfloat16
+    d = pkg.synthetic.make_inputs(Ba, T, H, 64, seed=33, bf16=bf16)
     rng = np.random.default_rng(34)
     mask = (rng.random((Ba, T)) < 0.8).astype(np.float32)
     mask[0, :5] = 0.0   # left padding
@@ -57,15 +63,52 @@ def test_prefill_with_mask_matches_oracle(wk, oracle):
     ids = np.array([2, 0, 3], np.int32)
     elapsed = np.array([5, 17, 0, 9], np.int32)
     st_gpu = to_dev(state)
-    out = wk.wkv7_infer_forward(*(to_dev(d[n]) for n in NAMES), torch.from_numpy(ids).cuda(), st_gpu,
-                                to_dev(mask), torch.from_numpy(elapsed).cuda(), use_dither=True)
+    out = wk.wkv7_infer_forward(*(to_dev(d[n], dtype) for n in NAMES), torch.from_numpy(ids).cuda(),
+                                st_gpu, to_dev(mask, dtype), torch.from_numpy(elapsed).cuda())
     st_ref = state.copy()
-    y_ref = oracle.infer_f32(*(d[n] for n in NAMES), ids, st_ref, mask, elapsed.view(np.uint32),
-                             use_dither=True)
+    y_ref = oracle.infer_f32(*(d[n] for n in NAMES), ids, st_ref, mask, elapsed.view(np.uint32))
     y = to_np(out.output)
     assert np.all(y[mask == 0] == 0.0)
-    assert rel_l2(y, y_ref) < 1e-5
+    if bf16:
+        y_ref = pkg.synthetic.bf16_round(y_ref)
+    assert rel_l2(y, y_ref) < (1e-5 if not bf16 else 1e-2)
     assert rel_l2(to_np(st_gpu), st_ref) < 1e-5
+    np.testing.assert_array_equal(to_np(st_gpu)[1], state[1])
+
+
+def test_config3_decode_at_full_size(wk, oracle):
+    """config[3] at its size: one decode step of 256 sequences, H = 40, bf16
+    operands, fp32 state ~ N(0, 0.1), the reference's F = f32 kernel (no
+    dither). The 256 active rows map onto a permutation of slots of a larger
+    320-slot buffer; output and every slot are compared with the oracle, and
+    the 64 untouched slots must be bit-identical."""
+    announce("config[3] decode at full size")
+    pkg = load_pkg()
+    Ba, H, full = 256, 40, 320
+    d = pkg.synthetic.make_inputs(Ba, 1, H, 64, seed=0x5EED0003, bf16=True, with_grad=False)
+    rng = np.random.default_rng(0x5EED0003)
+    state = (rng.standard_normal((full, H, 64, 64), dtype=np.float32) * np.float32(0.1))
+    ids = rng.permutation(full)[:Ba].astype(np.int32)
+    elapsed = rng.integers(0, 1 << 20, full).astype(np.int32)
+    st_gpu = to_dev(state)
+    out = wk.wkv7_infer_forward(*(to_dev(d[n], torch.bfloat16) for n in NAMES),
+                                torch.from_numpy(ids).cuda(), st_gpu, None,
+                                torch.from_numpy(elapsed).cuda())
+    torch.cuda.synchronize()
+    st_ref = state.copy()
+    y_ref = oracle.infer_f32(*(d[n] for n in NAMES), ids, st_ref, None, elapsed.view(np.uint32))
+    y = to_np(out.output)
+    got = to_np(st_gpu)
+    err_y = rel_l2(y, pkg.synthetic.bf16_round(y_ref))
+    # per (row, head) state errors, the fp32 state family's 1e-5 bar
+    num = np.sqrt(((got[ids].astype(np.float64) - st_ref[ids]) ** 2).sum(axis=(2, 3)))
+    den = np.sqrt((st_ref[ids].astype(np.float64) ** 2).sum(axis=(2, 3)))
+    print("config[3]", f"y {err_y:.2e} worst state pair {float((num / den).max()):.2e}", flush=True)
+    assert err_y < 1e-2
+    assert float((num / den).max()) < 1e-5
+    untouched = np.setdiff1d(np.arange(full), ids)
+    assert untouched.size == full - Ba
+    np.testing.assert_array_equal(got[untouched], state[untouched])
 
 
 def test_masked_padding_is_a_noop(wk):
