@@ -133,6 +133,35 @@ int rwkv_gated_readout_backward(const void *wkv7_output, const void *receptance,
                                 float *group_norm_bias_grad, void *workspace,
                                 int64_t workspace_bytes, void *stream);
 
+/* Bytes of the device array that rwkv_gated_readout_backward_noalloc uses in
+ * place of the workspace argument. */
+#define RWKV_READOUT_SCRATCH_BYTES (4 * 1024 * 1024)
+
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving or training loops,
+ * harnesses that forbid hipMalloc): rwkv_gated_readout_backward with the
+ * workspace replaced by a fixed array of RWKV_READOUT_SCRATCH_BYTES that the
+ * library holds on each GPU it runs on until the process ends. It allocates
+ * nothing. Calls whose workspace (rwkv_gated_readout_workspace_bytes) would
+ * exceed the array return WKV7_ERR_SCRATCH_LIMIT before any HIP call. Every
+ * call on one GPU shares that GPU's array: calls that overlap in time on one
+ * GPU (different streams without ordering between them) race and give wrong
+ * parameter gradients; order them. The array's device address is looked up
+ * on the first call per device, with that device current. Outputs equal
+ * rwkv_gated_readout_backward's bit for bit. */
+int rwkv_gated_readout_backward_noalloc(const void *wkv7_output, const void *receptance,
+                                        const void *replacement_key, const void *value,
+                                        const void *gate, const float *receptance_key_bonus,
+                                        const float *group_norm_weight,
+                                        const float *group_norm_bias, float epsilon,
+                                        int64_t rows, int64_t num_heads, int64_t head_size,
+                                        int dtype, int act_dtype, const void *output_grad,
+                                        void *wkv7_output_grad, void *receptance_grad,
+                                        void *replacement_key_grad, void *value_grad,
+                                        void *gate_grad, float *receptance_key_bonus_grad,
+                                        float *group_norm_weight_grad,
+                                        float *group_norm_bias_grad, void *stream);
+
 /*
  * End of the weight preparation. From the key and value projections
  * ("precursors") and the three LoRA products before their bias

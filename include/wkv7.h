@@ -82,7 +82,9 @@ typedef enum wkv7_status {
   WKV7_ERR_ALIGNMENT = 6,    /* a tensor pointer is misaligned */
   WKV7_ERR_OVERLAP = 7,      /* an output overlaps another operand */
   WKV7_ERR_FLAGS = 8,        /* a flag is not 0/1 or contradicts a pointer */
-  WKV7_ERR_HIP = 9           /* the kernel launch failed */
+  WKV7_ERR_HIP = 9,          /* the kernel launch failed */
+  WKV7_ERR_SCRATCH_LIMIT = 10 /* the call needs more than the library's fixed
+                                 scratch array (the _noalloc entry points) */
 } wkv7_status;
 
 typedef enum wkv7_dtype { WKV7_DTYPE_F32 = 0, WKV7_DTYPE_BF16 = 1 } wkv7_dtype;

@@ -21,7 +21,7 @@ STATUS_NAMES = {
     0: "WKV7_OK", 1: "WKV7_ERR_NULL_POINTER", 2: "WKV7_ERR_SHAPE",
     3: "WKV7_ERR_CHUNK_LEN", 4: "WKV7_ERR_HEAD_SIZE", 5: "WKV7_ERR_DTYPE",
     6: "WKV7_ERR_ALIGNMENT", 7: "WKV7_ERR_OVERLAP", 8: "WKV7_ERR_FLAGS",
-    9: "WKV7_ERR_HIP",
+    9: "WKV7_ERR_HIP", 10: "WKV7_ERR_SCRATCH_LIMIT",
 }
 
 # every symbol include/wkv7.h declares
@@ -35,6 +35,7 @@ EXPORTS = (
     "rwkv_token_shift_mix_workspace_bytes", "rwkv_token_shift_mix_forward",
     "rwkv_token_shift_mix_backward", "rwkv_gated_readout_workspace_bytes",
     "rwkv_gated_readout_forward", "rwkv_gated_readout_backward",
+    "rwkv_gated_readout_backward_noalloc",
     "rwkv_weight_prepare_workspace_bytes", "rwkv_weight_prepare_forward",
     "rwkv_weight_prepare_backward",
     "rwkv_cross_entropy_l2wrap_forward", "rwkv_cross_entropy_l2wrap_backward",
@@ -67,6 +68,8 @@ _SIGNATURES = {
                                    + [_P] * 2, _INT),
     "rwkv_gated_readout_backward": ([_P] * 8 + [ctypes.c_float] + [_I64] * 3 + [_INT] * 2
                                     + [_P] * 10 + [_I64, _P], _INT),
+    "rwkv_gated_readout_backward_noalloc": ([_P] * 8 + [ctypes.c_float] + [_I64] * 3
+                                            + [_INT] * 2 + [_P] * 10, _INT),
     "rwkv_weight_prepare_workspace_bytes": ([_I64] * 3, _I64),
     "rwkv_weight_prepare_forward": ([_P] * 11 + [_I64] * 3 + [_INT] * 2 + [_P] * 6, _INT),
     "rwkv_weight_prepare_backward": ([_P] * 11 + [_I64] * 3 + [_INT] * 2 + [_P] * 17

@@ -37,6 +37,8 @@
 // per-channel gradients) are reduced within a
 // block, written as one partial per block to a workspace and summed in a
 // fixed order by a second kernel, so results do not depend on scheduling.
+#include <atomic>
+#include <mutex>
 #include <type_traits>
 
 #include "neighbors_launch.hpp"
@@ -852,6 +854,45 @@ hipError_t launch_prepare_backward(const PrepareArgs& a, hipStream_t s) {
       dispatch_prepare<PrepareBackward>(a, dim3(static_cast<unsigned>(rb), static_cast<unsigned>(a.H)), s);
   if (e != hipSuccess) return e;
   return column_sum(a.workspace, rb, q, C, a.sums, s);
+}
+
+// ------------------------------------------------- fixed device scratch array
+// The gated readout backward's column-sum partials for callers that cannot
+// allocate (rwkv_gated_readout_backward_noalloc). Each GPU holds its own copy
+// of `scratch` at its own address for the life of the process. In host code
+// the name `scratch` is only a host-side stand-in, so it is never passed to a
+// kernel: the device address is looked up once per device with
+// hipGetSymbolAddress and kept in scratch_ptr[device].
+namespace {
+
+static __device__ __align__(256) float scratch[kReadoutScratchBytes / sizeof(float)];
+
+constexpr int kMaxScratchDevices = 256;
+std::atomic<float*> scratch_ptr[kMaxScratchDevices];
+std::mutex scratch_mu;
+
+}  // namespace
+
+hipError_t readout_scratch(float** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxScratchDevices) return hipErrorInvalidDevice;
+  float* p = scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    p = scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      void* addr = nullptr;
+      e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return e;
+      if (!addr) return hipErrorInvalidSymbol;
+      p = static_cast<float*>(addr);
+      scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return hipSuccess;
 }
 
 }  // namespace rwkv_nb

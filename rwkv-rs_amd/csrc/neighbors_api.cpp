@@ -13,6 +13,9 @@
 #include "neighbors_launch.hpp"
 #include "wkv7_launch.hpp"
 
+static_assert(rwkv_nb::kReadoutScratchBytes == RWKV_READOUT_SCRATCH_BYTES,
+              "the scratch array size the header states");
+
 namespace {
 
 constexpr int64_t kMaxGridY = 65535;
@@ -329,17 +332,24 @@ int rwkv_gated_readout_forward(const void* wkv7_output, const void* receptance,
   return wkv7::hip_status(rwkv_nb::launch_readout_forward(a, static_cast<hipStream_t>(stream)));
 }
 
-int rwkv_gated_readout_backward(const void* wkv7_output, const void* receptance,
-                                const void* replacement_key, const void* value, const void* gate,
-                                const float* receptance_key_bonus,
-                                const float* group_norm_weight, const float* group_norm_bias,
-                                float epsilon, int64_t rows, int64_t num_heads, int64_t head_size,
-                                int dtype, int act_dtype, const void* output_grad,
-                                void* wkv7_output_grad, void* receptance_grad,
-                                void* replacement_key_grad, void* value_grad, void* gate_grad,
-                                float* receptance_key_bonus_grad, float* group_norm_weight_grad,
-                                float* group_norm_bias_grad, void* workspace,
-                                int64_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// Checks and launch of the gated readout backward, shared by the entry point
+// that takes a workspace and the one that uses the library's scratch array.
+// With `scratch` set, `workspace` is ignored: the checks run first and the
+// scratch array's device address is looked up only for a valid call.
+int readout_backward(const void* wkv7_output, const void* receptance,
+                     const void* replacement_key, const void* value, const void* gate,
+                     const float* receptance_key_bonus, const float* group_norm_weight,
+                     const float* group_norm_bias, float epsilon, int64_t rows,
+                     int64_t num_heads, int64_t head_size, int dtype, int act_dtype,
+                     const void* output_grad, void* wkv7_output_grad, void* receptance_grad,
+                     void* replacement_key_grad, void* value_grad, void* gate_grad,
+                     float* receptance_key_bonus_grad, float* group_norm_weight_grad,
+                     float* group_norm_bias_grad, void* workspace, int64_t workspace_bytes,
+                     bool scratch, void* stream) {
   if (int rc = check_readout(wkv7_output, receptance, replacement_key, value, gate,
                              receptance_key_bonus, group_norm_weight, group_norm_bias, epsilon,
                              rows, num_heads, head_size, dtype, act_dtype))
@@ -351,7 +361,12 @@ int rwkv_gated_readout_backward(const void* wkv7_output, const void* receptance,
                    !replacement_key_grad || !value_grad || !gate_grad))
     return WKV7_ERR_NULL_POINTER;
   const int64_t need = readout_workspace(rows, num_heads);
-  if (need > 0 && (!workspace || workspace_bytes < need)) return WKV7_ERR_SHAPE;
+  if (scratch) {
+    if (need > rwkv_nb::kReadoutScratchBytes) return WKV7_ERR_SCRATCH_LIMIT;
+    workspace = nullptr;
+  } else if (need > 0 && (!workspace || workspace_bytes < need)) {
+    return WKV7_ERR_SHAPE;
+  }
   for (const void* p : {wkv7_output_grad, receptance_grad, replacement_key_grad, value_grad})
     if (p && !aligned_for(p, dtype)) return WKV7_ERR_ALIGNMENT;
   for (const void* p : {output_grad, static_cast<const void*>(gate_grad)})
@@ -370,6 +385,10 @@ int rwkv_gated_readout_backward(const void* wkv7_output, const void* receptance,
                    {gate, act}, {receptance_key_bonus, C * 4}, {group_norm_weight, C * 4},
                    {group_norm_bias, C * 4}, {output_grad, act}}))
     return WKV7_ERR_OVERLAP;
+  float* ws = static_cast<float*>(workspace);
+  if (scratch && need > 0) {
+    if (int rc = wkv7::hip_status(rwkv_nb::readout_scratch(&ws))) return rc;
+  }
   rwkv_nb::ReadoutArgs a{};
   a.y = wkv7_output;
   a.r = receptance;
@@ -393,8 +412,47 @@ int rwkv_gated_readout_backward(const void* wkv7_output, const void* receptance,
   a.bonus_grad = receptance_key_bonus_grad;
   a.weight_grad = group_norm_weight_grad;
   a.bias_grad = group_norm_bias_grad;
-  a.workspace = static_cast<float*>(workspace);
+  a.workspace = ws;
   return wkv7::hip_status(rwkv_nb::launch_readout_backward(a, static_cast<hipStream_t>(stream)));
+}
+
+}  // namespace
+
+extern "C" {
+
+int rwkv_gated_readout_backward(const void* wkv7_output, const void* receptance,
+                                const void* replacement_key, const void* value, const void* gate,
+                                const float* receptance_key_bonus,
+                                const float* group_norm_weight, const float* group_norm_bias,
+                                float epsilon, int64_t rows, int64_t num_heads, int64_t head_size,
+                                int dtype, int act_dtype, const void* output_grad,
+                                void* wkv7_output_grad, void* receptance_grad,
+                                void* replacement_key_grad, void* value_grad, void* gate_grad,
+                                float* receptance_key_bonus_grad, float* group_norm_weight_grad,
+                                float* group_norm_bias_grad, void* workspace,
+                                int64_t workspace_bytes, void* stream) {
+  return readout_backward(wkv7_output, receptance, replacement_key, value, gate,
+                          receptance_key_bonus, group_norm_weight, group_norm_bias, epsilon,
+                          rows, num_heads, head_size, dtype, act_dtype, output_grad,
+                          wkv7_output_grad, receptance_grad, replacement_key_grad, value_grad,
+                          gate_grad, receptance_key_bonus_grad, group_norm_weight_grad,
+                          group_norm_bias_grad, workspace, workspace_bytes, false, stream);
+}
+
+int rwkv_gated_readout_backward_noalloc(
+    const void* wkv7_output, const void* receptance, const void* replacement_key,
+    const void* value, const void* gate, const float* receptance_key_bonus,
+    const float* group_norm_weight, const float* group_norm_bias, float epsilon, int64_t rows,
+    int64_t num_heads, int64_t head_size, int dtype, int act_dtype, const void* output_grad,
+    void* wkv7_output_grad, void* receptance_grad, void* replacement_key_grad, void* value_grad,
+    void* gate_grad, float* receptance_key_bonus_grad, float* group_norm_weight_grad,
+    float* group_norm_bias_grad, void* stream) {
+  return readout_backward(wkv7_output, receptance, replacement_key, value, gate,
+                          receptance_key_bonus, group_norm_weight, group_norm_bias, epsilon,
+                          rows, num_heads, head_size, dtype, act_dtype, output_grad,
+                          wkv7_output_grad, receptance_grad, replacement_key_grad, value_grad,
+                          gate_grad, receptance_key_bonus_grad, group_norm_weight_grad,
+                          group_norm_bias_grad, nullptr, 0, true, stream);
 }
 
 int64_t rwkv_weight_prepare_workspace_bytes(int64_t rows, int64_t num_heads, int64_t head_size) {

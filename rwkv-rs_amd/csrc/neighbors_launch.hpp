@@ -100,4 +100,10 @@ hipError_t launch_readout_backward(const ReadoutArgs& a, hipStream_t s);
 hipError_t launch_prepare_forward(const PrepareArgs& a, hipStream_t s);
 hipError_t launch_prepare_backward(const PrepareArgs& a, hipStream_t s);
 
+// Size of the library's fixed device array that stands in for the gated
+// readout backward's workspace, and its device address on the current device
+// (looked up on the first call per device; no allocation).
+constexpr int64_t kReadoutScratchBytes = int64_t(4) << 20;
+hipError_t readout_scratch(float** out);
+
 }  // namespace rwkv_nb

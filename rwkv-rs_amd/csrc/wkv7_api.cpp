@@ -109,6 +109,8 @@ const char* wkv7_strerror(int status) {
     case WKV7_ERR_OVERLAP: return "an output buffer overlaps another operand";
     case WKV7_ERR_FLAGS: return "invalid flag value or flag/pointer mismatch";
     case WKV7_ERR_HIP: return "HIP kernel launch failed";
+    case WKV7_ERR_SCRATCH_LIMIT:
+      return "the call needs more scratch memory than the library's fixed device array holds";
     default: return "unknown wkv7 status";
   }
 }

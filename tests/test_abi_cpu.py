@@ -34,7 +34,7 @@ def declared_functions(header=HEADER, prefix="wkv7_"):
 def test_header_declares_expected_entry_points():
     names = declared_functions()
     assert len(names) == 13, names
-    assert len(declared_functions(NEIGHBORS_HEADER, "rwkv_")) == 9
+    assert len(declared_functions(NEIGHBORS_HEADER, "rwkv_")) == 10
     assert len(declared_functions(LOSS_HEADER, "rwkv_")) == 2
 
 
