@@ -70,7 +70,7 @@
 extern "C" {
 #endif
 
-#define WKV7_ABI_VERSION 1
+#define WKV7_ABI_VERSION 2
 
 typedef enum wkv7_status {
   WKV7_OK = 0,
@@ -81,7 +81,8 @@ typedef enum wkv7_status {
   WKV7_ERR_DTYPE = 5,        /* unknown dtype code */
   WKV7_ERR_ALIGNMENT = 6,    /* a tensor pointer is misaligned */
   WKV7_ERR_OVERLAP = 7,      /* an output overlaps another operand */
-  WKV7_ERR_FLAGS = 8,        /* a flag is not 0/1 or contradicts a pointer */
+  WKV7_ERR_FLAGS = 8,        /* a flag is not 0/1, contradicts a pointer, or
+                                asks for the dither with an fp32 state */
   WKV7_ERR_HIP = 9,          /* the kernel launch failed */
   WKV7_ERR_SCRATCH_LIMIT = 10 /* the call needs more than the library's fixed
                                  scratch array (the _noalloc entry points) */
@@ -207,26 +208,41 @@ int wkv7_statetune_backward(const void *weight_decay, const void *receptance,
 
 /* Wkv7InferBackend::wkv7_infer_forward (wkv7_infer/mod.rs:30-51; host
  * wkv7_infer/host.rs:27-187). Per-token tensors are
- * [active_batch_size, context_len, num_heads, 64]. Row b uses and updates, in
- * place, slot batch_ids[b] of `state` ([full_batch_size, num_heads, 64, 64],
- * fp32); batch_ids must be distinct and in [0, full_batch_size) (the reference
- * asserts this in debug builds, examples/rwkv-lm/src/inferring.rs:224-234).
- * context_mask ([active_batch_size, context_len] in dtype, NULL = all ones):
- * a 0 entry gives output 0 and leaves the state untouched. use_dither = 1 adds
- * the reference's deterministic dither (wkv7_infer/kernel.rs:8-13) seeded with
- * elapsed_t[slot] + (unmasked steps so far); elapsed_t ([full_batch_size],
- * read as uint32) may be NULL only when use_dither = 0. The reference turns
- * the dither on exactly when its element type is not fp32
- * (wkv7_infer/host.rs:157); here the state is always fp32 and the caller
- * chooses. */
+ * [active_batch_size, context_len, num_heads, 64] in dtype. Row b uses and
+ * updates, in place, slot batch_ids[b] of `state` ([full_batch_size,
+ * num_heads, 64, 64] in state_dtype); batch_ids must be distinct and in
+ * [0, full_batch_size) (the reference asserts this in debug builds,
+ * examples/rwkv-lm/src/inferring.rs:224-234; an out-of-range id gets output
+ * 0 and touches no state). context_mask ([active_batch_size, context_len] in
+ * dtype, NULL = all ones): a 0 entry gives output 0 and leaves the state
+ * untouched.
+ *
+ * state_dtype selects which instantiation of the reference kernel runs:
+ *   WKV7_DTYPE_F32   the reference at element type f32 (fp32 state and
+ *                    arithmetic; bf16 operands are used as their exact fp32
+ *                    values). No dither: use_dither must be 0, as the
+ *                    reference's host sets it (host.rs:157).
+ *   WKV7_DTYPE_BF16  the reference at element type bf16 (requires dtype
+ *                    bf16): bf16 state, the decay rounded to bf16 after the
+ *                    optional dither, and every product and sum of the update
+ *                    and of the two sums over the key index rounded to bf16
+ *                    (ties to even) in the kernel's order
+ *                    (wkv7_infer/kernel.rs:71-98). The reference always
+ *                    passes use_dither = 1 here (host.rs:157).
+ * use_dither = 1 adds the reference's deterministic dither
+ * (wkv7_infer/kernel.rs:8-13) seeded with elapsed_t[slot] + (unmasked steps
+ * so far) to the fp32 decay before its rounding; elapsed_t
+ * ([full_batch_size], read as uint32) may be NULL only when use_dither = 0.
+ * The state buffer must be 16-byte aligned. */
 int wkv7_infer_forward(const void *weight_decay, const void *receptance,
                        const void *key, const void *value, const void *removal,
                        const void *replacement, const int32_t *batch_ids,
-                       float *state, const void *context_mask,
+                       void *state, const void *context_mask,
                        const int32_t *elapsed_t, int64_t active_batch_size,
                        int64_t context_len, int64_t num_heads,
                        int64_t head_size, int64_t full_batch_size, int dtype,
-                       int use_dither, void *output, void *stream);
+                       int state_dtype, int use_dither, void *output,
+                       void *stream);
 
 #ifdef __cplusplus
 }

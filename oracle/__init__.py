@@ -14,6 +14,8 @@ Functions (numpy in, numpy out) wrap ``libwkv7_oracle.so`` built from
 * ``forward_f64`` / ``grad_f64`` -- fp64 forward and a back-propagation
   through time that stores every state (no reversal)
 * ``infer_f32``    -- slot-mapped decode, wkv7_infer/kernel.rs:15-114
+* ``infer_bf16``   -- the same kernel with element type bf16: bf16 state,
+  decay (plus dither) rounded to bf16, every product and sum rounded to bf16
 * ``dither``       -- deterministic_dither, wkv7_infer/kernel.rs:8-13
 
 How each function is pinned (tests/test_oracle_*.py):
@@ -28,6 +30,12 @@ How each function is pinned (tests/test_oracle_*.py):
 * infer: T=1 infer == one forward step (bitwise), masked steps are no-ops, the
   reference's two scalar dither/mask tests (wkv7_infer/mod.rs:189-269), and
   integer known answers of the dither hash.
+* infer_bf16: the reference's two scalar tests (wkv7_infer/mod.rs:143-269) at
+  N=1 with every F operation rounded to bf16; inputs whose every
+  intermediate is a small integer (bf16 arithmetic is then exact: causal
+  linear attention, a closed form); agreement with infer_f32 to bf16
+  rounding; a row-vectorised numpy evaluation of the same rounding points
+  (tests/test_oracle_infer_bf16.py).
 """
 
 from __future__ import annotations
@@ -71,10 +79,13 @@ def _load():
         [_i64] * 5 + [_f32p] * 6 + [ctypes.POINTER(ctypes.c_int32), _f32p, _f32p,
                                     ctypes.POINTER(ctypes.c_uint32), ctypes.c_int,
                                     _f32p])
+    lib.wkv7o_infer_bf16.argtypes = lib.wkv7o_infer_f32.argtypes
+    lib.wkv7o_round_bf16.argtypes = [ctypes.c_float]
+    lib.wkv7o_round_bf16.restype = ctypes.c_float
     lib.wkv7o_dither.argtypes = [ctypes.c_uint32]
     lib.wkv7o_dither.restype = ctypes.c_float
     for fn in ("wkv7o_forward_f32", "wkv7o_backward_f32", "wkv7o_forward_f64",
-               "wkv7o_grad_f64", "wkv7o_infer_f32"):
+               "wkv7o_grad_f64", "wkv7o_infer_f32", "wkv7o_infer_bf16"):
         getattr(lib, fn).restype = ctypes.c_int
     _lib = lib
     return lib
@@ -179,6 +190,34 @@ def infer_f32(w, r, k, v, a, b, batch_ids, state, context_mask=None,
     """Slot-mapped decode. ``state`` ([full_batch, H, N, N] fp32) is updated in
     place, as the reference kernel does (wkv7_infer/kernel.rs:103-113).
     Returns the output [Ba, T, H, N]."""
+    return _infer("wkv7o_infer_f32", w, r, k, v, a, b, batch_ids, state, context_mask,
+                  elapsed_t, use_dither)
+
+
+def infer_bf16(w, r, k, v, a, b, batch_ids, state, context_mask=None,
+               elapsed_t=None, use_dither=True):
+    """Slot-mapped decode with element type bf16 (the reference kernel at
+    F = bf16; its host turns the dither on for every F that is not f32,
+    wkv7_infer/host.rs:157). Operands, mask and ``state`` are float32 arrays
+    holding bf16 values; ``state`` is updated in place and stays bf16-valued.
+    Returns the output [Ba, T, H, N] (bf16 values)."""
+    for x in (w, r, k, v, a, b, state):
+        if np.any(np.asarray(x, np.float32) != _round_bf16_np(x)):
+            raise ValueError("infer_bf16 takes bf16 values")
+    return _infer("wkv7o_infer_bf16", w, r, k, v, a, b, batch_ids, state, context_mask,
+                  elapsed_t, use_dither)
+
+
+def _round_bf16_np(x):
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    return ((u + np.uint32(0x7FFF) + ((u >> 16) & 1)) & np.uint32(0xFFFF0000)).view(np.float32)
+
+
+def round_bf16(x: float) -> float:
+    return float(_load().wkv7o_round_bf16(ctypes.c_float(x)))
+
+
+def _infer(fn, w, r, k, v, a, b, batch_ids, state, context_mask, elapsed_t, use_dither):
     lib = _load()
     w, r, k, v, a, b = (_c(x, np.float32) for x in (w, r, k, v, a, b))
     if state.dtype != np.float32 or not state.flags.c_contiguous:
@@ -189,13 +228,13 @@ def infer_f32(w, r, k, v, a, b, batch_ids, state, context_mask=None,
     mask = _c(context_mask, np.float32)
     et = _c(elapsed_t, np.uint32)
     y = np.empty_like(w)
-    rc = lib.wkv7o_infer_f32(
+    rc = getattr(lib, fn)(
         Ba, T, H, N, full_batch, *(_p(x, _f32p) for x in (w, r, k, v, a, b)),
         _p(batch_ids, ctypes.POINTER(ctypes.c_int32)), _p(state, _f32p),
         _p(mask, _f32p), _p(et, ctypes.POINTER(ctypes.c_uint32)),
         int(bool(use_dither)), _p(y, _f32p))
     if rc != 0:
-        raise RuntimeError(f"wkv7o_infer_f32 failed ({rc})")
+        raise RuntimeError(f"{fn} failed ({rc})")
     return y
 
 

@@ -11,7 +11,8 @@
  * Reference files (all under /root/reference/crates/rwkv-nn/src/kernels/):
  *   wkv7_common/kernel.rs:6-114    forward kernel
  *   wkv7_common/kernel.rs:116-308  backward kernel
- *   wkv7_infer/kernel.rs:8-114     inference kernel and dither
+ *   wkv7_infer/kernel.rs:8-114     inference kernel and dither, with F = f32
+ *                                  and with F = bf16
  */
 #include "wkv7_oracle.h"
 
@@ -392,6 +393,85 @@ int wkv7o_infer_f32(int64_t Ba, int64_t T, int64_t H, int64_t N,
             row[i] = row[i] * sw[i] + removal_state * b[base + i] +
                      k[base + i] * vj;
             yy += row[i] * r[base + i];
+          }
+          y[base + j] = yy;
+        }
+        valid_t += 1u;
+      }
+    }
+  }
+  free(sw);
+  return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* inference with F = bf16, wkv7_infer/kernel.rs:15-114                      */
+/* ------------------------------------------------------------------------ */
+float wkv7o_round_bf16(float x) {
+  uint32_t u;
+  memcpy(&u, &x, sizeof u);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu) != 0u) {
+    u |= 0x00400000u; /* quiet NaN, payload kept in the upper half */
+  } else {
+    u += 0x7fffu + ((u >> 16) & 1u); /* ties to even; overflow goes to inf */
+  }
+  u &= 0xffff0000u;
+  memcpy(&x, &u, sizeof x);
+  return x;
+}
+
+/* One F = bf16 operation: the fp32 result of two bf16 operands, rounded to
+ * bf16. A product of two bf16 values is exact in fp32; a sum is rounded twice
+ * (fp32, then bf16), which equals one rounding because fp32 carries more than
+ * 2 * 8 + 2 significand bits. */
+#define BF(x) wkv7o_round_bf16(x)
+
+int wkv7o_infer_bf16(int64_t Ba, int64_t T, int64_t H, int64_t N,
+                     int64_t full_batch, const float *w, const float *r,
+                     const float *k, const float *v, const float *a,
+                     const float *b, const int32_t *batch_ids, float *state,
+                     const float *mask, const uint32_t *elapsed_t,
+                     int use_dither, float *y) {
+  if (bad_shape(Ba, T, H, N) || full_batch < 0) return -1;
+  for (int64_t bi = 0; bi < Ba; ++bi)
+    if (batch_ids[bi] < 0 || batch_ids[bi] >= full_batch) return -2;
+  float *sw = (float *)malloc(sizeof(float) * (size_t)N);
+  for (int64_t bi = 0; bi < Ba; ++bi) {
+    const int64_t slot = batch_ids[bi];
+    const uint32_t e_t = elapsed_t ? elapsed_t[slot] : 0u;
+    for (int64_t hi = 0; hi < H; ++hi) {
+      float *S = state + (slot * H + hi) * N * N;
+      uint32_t valid_t = 0;
+      for (int64_t t = 0; t < T; ++t) {
+        const int64_t base = tok(T, H, N, bi, t, hi);
+        /* kernel.rs:59-62: the mask is an F value compared with 0 */
+        if (mask && mask[bi * T + t] == 0.0f) {
+          for (int64_t j = 0; j < N; ++j) y[base + j] = 0.0f;
+          continue;
+        }
+        /* kernel.rs:71-78: decay in fp32, dither added in fp32, one cast to F */
+        for (int64_t i = 0; i < N; ++i) {
+          const float w_sig = 1.0f / (1.0f + expf(-w[base + i]));
+          float wd = expf(W_SCALE_F * w_sig);
+          if (use_dither) wd += wkv7o_dither(e_t + valid_t);
+          sw[i] = BF(wd);
+        }
+        for (int64_t j = 0; j < N; ++j) {
+          float *row = S + j * N;
+          /* kernel.rs:81-85: removal_state += removal[i] * state[i], in F */
+          float removal_state = 0.0f;
+          for (int64_t i = 0; i < N; ++i)
+            removal_state = BF(removal_state + BF(a[base + i] * row[i]));
+          const float vj = v[base + j];
+          float yy = 0.0f;
+          /* kernel.rs:90-96: state[i] * w[i] + removal_state * b[i] + k[i] * v,
+           * left to right, then y += state[i] * r[i], all in F */
+          for (int64_t i = 0; i < N; ++i) {
+            const float p0 = BF(row[i] * sw[i]);
+            const float p1 = BF(removal_state * b[base + i]);
+            const float p2 = BF(k[base + i] * vj);
+            row[i] = BF(BF(p0 + p1) + p2);
+            yy = BF(yy + BF(row[i] * r[base + i]));
           }
           y[base + j] = yy;
         }

@@ -70,6 +70,28 @@ int wkv7o_infer_f32(int64_t Ba, int64_t T, int64_t H, int64_t N,
                     const float *mask, const uint32_t *elapsed_t,
                     int use_dither, float *y);
 
+/* The reference's inference kernel with element type F = bf16
+ * (wkv7_infer/kernel.rs:15-114 instantiated at bf16, dither on per
+ * wkv7_infer/host.rs:157 when use_dither = 1). Every F-typed value is a bf16:
+ * the state read from and written back to the bf16 state buffer
+ * (kernel.rs:35-42, 110-113), the operands staged in F (kernel.rs:66-70), the
+ * decay computed in fp32 (plus the dither) and rounded to F once
+ * (kernel.rs:71-78), and each F product and sum of the removal-state sum, the
+ * state update and the output sum rounded to bf16, round to nearest even, in
+ * the kernel's evaluation order (kernel.rs:81-98). All arrays are float32
+ * holding bf16 values; `state` ([full_batch, H, N, N]) is updated in place and
+ * keeps holding bf16 values. mask ([Ba, T], NULL = all ones) and elapsed_t as
+ * for wkv7o_infer_f32. */
+int wkv7o_infer_bf16(int64_t Ba, int64_t T, int64_t H, int64_t N,
+                     int64_t full_batch, const float *w, const float *r,
+                     const float *k, const float *v, const float *a,
+                     const float *b, const int32_t *batch_ids, float *state,
+                     const float *mask, const uint32_t *elapsed_t,
+                     int use_dither, float *y);
+
+/* float32 -> nearest bf16 (ties to even), returned as float32. */
+float wkv7o_round_bf16(float x);
+
 /* deterministic_dither, wkv7_infer/kernel.rs:8-13. */
 float wkv7o_dither(uint32_t seed);
 

@@ -107,7 +107,8 @@ const char* wkv7_strerror(int status) {
     case WKV7_ERR_DTYPE: return "unknown dtype (expected WKV7_DTYPE_F32 or WKV7_DTYPE_BF16)";
     case WKV7_ERR_ALIGNMENT: return "tensor pointer is misaligned";
     case WKV7_ERR_OVERLAP: return "an output buffer overlaps another operand";
-    case WKV7_ERR_FLAGS: return "invalid flag value or flag/pointer mismatch";
+    case WKV7_ERR_FLAGS:
+      return "invalid flag value, flag/pointer mismatch, or dither asked for an fp32 state";
     case WKV7_ERR_HIP: return "HIP kernel launch failed";
     case WKV7_ERR_SCRATCH_LIMIT:
       return "the call needs more scratch memory than the library's fixed device array holds";
@@ -310,20 +311,26 @@ int wkv7_statetune_backward(const void* w, const void* r, const void* k, const v
 
 int wkv7_infer_forward(const void* weight_decay, const void* receptance, const void* key,
                        const void* value, const void* removal, const void* replacement,
-                       const int32_t* batch_ids, float* state, const void* context_mask,
+                       const int32_t* batch_ids, void* state, const void* context_mask,
                        const int32_t* elapsed_t, int64_t active_batch_size, int64_t context_len,
                        int64_t num_heads, int64_t head_size, int64_t full_batch_size, int dtype,
-                       int use_dither, void* output, void* stream) {
+                       int state_dtype, int use_dither, void* output, void* stream) {
   if (int rc = check_dtype(dtype)) return rc;
+  if (int rc = check_dtype(state_dtype)) return rc;
+  // a bf16 state is the reference's kernel at element type bf16: every
+  // operand is bf16 too
+  if (state_dtype == WKV7_DTYPE_BF16 && dtype != WKV7_DTYPE_BF16) return WKV7_ERR_DTYPE;
   if (head_size != kN) return WKV7_ERR_HEAD_SIZE;
   if (active_batch_size < 0 || context_len < 0 || num_heads < 0 || full_batch_size < 0 ||
       active_batch_size > kMaxGridDim || num_heads > kMaxGridDim || context_len > INT32_MAX ||
       full_batch_size > INT32_MAX || active_batch_size > full_batch_size)
     return WKV7_ERR_SHAPE;
   if (int rc = check_flag(use_dither)) return rc;
+  // the reference dithers only when the element type is not f32 (host.rs:157)
+  if (use_dither && state_dtype != WKV7_DTYPE_BF16) return WKV7_ERR_FLAGS;
   const int64_t toks_n = active_batch_size * context_len * num_heads * kN;
   const int64_t tok = toks_n * elem_bytes(dtype);
-  const int64_t st = full_batch_size * num_heads * kN * kN * 4;
+  const int64_t st = full_batch_size * num_heads * kN * kN * elem_bytes(state_dtype);
   const void* toks[6] = {weight_decay, receptance, key, value, removal, replacement};
   if (toks_n > 0) {
     for (const void* p : toks)
@@ -352,6 +359,7 @@ int wkv7_infer_forward(const void* weight_decay, const void* receptance, const v
 
   wkv7::InferDesc d;
   d.dtype = static_cast<wkv7::Dtype>(dtype);
+  d.state_dtype = static_cast<wkv7::Dtype>(state_dtype);
   d.Ba = static_cast<int>(active_batch_size);
   d.T = static_cast<int>(context_len);
   d.H = static_cast<int>(num_heads);

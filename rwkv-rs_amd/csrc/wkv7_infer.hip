@@ -2,20 +2,29 @@
 //
 // Semantics: /root/reference/crates/rwkv-nn/src/kernels/wkv7_infer/kernel.rs:15-114
 // (wkv7_infer_forward_kernel). Active row b works on state slot batch_ids[b]
-// of a [full_batch, H, 64, 64] fp32 state buffer, read and written in place
+// of a [full_batch, H, 64, 64] state buffer, read and written in place
 // (kernel.rs:27-42, 103-113). A step whose context_mask entry is 0 writes
-// y = 0 and leaves the state untouched (kernel.rs:57-62). With use_dither the
-// decay gets deterministic_dither(elapsed_t[slot] + valid_t) added, where
-// valid_t counts the unmasked steps of this call before the current one
-// (kernel.rs:8-13, 73-77). The state is always fp32 here; the reference's
-// dither is tied to a reduced-precision state element type, so callers that
-// want its arithmetic pass use_dither explicitly.
+// y = 0 and leaves the state untouched (kernel.rs:57-62). With use_dither
+// (bf16 state only) the decay gets deterministic_dither(elapsed_t[slot] +
+// valid_t) added, where valid_t counts the unmasked steps of this call before
+// the current one (kernel.rs:8-13, 73-77).
 //
-// Design: the forward kernel's thread layout and per-step arithmetic (one
-// workgroup per (active row, head), a 2x4 state block per thread in VGPRs,
-// operands from LDS). At T = 1 the kernel is bound by the 16 KiB state read
-// and 16 KiB state write per (row, head): every thread moves two 16-byte rows
-// each way, and the grid has Ba*H workgroups.
+// Two state element types, as the reference's kernel is instantiated:
+// - fp32 state (wkv7_infer_kernel): the reference at F = f32, which runs
+//   without the dither (host.rs:157); bf16 operands are carried as their
+//   exact fp32 values.
+// - bf16 state (wkv7_infer_bf16_kernel): the reference at F = bf16. The
+//   state, the staged operands and every product and sum are bf16: the decay
+//   is formed in fp32, gets the dither, and is rounded to bf16 once
+//   (kernel.rs:71-78); the removal-state sum, the state update and the output
+//   sum round each operation to bf16 in the kernel's order (kernel.rs:81-98),
+//   summing over the key index left to right.
+//
+// Design of the fp32-state kernel: the forward kernel's thread layout and
+// per-step arithmetic (one workgroup per (active row, head), a 2x4 state
+// block per thread in VGPRs, operands from LDS). At T = 1 it is bound by the
+// 16 KiB state read and 16 KiB state write per (row, head): every thread
+// moves two 16-byte rows each way, and the grid has Ba*H workgroups.
 #include "wkv7_device.hpp"
 #include "wkv7_launch.hpp"
 
@@ -39,9 +48,8 @@ struct InferParams {
   const int32_t* batch_ids;
   float* state;
   const Tin* mask;
-  const int32_t* elapsed_t;
   Tin* y;
-  int T, H, full_batch, use_dither;
+  int T, H, full_batch;
 };
 
 template <typename Tin>
@@ -79,7 +87,6 @@ __global__ __launch_bounds__(kThreads) void wkv7_infer_kernel(InferParams<Tin> p
     }
     return;
   }
-  const uint32_t elapsed = p.elapsed_t ? (uint32_t)p.elapsed_t[slot] : 0u;
   const int64_t tstride = (int64_t)p.H * kHead;
   const int64_t tok0 = ((int64_t)bi * T * p.H + h) * kHead;
 
@@ -94,21 +101,12 @@ __global__ __launch_bounds__(kThreads) void wkv7_infer_kernel(InferParams<Tin> p
 
   typedef Io<Tin> io;
   typename io::raw pre[V_COUNT];
-  uint32_t valid_before_tile = 0;
   bool pre_live = true;
-  uint32_t pre_vt = 0;   // unmasked steps before this thread's staged step
 
   auto gload = [&](int t0) {
     const int t = t0 + sl;
     if (stager && t < T) {
       pre_live = !p.mask || mask_on<Tin>(p.mask, (int64_t)bi * T + t);
-      uint32_t vt = valid_before_tile;
-      if (p.mask) {
-        for (int u = t0; u < t; ++u) vt += mask_on<Tin>(p.mask, (int64_t)bi * T + u) ? 1u : 0u;
-      } else {
-        vt += (uint32_t)(t - t0);
-      }
-      pre_vt = vt;
       const int64_t off = tok0 + (int64_t)t * tstride + 4 * pp;
       pre[V_W] = io::load(p.w + off);
       pre[V_R] = io::load(p.r + off);
@@ -121,11 +119,10 @@ __global__ __launch_bounds__(kThreads) void wkv7_infer_kernel(InferParams<Tin> p
   auto lstore = [&](int buf, int t0) {
     if (stager && t0 + sl < T) {
       float4 x = io::widen(pre[V_W]);
-      const float dith = p.use_dither ? dither_f(elapsed + pre_vt) : 0.0f;
-      x.x = decay_f(sigmoid_f(x.x)) + dith;
-      x.y = decay_f(sigmoid_f(x.y)) + dith;
-      x.z = decay_f(sigmoid_f(x.z)) + dith;
-      x.w = decay_f(sigmoid_f(x.w)) + dith;
+      x.x = decay_f(sigmoid_f(x.x));
+      x.y = decay_f(sigmoid_f(x.y));
+      x.z = decay_f(sigmoid_f(x.z));
+      x.w = decay_f(sigmoid_f(x.w));
       tile[buf][V_W][sl][pp] = x;
       tile[buf][V_R][sl][pp] = io::widen(pre[V_R]);
       tile[buf][V_K][sl][pp] = io::widen(pre[V_K]);
@@ -134,12 +131,6 @@ __global__ __launch_bounds__(kThreads) void wkv7_infer_kernel(InferParams<Tin> p
       tile[buf][V_B][sl][pp] = io::widen(pre[V_B]);
       if (pp == 0) live[buf][sl] = pre_live ? 1 : 0;
     }
-  };
-  auto count_live = [&](int t0, int nst) {
-    if (!p.mask) return (uint32_t)nst;
-    uint32_t n = 0;
-    for (int u = 0; u < nst; ++u) n += mask_on<Tin>(p.mask, (int64_t)bi * T + t0 + u) ? 1u : 0u;
-    return n;
   };
 
   const int ntiles = (T + kTile - 1) / kTile;
@@ -153,7 +144,6 @@ __global__ __launch_bounds__(kThreads) void wkv7_infer_kernel(InferParams<Tin> p
     const int buf = ti & 1;
     const int t0 = ti * kTile;
     const int nst = min(kTile, T - t0);
-    valid_before_tile += count_live(t0, nst);
     if (ti + 1 < ntiles) gload(t0 + kTile);
 
     for (int s = 0; s < nst; ++s) {
@@ -181,6 +171,169 @@ __global__ __launch_bounds__(kThreads) void wkv7_infer_kernel(InferParams<Tin> p
   *reinterpret_cast<float4*>(st + rt * kHead) = make_float4(St[0], St[1], St[2], St[3]);
 }
 
+// ------------------------------------------------------------ bf16 state
+// One wave per (active row, head); lane j owns value row j of the state, so
+// each row's sums over the key index run left to right inside one lane, as
+// the reference's thread j does (kernel.rs:81-96). The row is held as 64
+// fp32 registers carrying bf16 values. The step's key-indexed operands (the
+// rounded decay, a, b, k, r) go through LDS as fp32 and are read back as
+// broadcasts; lane j keeps its own v_j. The 8 KiB state moves between HBM and
+// the lanes' rows through LDS, with coalesced 16-byte accesses on the HBM
+// side and each row's 16-byte pieces rotated by row + row / 8 so that neither
+// the row-per-lane reads nor the contiguous writes conflict on LDS banks.
+struct InferBf16Params {
+  const bf16_t *w, *r, *k, *v, *a, *b;
+  const int32_t* batch_ids;
+  bf16_t* state;
+  const bf16_t* mask;
+  const int32_t* elapsed_t;
+  bf16_t* y;
+  int T, H, full_batch, use_dither;
+};
+
+// one bf16 operation: an fp32 result of bf16 operands rounded to bf16 (ties
+// to even). Products of two bf16 values are exact in fp32, and a sum rounded
+// to fp32 and then to bf16 equals the sum rounded once (fp32 carries more
+// than twice bf16's significand bits plus two).
+__device__ __forceinline__ float rb(float x) { return (float)(__bf16)x; }
+
+__device__ __forceinline__ int rot_piece(int row, int q) { return row * 8 + ((q + row + (row >> 3)) & 7); }
+
+__global__ __launch_bounds__(64) void wkv7_infer_bf16_kernel(InferBf16Params p) {
+  __shared__ uint4 srow[kHead * 8];      // the state, 8 pieces of 16 bytes per row
+  __shared__ float4 ops[5][kHead / 4];   // rounded decay, a, b, k, r of the step
+  enum { O_W = 0, O_A, O_B, O_K, O_R };
+
+  const int h = blockIdx.x, bi = blockIdx.y;
+  const int lane = threadIdx.x;
+  const int T = p.T;
+  const int64_t tstride = (int64_t)p.H * kHead;
+  const int64_t tok0 = ((int64_t)bi * T * p.H + h) * kHead + lane;
+  const int64_t slot = p.batch_ids[bi];
+  // an out-of-range slot is refused: zero output, no state touched
+  if (slot < 0 || slot >= p.full_batch) {
+    for (int t = 0; t < T; ++t) p.y[tok0 + (int64_t)t * tstride] = 0;
+    return;
+  }
+  uint4* st = reinterpret_cast<uint4*>(p.state + (slot * p.H + h) * (kHead * kHead));
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    const int u = m * 64 + lane;
+    srow[rot_piece(u >> 3, u & 7)] = st[u];
+  }
+  __syncthreads();
+  float s[kHead];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const uint4 x = srow[rot_piece(lane, q)];
+    const uint32_t wds[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      s[8 * q + 2 * e] = __uint_as_float(wds[e] << 16);
+      s[8 * q + 2 * e + 1] = __uint_as_float(wds[e] & 0xffff0000u);
+    }
+  }
+
+  const uint32_t elapsed = p.elapsed_t ? (uint32_t)p.elapsed_t[slot] : 0u;
+  uint32_t valid_t = 0;
+  float* opf = reinterpret_cast<float*>(ops);
+  // operands of step t, loaded one step ahead
+  bool nlive = false;
+  bf16_t nw = 0, na = 0, nb = 0, nk = 0, nr = 0, nv = 0;
+  auto fetch = [&](int t) {
+    nlive = !p.mask || (p.mask[(int64_t)bi * T + t] & 0x7fffu) != 0u;
+    if (nlive) {
+      const int64_t off = tok0 + (int64_t)t * tstride;
+      nw = p.w[off]; na = p.a[off]; nb = p.b[off]; nk = p.k[off]; nr = p.r[off]; nv = p.v[off];
+    }
+  };
+  if (T > 0) fetch(0);
+  for (int t = 0; t < T; ++t) {
+    const int64_t off = tok0 + (int64_t)t * tstride;
+    const bool live = nlive;
+    const bf16_t cw = nw, ca = na, cb = nb, ck = nk, cr = nr, cv = nv;
+    if (t + 1 < T) fetch(t + 1);
+    if (!live) {   // uniform: the mask entry is one per (row, step)
+      p.y[off] = 0;
+      continue;
+    }
+    float wd = decay_f(sigmoid_f(bf16_to_f32(cw)));
+    if (p.use_dither) wd += dither_f(elapsed + valid_t);
+    __syncthreads();   // the previous step's reads of ops are done
+    opf[O_W * kHead + lane] = rb(wd);
+    opf[O_A * kHead + lane] = bf16_to_f32(ca);
+    opf[O_B * kHead + lane] = bf16_to_f32(cb);
+    opf[O_K * kHead + lane] = bf16_to_f32(ck);
+    opf[O_R * kHead + lane] = bf16_to_f32(cr);
+    const float vj = bf16_to_f32(cv);
+    __syncthreads();
+    float sa = 0.0f;
+#pragma unroll
+    for (int i4 = 0; i4 < kHead / 4; ++i4) {
+      const float4 a4 = ops[O_A][i4];
+      sa = rb(sa + rb(a4.x * s[4 * i4 + 0]));
+      sa = rb(sa + rb(a4.y * s[4 * i4 + 1]));
+      sa = rb(sa + rb(a4.z * s[4 * i4 + 2]));
+      sa = rb(sa + rb(a4.w * s[4 * i4 + 3]));
+    }
+    float y = 0.0f;
+#pragma unroll
+    for (int i4 = 0; i4 < kHead / 4; ++i4) {
+      const float4 w4 = ops[O_W][i4], b4 = ops[O_B][i4], k4 = ops[O_K][i4], r4 = ops[O_R][i4];
+      const float wv[4] = {w4.x, w4.y, w4.z, w4.w}, bv[4] = {b4.x, b4.y, b4.z, b4.w};
+      const float kv[4] = {k4.x, k4.y, k4.z, k4.w}, rv[4] = {r4.x, r4.y, r4.z, r4.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float& si = s[4 * i4 + e];
+        si = rb(rb(rb(si * wv[e]) + rb(sa * bv[e])) + rb(kv[e] * vj));
+        y = rb(y + rb(si * rv[e]));
+      }
+    }
+    p.y[off] = (bf16_t)(__float_as_uint(y) >> 16);
+    ++valid_t;
+  }
+
+  // write the rows back through LDS: coalesced 16-byte stores
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    uint4 x;
+    uint32_t* wds = reinterpret_cast<uint32_t*>(&x);
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      wds[e] = (__float_as_uint(s[8 * q + 2 * e]) >> 16) |
+               (__float_as_uint(s[8 * q + 2 * e + 1]) & 0xffff0000u);
+    srow[rot_piece(lane, q)] = x;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    const int u = m * 64 + lane;
+    st[u] = srow[rot_piece(u >> 3, u & 7)];
+  }
+}
+
+hipError_t launch_infer_bf16(const InferDesc& d, hipStream_t stream) {
+  InferBf16Params p;
+  p.w = static_cast<const bf16_t*>(d.w);
+  p.r = static_cast<const bf16_t*>(d.r);
+  p.k = static_cast<const bf16_t*>(d.k);
+  p.v = static_cast<const bf16_t*>(d.v);
+  p.a = static_cast<const bf16_t*>(d.a);
+  p.b = static_cast<const bf16_t*>(d.b);
+  p.batch_ids = d.batch_ids;
+  p.state = static_cast<bf16_t*>(d.state);
+  p.mask = static_cast<const bf16_t*>(d.context_mask);
+  p.elapsed_t = d.elapsed_t;
+  p.y = static_cast<bf16_t*>(d.y);
+  p.T = d.T;
+  p.H = d.H;
+  p.full_batch = d.full_batch;
+  p.use_dither = d.use_dither;
+  hipLaunchKernelGGL(wkv7_infer_bf16_kernel, dim3(d.H, d.Ba, 1), dim3(64, 1, 1), 0, stream, p);
+  return hipGetLastError();
+}
+
 template <typename Tin>
 hipError_t launch_infer_t(const InferDesc& d, hipStream_t stream) {
   InferParams<Tin> p;
@@ -191,14 +344,12 @@ hipError_t launch_infer_t(const InferDesc& d, hipStream_t stream) {
   p.a = static_cast<const Tin*>(d.a);
   p.b = static_cast<const Tin*>(d.b);
   p.batch_ids = d.batch_ids;
-  p.state = d.state;
+  p.state = static_cast<float*>(d.state);
   p.mask = static_cast<const Tin*>(d.context_mask);
-  p.elapsed_t = d.elapsed_t;
   p.y = static_cast<Tin*>(d.y);
   p.T = d.T;
   p.H = d.H;
   p.full_batch = d.full_batch;
-  p.use_dither = d.use_dither;
   const dim3 grid(d.H, d.Ba, 1), block(kThreads, 1, 1);
   if (d.T == 1)
     hipLaunchKernelGGL((wkv7_infer_kernel<Tin, 1>), grid, block, 0, stream, p);
@@ -211,6 +362,7 @@ hipError_t launch_infer_t(const InferDesc& d, hipStream_t stream) {
 
 hipError_t launch_infer(const InferDesc& d, hipStream_t stream) {
   if (d.Ba == 0 || d.H == 0) return hipSuccess;
+  if (d.state_dtype == Dtype::BF16) return launch_infer_bf16(d, stream);
   return d.dtype == Dtype::BF16 ? launch_infer_t<bf16_t>(d, stream) : launch_infer_t<float>(d, stream);
 }
 

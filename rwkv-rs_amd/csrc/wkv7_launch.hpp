@@ -40,10 +40,11 @@ struct BackwardDesc {
 // (wkv7_infer/host.rs:27-187).
 struct InferDesc {
   Dtype dtype;
+  Dtype state_dtype;            // fp32, or bf16 (then dtype is bf16 too)
   int Ba, T, H, full_batch;
   const void *w, *r, *k, *v, *a, *b;   // [Ba,T,H,64] in dtype
   const int32_t* batch_ids;     // [Ba], values in [0, full_batch)
-  float* state;                 // [full_batch,H,64,64], updated in place
+  void* state;                  // [full_batch,H,64,64] in state_dtype, updated in place
   const void* context_mask;     // [Ba,T] in dtype, or nullptr (all ones)
   const int32_t* elapsed_t;     // [full_batch] (read as u32), or nullptr
   int use_dither;

@@ -580,10 +580,14 @@ class AutoRegressiveModel(nn.Module):
         N = self.cells.cells[0].time_mixer.head_size
         n = len(self.cells.cells)
 
-        def z(*shape):
-            return torch.zeros(*shape, dtype=torch.float32, device=device)
+        # the WKV7 state has the operator's element type, as the reference
+        # keeps it in its backend's float type (wkv7_infer/kernel.rs:35-42)
+        state_dtype = self.cells.cells[0].time_mixer.wkv7_dtype
+
+        def z(*shape, dtype=torch.float32):
+            return torch.zeros(*shape, dtype=dtype, device=device)
         return InferState([z(full_batch_size, C) for _ in range(n)],
-                          [z(full_batch_size, H, N, N) for _ in range(n)],
+                          [z(full_batch_size, H, N, N, dtype=state_dtype) for _ in range(n)],
                           [z(full_batch_size, C) for _ in range(n)],
                           torch.zeros(full_batch_size, dtype=torch.int32, device=device))
 
@@ -604,8 +608,7 @@ class AutoRegressiveModel(nn.Module):
         B, T = contexts.shape
         if T == 0:
             raise ValueError("contexts must be non-empty")
-        ops32 = self.cells.cells[0].time_mixer.wkv7_dtype == torch.float32
-        kernel = _wkv7.KernelInfer if ops32 else _DitheredInfer
+        kernel = _wkv7.KernelInfer
         x = self.layer_norm_for_first_cell(self.embed(contexts))
         x, st, state, sc = self.cells(x, batch_ids, kernel, infer_state.elapsed_t, context_mask,
                                       infer_state.shift_time, infer_state.state,
@@ -640,8 +643,9 @@ class InferState:
     """The per-slot buffers of a serving loop (examples/rwkv-lm/src/
     inferring.rs:100-180): for each cell the time- and channel-mix token
     shifts ([full_batch, C], fp32) and the WKV7 state ([full_batch, H, 64,
-    64], fp32), and each slot's elapsed_t (int32), the dither seed's step
-    count."""
+    64], in the operator's element type: bf16 for bf16 operands, where the
+    decode kernel runs the reference's bf16 arithmetic and its dither), and
+    each slot's elapsed_t (int32), the dither seed's step count."""
     shift_time: List[torch.Tensor]
     state: List[torch.Tensor]
     shift_channel: List[torch.Tensor]
@@ -667,16 +671,6 @@ class InferState:
         for t in self.shift_time + self.state + self.shift_channel:
             t[slot].zero_()
         self.elapsed_t[slot] = 0
-
-
-class _DitheredInfer:
-    """KernelInfer with the dither on: the reference dithers the decay when
-    the operands are not fp32 (wkv7_infer/host.rs:157)."""
-
-    @staticmethod
-    def forward(input, state, batch_ids, elapsed_t, chunk_len, context_mask):
-        return _wkv7.KernelInfer.forward(input, state, batch_ids, elapsed_t, chunk_len,
-                                         context_mask, use_dither=True)
 
 
 UNEMBED_MODES = ("skip", "last", "full")

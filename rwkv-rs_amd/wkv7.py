@@ -281,18 +281,29 @@ def wkv7_statetune_backward(weight_decay, receptance, key, value, removal, repla
 # ---------------------------------------------------- Wkv7InferBackend (mirror)
 def wkv7_infer_forward(weight_decay, receptance, key, value, removal, replacement, batch_ids,
                        initial_state, context_mask, elapsed_t,
-                       use_dither: bool = False) -> Wkv7InferForwardOutput:
-    """wkv7_infer/mod.rs:58-82. ``initial_state`` ([full_batch, H, 64, 64],
-    float32) is updated in place and returned as ``final_state``, like the
-    reference's aliasing (wkv7_infer/host.rs:151). ``use_dither`` replaces the
-    reference's "element type is not f32" switch (host.rs:157): the state here
-    is always float32."""
+                       use_dither: Optional[bool] = None) -> Wkv7InferForwardOutput:
+    """wkv7_infer/mod.rs:58-82. ``initial_state`` ([full_batch, H, 64, 64])
+    is updated in place and returned as ``final_state``, like the reference's
+    aliasing (wkv7_infer/host.rs:151). Its dtype picks the reference kernel's
+    element type: float32 (operands float32 or bfloat16, used as exact fp32
+    values) or bfloat16 (operands bfloat16; the state and every operation of
+    the step in bf16). ``use_dither`` defaults to the reference's switch,
+    "element type is not f32" (host.rs:157), i.e. on for a bfloat16 state; a
+    float32 state cannot be dithered."""
     w, r, k, v, a, b = _tokens(weight_decay, receptance, key, value, removal, replacement)
     Ba, T, H, N = w.shape
     dev = w.device
-    if initial_state.dtype != torch.float32 or not initial_state.is_contiguous() \
-            or initial_state.device != dev:
-        raise ValueError("initial_state must be a contiguous float32 tensor on the operands' device")
+    if initial_state.dtype not in (torch.float32, torch.bfloat16) \
+            or not initial_state.is_contiguous() or initial_state.device != dev:
+        raise ValueError("initial_state must be a contiguous float32 or bfloat16 tensor on the "
+                         "operands' device")
+    if initial_state.dtype == torch.bfloat16 and w.dtype != torch.bfloat16:
+        raise TypeError("a bfloat16 state needs bfloat16 operands (the reference kernel at "
+                        "element type bf16)")
+    if use_dither is None:
+        use_dither = initial_state.dtype != torch.float32
+    if use_dither and initial_state.dtype == torch.float32:
+        raise ValueError("the dither applies to a bfloat16 state only (wkv7_infer/host.rs:157)")
     full_batch = initial_state.shape[0]
     if tuple(initial_state.shape[1:]) != (H, N, N):
         raise ValueError("initial_state must be [full_batch, num_heads, 64, 64]")
@@ -312,7 +323,8 @@ def wkv7_infer_forward(weight_decay, receptance, key, value, removal, replacemen
     output = torch.empty_like(w)
     _native.call("wkv7_infer_forward", _ptr(w), _ptr(r), _ptr(k), _ptr(v), _ptr(a), _ptr(b),
                  _ptr(ids), _ptr(initial_state), _ptr(mask), _ptr(et), Ba, T, H, N, full_batch,
-                 _dtype_code(w), int(bool(use_dither)), _ptr(output), _stream(dev))
+                 _dtype_code(w), _dtype_code(initial_state), int(bool(use_dither)), _ptr(output),
+                 _stream(dev))
     return Wkv7InferForwardOutput(output=output, final_state=initial_state)
 
 
@@ -435,7 +447,7 @@ class KernelInfer:
 
     @staticmethod
     def forward(input: Wkv7ForwardInput, state, batch_ids, elapsed_t, chunk_len,
-                context_mask, use_dither: bool = False) -> KernelOutput:
+                context_mask, use_dither: Optional[bool] = None) -> KernelOutput:
         if state is None:
             raise ValueError("initial_state required")
         if elapsed_t is None:

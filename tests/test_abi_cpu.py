@@ -49,7 +49,7 @@ def test_library_exports_every_declared_symbol(native):
 
 def test_version_and_strings(native):
     lib = native.lib()
-    assert lib.wkv7_abi_version() == 1
+    assert lib.wkv7_abi_version() == 2
     assert lib.wkv7_strerror(3).decode() == "chunk_len must divide sequence length"
     assert lib.wkv7_strerror(4).decode() == "head_size must be 64"
     assert lib.wkv7_strerror(123).decode() == "unknown wkv7 status"
@@ -124,20 +124,26 @@ def test_infer_validation(native):
 
     def inf(**over):
         a = dict(ids=FAKE * 10, state=FAKE * 20, mask=None, et=None, Ba=2, T=1, H=4, N=64,
-                 full=4, dtype=1, dither=0, y=FAKE * 30)
+                 full=4, dtype=1, sdtype=0, dither=0, y=FAKE * 30)
         a.update(over)
         return lib.wkv7_infer_forward(FAKE, FAKE * 2, FAKE * 3, FAKE * 4, FAKE * 5, FAKE * 6,
                                       a["ids"], a["state"], a["mask"], a["et"], a["Ba"], a["T"],
-                                      a["H"], a["N"], a["full"], a["dtype"], a["dither"], a["y"],
-                                      None)
+                                      a["H"], a["N"], a["full"], a["dtype"], a["sdtype"],
+                                      a["dither"], a["y"], None)
     assert inf(N=16) == 4
     assert inf(Ba=5) == 2             # more active rows than slots
     assert inf(ids=None) == 1
-    assert inf(dither=1) == 1         # elapsed_t required for the dither
+    assert inf(sdtype=1, dither=1) == 1   # elapsed_t required for the dither
     assert inf(dither=3) == 8
+    # the reference dithers only a reduced-precision element type (host.rs:157)
+    assert inf(dither=1, et=FAKE * 40) == 8
+    assert inf(sdtype=1, dtype=0) == 5    # a bf16 state needs bf16 operands
+    assert inf(sdtype=2) == 5
     assert inf(y=FAKE * 3) == 7       # output aliases key
     assert inf(state=FAKE) == 7       # state aliases weight_decay
+    assert inf(state=FAKE * 20 + 8) == 6   # the state needs 16-byte alignment
     assert inf(Ba=0) == 0
+    assert inf(Ba=0, sdtype=1) == 0
 
 
 def test_python_mirror_checks_chunk_len_before_the_gpu():

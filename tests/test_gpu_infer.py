@@ -18,31 +18,126 @@ def wk():
     return load_pkg().wkv7
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("dither", [False, True])
-def test_decode_step_slot_mapped(wk, oracle, dtype, dither):
-    announce("infer T=1", dtype, dither)
+def bf16_state_close(got, want):
+    """The bf16-state kernel against the bf16 oracle: the same bf16
+    operations in the same order. Only the fp32 decay (exp, division) could
+    differ, where the GPU's and the host's fp32 exp land on different sides of
+    a bf16 rounding point; on these seeded inputs they do not, and the tests
+    require bit-identical results. Returns the fraction of identical elements
+    and the relative L2 error."""
+    got = np.asarray(got, np.float32)
+    want = np.asarray(want, np.float32)
+    same = float(np.mean(got.view(np.uint32) == want.view(np.uint32)))
+    return same, rel_l2(got, want)
+
+
+@pytest.mark.parametrize("dtype,state_dtype", [(torch.float32, torch.float32),
+                                               (torch.bfloat16, torch.float32),
+                                               (torch.bfloat16, torch.bfloat16)])
+def test_decode_step_slot_mapped(wk, oracle, dtype, state_dtype):
+    announce("infer T=1", dtype, state_dtype)
     pkg = load_pkg()
     Ba, H, full = 6, 5, 11
+    bf16_state = state_dtype == torch.bfloat16
     d = pkg.synthetic.make_inputs(Ba, 1, H, 64, seed=31, bf16=(dtype == torch.bfloat16))
     rng = np.random.default_rng(32)
     state = (rng.standard_normal((full, H, 64, 64)) * 0.1).astype(np.float32)
+    if bf16_state:
+        state = pkg.synthetic.bf16_round(state).reshape(state.shape)
     ids = np.array([7, 0, 3, 10, 5, 1], np.int32)
     elapsed = rng.integers(0, 1000, full).astype(np.int32)
-    st_gpu = to_dev(state)
+    st_gpu = to_dev(state, state_dtype)
     out = wk.wkv7_infer_forward(*(to_dev(d[n], dtype) for n in NAMES), torch.from_numpy(ids).cuda(),
-                                st_gpu, None, torch.from_numpy(elapsed).cuda(), use_dither=dither)
+                                st_gpu, None, torch.from_numpy(elapsed).cuda())
     st_ref = state.copy()
-    y_ref = oracle.infer_f32(*(d[n] for n in NAMES), ids, st_ref, None, elapsed.view(np.uint32),
-                             use_dither=dither)
-    tol = 1e-5 if dtype == torch.float32 else 1e-2
-    if dtype == torch.bfloat16:
-        y_ref = pkg.synthetic.bf16_round(y_ref)
-    assert rel_l2(to_np(out.output), y_ref) < tol
     assert out.final_state.data_ptr() == st_gpu.data_ptr()
-    assert rel_l2(to_np(st_gpu), st_ref) < 1e-5
     untouched = [s for s in range(full) if s not in ids]
+    if bf16_state:
+        # the reference at element type bf16, dither on (host.rs:157)
+        y_ref = oracle.infer_bf16(*(d[n] for n in NAMES), ids, st_ref, None,
+                                  elapsed.view(np.uint32))
+        same_y, err_y = bf16_state_close(to_np(out.output), y_ref)
+        same_s, err_s = bf16_state_close(to_np(st_gpu), st_ref)
+        print("bf16 state", same_y, err_y, same_s, err_s, flush=True)
+        assert same_y == 1.0 and same_s == 1.0, (err_y, err_s)
+    else:
+        y_ref = oracle.infer_f32(*(d[n] for n in NAMES), ids, st_ref, None)
+        tol = 1e-5 if dtype == torch.float32 else 1e-2
+        if dtype == torch.bfloat16:
+            y_ref = pkg.synthetic.bf16_round(y_ref)
+        assert rel_l2(to_np(out.output), y_ref) < tol
+        assert rel_l2(to_np(st_gpu), st_ref) < 1e-5
     np.testing.assert_array_equal(to_np(st_gpu)[untouched], state[untouched])
+
+
+def test_bf16_state_prefill_with_mask_and_dither(wk, oracle):
+    """The reference at element type bf16 over a ragged, left-padded prefill
+    (the per-step kernel path with T > 1): bf16 state, decay rounded after the
+    dither, seeds elapsed_t + valid steps."""
+    announce("infer bf16 state prefill")
+    pkg = load_pkg()
+    Ba, T, H, full = 3, 37, 2, 5
+    d = pkg.synthetic.make_inputs(Ba, T, H, 64, seed=38, bf16=True)
+    rng = np.random.default_rng(39)
+    mask = (rng.random((Ba, T)) < 0.8).astype(np.float32)
+    mask[0, :5] = 0.0
+    state = pkg.synthetic.bf16_round(
+        (rng.standard_normal((full, H, 64, 64)) * 0.1).astype(np.float32)).reshape(full, H, 64, 64)
+    ids = np.array([4, 0, 2], np.int32)
+    elapsed = np.array([5, 17, 0, 9, 1 << 30], np.int32)
+    st_gpu = to_dev(state, torch.bfloat16)
+    out = wk.wkv7_infer_forward(*(to_dev(d[n], torch.bfloat16) for n in NAMES),
+                                torch.from_numpy(ids).cuda(), st_gpu, to_dev(mask, torch.bfloat16),
+                                torch.from_numpy(elapsed).cuda())
+    st_ref = state.copy()
+    y_ref = oracle.infer_bf16(*(d[n] for n in NAMES), ids, st_ref, mask, elapsed.view(np.uint32))
+    y = to_np(out.output)
+    assert np.all(y[mask == 0] == 0.0)
+    same_y, err_y = bf16_state_close(y, y_ref)
+    same_s, err_s = bf16_state_close(to_np(st_gpu), st_ref)
+    print("bf16 state prefill", same_y, err_y, same_s, err_s, flush=True)
+    assert same_y == 1.0 and same_s == 1.0, (err_y, err_s)
+    np.testing.assert_array_equal(to_np(st_gpu)[[1, 3]], state[[1, 3]])
+
+
+def test_config3_decode_bf16_state(wk, oracle):
+    """config[3]'s shape (256 sequences, one step, H = 40) on the reference's
+    bf16 instantiation: bf16 state ~ N(0, 0.1) rounded to bf16, dither on,
+    slots a permutation of a 320-slot buffer."""
+    announce("config[3] decode, bf16 state")
+    pkg = load_pkg()
+    Ba, H, full = 256, 40, 320
+    d = pkg.synthetic.make_inputs(Ba, 1, H, 64, seed=0x5EED0003, bf16=True, with_grad=False)
+    rng = np.random.default_rng(0x5EED0013)
+    state = pkg.synthetic.bf16_round(
+        rng.standard_normal((full, H, 64, 64), dtype=np.float32) * np.float32(0.1)
+    ).reshape(full, H, 64, 64)
+    ids = rng.permutation(full)[:Ba].astype(np.int32)
+    elapsed = rng.integers(0, 1 << 20, full).astype(np.int32)
+    st_gpu = to_dev(state, torch.bfloat16)
+    out = wk.wkv7_infer_forward(*(to_dev(d[n], torch.bfloat16) for n in NAMES),
+                                torch.from_numpy(ids).cuda(), st_gpu, None,
+                                torch.from_numpy(elapsed).cuda())
+    torch.cuda.synchronize()
+    st_ref = state.copy()
+    y_ref = oracle.infer_bf16(*(d[n] for n in NAMES), ids, st_ref, None, elapsed.view(np.uint32))
+    got = to_np(st_gpu)
+    same_y, err_y = bf16_state_close(to_np(out.output), y_ref)
+    same_s, err_s = bf16_state_close(got[ids], st_ref[ids])
+    print("config[3] bf16 state", same_y, err_y, same_s, err_s, flush=True)
+    assert same_y == 1.0 and same_s == 1.0, (err_y, err_s)
+    untouched = np.setdiff1d(np.arange(full), ids)
+    np.testing.assert_array_equal(got[untouched], state[untouched])
+
+
+def test_dither_with_an_fp32_state_is_refused(wk):
+    # the reference dithers only when its element type is not f32 (host.rs:157)
+    ins = [torch.zeros(1, 1, 1, 64, device="cuda") for _ in NAMES]
+    st = torch.zeros(1, 1, 64, 64, device="cuda")
+    et = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ids = torch.zeros(1, dtype=torch.int32, device="cuda")
+    with pytest.raises(ValueError, match="dither"):
+        wk.wkv7_infer_forward(*ins, ids, st, None, et, use_dither=True)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
@@ -112,22 +207,24 @@ def test_config3_decode_at_full_size(wk, oracle):
 
 
 def test_masked_padding_is_a_noop(wk):
-    # wkv7_infer/mod.rs:189-230 at N=64: left padding with masked steps gives the
-    # unpadded outputs and state, dither on.
+    # wkv7_infer/mod.rs:189-230 at N=64 on the reference's bf16 instantiation
+    # (dither on): left padding with masked steps gives the unpadded outputs
+    # and state bit for bit.
     announce("infer padding no-op")
     pkg = load_pkg()
     H = 3
-    d = pkg.synthetic.make_inputs(1, 6, H, 64, seed=35)
-    pad = pkg.synthetic.make_inputs(1, 2, H, 64, seed=36)
+    d = pkg.synthetic.make_inputs(1, 6, H, 64, seed=35, bf16=True)
+    pad = pkg.synthetic.make_inputs(1, 2, H, 64, seed=36, bf16=True)
     padded = {n: np.concatenate([pad[n], d[n]], 1) for n in NAMES}
     mask_p = np.array([[0, 0, 1, 1, 1, 1, 1, 1]], np.float32)
     et = torch.tensor([17], dtype=torch.int32, device="cuda")
     ids = torch.tensor([0], dtype=torch.int32, device="cuda")
-    s_u = torch.zeros(1, H, 64, 64, device="cuda")
-    s_p = torch.zeros(1, H, 64, 64, device="cuda")
-    y_u = wk.wkv7_infer_forward(*(to_dev(d[n]) for n in NAMES), ids, s_u, None, et, use_dither=True).output
-    y_p = wk.wkv7_infer_forward(*(to_dev(padded[n]) for n in NAMES), ids, s_p, to_dev(mask_p), et,
-                                use_dither=True).output
+    s_u = torch.zeros(1, H, 64, 64, device="cuda", dtype=torch.bfloat16)
+    s_p = torch.zeros(1, H, 64, 64, device="cuda", dtype=torch.bfloat16)
+    bf = torch.bfloat16
+    y_u = wk.wkv7_infer_forward(*(to_dev(d[n], bf) for n in NAMES), ids, s_u, None, et).output
+    y_p = wk.wkv7_infer_forward(*(to_dev(padded[n], bf) for n in NAMES), ids, s_p,
+                                to_dev(mask_p, bf), et).output
     assert torch.all(y_p[:, :2] == 0)
     assert torch.equal(y_p[:, 2:], y_u)
     assert torch.equal(s_p, s_u)
@@ -148,7 +245,8 @@ def test_decode_matches_forward_step(wk):
 
 
 def test_decode_step_replays_from_a_captured_graph(wk):
-    """A serving loop captures its decode step once and replays it: the
+    """A serving loop captures its decode step once and replays it (here the
+    reference's bf16 instantiation: bf16 state, dither seeded from elapsed_t): the
     entry point enqueues one kernel on the caller's stream and neither
     allocates nor clears memory, so it can sit in a HIP graph. Four replays,
     each after new tokens are copied into the captured inputs, against the
@@ -161,7 +259,7 @@ def test_decode_step_replays_from_a_captured_graph(wk):
     dev = torch.device("cuda:0")
     ids = torch.tensor([5, 0, 2, 3], dtype=torch.int32, device=dev)
     gen = torch.Generator().manual_seed(41)
-    state = (torch.randn(full, H, 64, 64, generator=gen) * 0.1).to(dev)
+    state = (torch.randn(full, H, 64, 64, generator=gen) * 0.1).to(dev, torch.bfloat16)
     elapsed = torch.randint(0, 100, (full,), generator=gen, dtype=torch.int32).to(dev)
 
     def fresh(seed):
@@ -171,7 +269,7 @@ def test_decode_step_replays_from_a_captured_graph(wk):
     static_in = fresh(50)
 
     def step(ins, st, el):
-        out = wk.wkv7_infer_forward(*ins, ids, st, None, el, use_dither=True)
+        out = wk.wkv7_infer_forward(*ins, ids, st, None, el)   # bf16 state: dither on
         el[ids.long()] += 1
         return out.output
 

@@ -1,7 +1,7 @@
 """GPU tests of the model's serving path (``AutoRegressiveModel.infer``, the
 mirror of examples/rwkv-lm/src/model.rs:184-300 with the buffers and
 elapsed_t bookkeeping of inferring.rs:61-87, 100-180), on the decode kernel
-and the fused neighbour ops, fp32 operands:
+and the fused neighbour ops, fp32 operands (and one bf16 case):
 
 * a whole prompt through ``infer`` gives the training path's logits (the
   chunked pretrain kernel from a zero state), within 1e-5 relative L2;
@@ -110,3 +110,39 @@ def test_slot_mapped_batch_with_left_padding(neighbor_ops):
         for slot in (0, 2, 4):
             assert torch.equal(x[slot], y[slot])
     assert st.elapsed_t.tolist() == [0, 11, 0, 16, 0]
+
+
+@torch.no_grad()
+def test_bf16_operator_serves_with_a_bf16_state_and_the_dither():
+    """With bf16 operands the serving path runs the reference's decode at
+    element type bf16 (wkv7_infer/kernel.rs at F = bf16, dither on per
+    host.rs:157): the per-slot WKV7 state is bf16; prefill then token-by-token
+    decode matches one call to bf16 rounding (the per-token operands are the
+    same; only the row count of the matrix products differs); and the dither
+    is live: the same prompt from a different elapsed_t leaves another state."""
+    model = tiny_model(seed=3, std=0.2, neighbor_ops="hip", wkv7_dtype=torch.bfloat16).to(DEV)
+    toks = _prompt(2, 20, 6)
+    ids = torch.tensor([1, 0], device=DEV)
+    one = model.new_infer_state(2)
+    assert all(s.dtype == torch.bfloat16 for s in one.state)
+    announce("model infer bf16", "one call")
+    want = model.infer(toks, ids, one)
+    one.advance(ids, 20)
+    step = model.new_infer_state(2)
+    announce("model infer bf16", "prefill 12 + 8 decode steps")
+    model.infer(toks[:, :12], ids, step, unembed_mode="skip")
+    step.advance(ids, 12)
+    for t in range(12, 20):
+        got = model.infer(toks[:, t:t + 1], ids, step)
+        step.advance(ids, 1)
+    torch.cuda.synchronize()
+    assert _err(got, want) <= 2e-2
+    for a, b in zip(step.state, one.state):
+        assert _err(a, b) <= 2e-2
+    assert step.elapsed_t.tolist() == [20, 20]
+    shifted = model.new_infer_state(2)
+    shifted.elapsed_t.fill_(1000)
+    announce("model infer bf16", "other dither seeds")
+    model.infer(toks, ids, shifted)
+    torch.cuda.synchronize()
+    assert any(not torch.equal(a, b) for a, b in zip(shifted.state, one.state))
