@@ -174,7 +174,7 @@ def pmc_summary(dirs):
         print(f"traffic_bytes {k}: {int(round(b))}")
 
 
-def bench_train(cfg, steps, warmup, with_cpu, probe=False):
+def bench_train(cfg, steps, warmup, with_cpu, probe=False, kernels="auto"):
     import torch
     pkg = importlib.import_module("rwkv-rs_amd")
     native = importlib.import_module("rwkv-rs_amd._native")
@@ -197,18 +197,20 @@ def bench_train(cfg, steps, warmup, with_cpu, probe=False):
     dtype_code = native.DTYPE_BF16 if io == torch.bfloat16 else native.DTYPE_F32
     stream = torch.cuda.current_stream(dev)
     sp = stream.cuda_stream
+    # the statepass operator (flags 1, 1 both ways) with an explicit kernel family
+    opts = native.Wkv7Options(native.KERNELS_STEP if kernels == "step" else native.KERNELS_AUTO, 0)
+    optp = native.options_ref(opts)
 
     def fwd():
-        native.check(lib.wkv7_statepass_forward(*ins, s0.data_ptr(), B, T, H, N_HEAD, C,
-                                                dtype_code, ckpt.data_ptr(), sa.data_ptr(),
-                                                y.data_ptr(), sT.data_ptr(), sp))
+        native.check(lib.wkv7_forward_ex(*ins, s0.data_ptr(), B, T, H, N_HEAD, C, dtype_code,
+                                         1, 1, ckpt.data_ptr(), sa.data_ptr(), y.data_ptr(),
+                                         sT.data_ptr(), optp, sp))
 
     def bwd():
-        native.check(lib.wkv7_statepass_backward(*ins, ckpt.data_ptr(), sa.data_ptr(),
-                                                 d["dy"].data_ptr(), dsT.data_ptr(), B, T, H,
-                                                 N_HEAD, C, dtype_code,
-                                                 *(g.data_ptr() for g in grads),
-                                                 ds0.data_ptr(), sp))
+        native.check(lib.wkv7_backward_ex(*ins, ckpt.data_ptr(), sa.data_ptr(),
+                                          d["dy"].data_ptr(), dsT.data_ptr(), B, T, H, N_HEAD, C,
+                                          dtype_code, 1, 1, *(g.data_ptr() for g in grads),
+                                          ds0.data_ptr(), optp, sp))
 
     for _ in range(warmup):
         fwd()
@@ -241,8 +243,7 @@ def bench_train(cfg, steps, warmup, with_cpu, probe=False):
     # 1/16 of a checkpoint in
     e = 2 if io == torch.bfloat16 else 4
     # which kernels ran (launch_forward / launch_backward dispatch)
-    chunked = (io == torch.bfloat16 and C == 16 and T % 16 == 0
-               and os.environ.get("WKV7_BF16_PATH") != "valu")
+    chunked = io == torch.bfloat16 and C == 16 and T % 16 == 0 and kernels == "auto"
     bwd_kernel = "wkv7_bwd_chunk_kernel" if chunked else "wkv7_bwd_kernel"
     fwd_bytes = head_steps * (7 * N_HEAD * e + N_HEAD * 4 + N_HEAD * N_HEAD * 4 / C)
     bwd_bytes = head_steps * (13 * N_HEAD * e + N_HEAD * 4 + N_HEAD * N_HEAD * 4 / C)
@@ -300,8 +301,8 @@ def bench_decode(cfg, steps, warmup, probe=False):
     def step():
         native.check(lib.wkv7_infer_forward(*(d[n].data_ptr() for n in names), ids.data_ptr(),
                                             state.data_ptr(), None, et.data_ptr(), B, T, H,
-                                            N_HEAD, B, native.DTYPE_BF16, 0, y.data_ptr(),
-                                            stream.cuda_stream))
+                                            N_HEAD, B, native.DTYPE_BF16, native.DTYPE_F32, 0,
+                                            y.data_ptr(), stream.cuda_stream))
 
     for _ in range(warmup):
         step()
@@ -395,6 +396,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="cfg1", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--kernels", default="auto", choices=("auto", "step"),
+                    help="cfg0-cfg2: the library's choice, or the step-by-step kernels throughout")
     ap.add_argument("--neighbor-ops", default="hip", choices=("hip", "torch"),
                     help="cfg4: the ops beside the operator as fused kernels or torch ops")
     ap.add_argument("--copy-probe", action="store_true",
@@ -419,7 +422,7 @@ def main():
     else:
         out = bench_train(cfg, args.steps, args.warmup,
                           with_cpu=(not args.no_cpu and args.config == "cfg1"),
-                          probe=args.copy_probe)
+                          probe=args.copy_probe, kernels=args.kernels)
     print(json.dumps(out), flush=True)
 
 

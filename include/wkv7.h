@@ -84,8 +84,11 @@ typedef enum wkv7_status {
   WKV7_ERR_FLAGS = 8,        /* a flag is not 0/1, contradicts a pointer, or
                                 asks for the dither with an fp32 state */
   WKV7_ERR_HIP = 9,          /* the kernel launch failed */
-  WKV7_ERR_SCRATCH_LIMIT = 10 /* the call needs more than the library's fixed
+  WKV7_ERR_SCRATCH_LIMIT = 10, /* the call needs more than the library's fixed
                                  scratch array (the _noalloc entry points) */
+  WKV7_ERR_HANDOVER = 11      /* a chunked-forward launch gave up an internal
+                                 wait; its outputs were poisoned with NaN
+                                 (reported by wkv7_take_faults) */
 } wkv7_status;
 
 typedef enum wkv7_dtype { WKV7_DTYPE_F32 = 0, WKV7_DTYPE_BF16 = 1 } wkv7_dtype;
@@ -134,6 +137,57 @@ int wkv7_backward(const void *weight_decay, const void *receptance,
                   void *receptance_grad, void *key_grad, void *value_grad,
                   void *removal_grad, void *replacement_grad,
                   float *initial_state_grad, void *stream);
+
+/* ---------------------------------------------------------------------------
+ * Explicit kernel choice. No counterpart in the reference (whose backend picks
+ * one kernel per element type). wkv7_forward / wkv7_backward and the trait
+ * entry points use WKV7_KERNELS_AUTO: the chunked matrix-core kernels for
+ * bf16 operands with chunk_len 16 (T a multiple of 16), the step-by-step fp32
+ * kernels otherwise. WKV7_KERNELS_STEP runs the step kernels for every case
+ * (to compare the two families on one input). handover_spin_limit bounds the
+ * polls of each hand-over wait inside the chunked forward (0 = the default,
+ * about 0.1 s); it exists so that tests can force the fault path below.
+ * options may be NULL (all defaults).
+ * ------------------------------------------------------------------------- */
+typedef enum wkv7_kernels { WKV7_KERNELS_AUTO = 0, WKV7_KERNELS_STEP = 1 } wkv7_kernels;
+
+typedef struct wkv7_options {
+  int kernels;                  /* wkv7_kernels */
+  uint32_t handover_spin_limit; /* 0 = default */
+} wkv7_options;
+
+int wkv7_forward_ex(const void *weight_decay, const void *receptance,
+                    const void *key, const void *value, const void *removal,
+                    const void *replacement, const float *initial_state,
+                    int64_t batch_size, int64_t context_len, int64_t num_heads,
+                    int64_t head_size, int64_t chunk_len, int dtype,
+                    int use_initial_state, int return_final_state, float *state,
+                    float *removal_state, void *output, float *final_state,
+                    const wkv7_options *options, void *stream);
+
+int wkv7_backward_ex(const void *weight_decay, const void *receptance,
+                     const void *key, const void *value, const void *removal,
+                     const void *replacement, const float *state,
+                     const float *removal_state, const void *output_grad,
+                     const float *final_state_grad, int64_t batch_size,
+                     int64_t context_len, int64_t num_heads, int64_t head_size,
+                     int64_t chunk_len, int dtype, int use_final_state_grad,
+                     int write_initial_state_grad, void *weight_decay_grad,
+                     void *receptance_grad, void *key_grad, void *value_grad,
+                     void *removal_grad, void *replacement_grad,
+                     float *initial_state_grad, const wkv7_options *options,
+                     void *stream);
+
+/* Hand-over faults of the chunked forward. Its producer and consumer waves
+ * pass chunks through LDS flags with bounded waits. A wait that gives up
+ * (which a correct kernel never does) makes the launch overwrite every output
+ * of that (batch, head) -- output, removal_state, the checkpoints, the final
+ * state -- with NaN, and adds one to a counter on the device. No counterpart
+ * in the reference. wkv7_take_faults waits for `stream`, stores in *count the
+ * number of such events on the current device since the previous call,
+ * resets the counter, and returns WKV7_ERR_HANDOVER if *count > 0 (WKV7_OK
+ * otherwise). Calls on one device must not overlap. */
+int wkv7_take_faults(void *stream, uint32_t *count);
 
 /* Wkv7PretrainBackend (wkv7_pretrain/mod.rs:18-41; CubeBackend impl
  * wkv7_pretrain/forward.rs:13-85): no initial state, no final state. */

@@ -14,20 +14,33 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libwkv7_hip.so")
 
 WKV7_OK = 0
+WKV7_ERR_HANDOVER = 11
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
+KERNELS_AUTO = 0
+KERNELS_STEP = 1
 
 STATUS_NAMES = {
     0: "WKV7_OK", 1: "WKV7_ERR_NULL_POINTER", 2: "WKV7_ERR_SHAPE",
     3: "WKV7_ERR_CHUNK_LEN", 4: "WKV7_ERR_HEAD_SIZE", 5: "WKV7_ERR_DTYPE",
     6: "WKV7_ERR_ALIGNMENT", 7: "WKV7_ERR_OVERLAP", 8: "WKV7_ERR_FLAGS",
-    9: "WKV7_ERR_HIP", 10: "WKV7_ERR_SCRATCH_LIMIT",
+    9: "WKV7_ERR_HIP", 10: "WKV7_ERR_SCRATCH_LIMIT", 11: "WKV7_ERR_HANDOVER",
 }
+
+
+class Wkv7Options(ctypes.Structure):
+    """struct wkv7_options (include/wkv7.h)."""
+    _fields_ = [("kernels", ctypes.c_int), ("handover_spin_limit", ctypes.c_uint32)]
+
+
+def options_ref(opts):
+    """A pointer argument for an optional wkv7_options (None -> NULL)."""
+    return None if opts is None else ctypes.cast(ctypes.pointer(opts), ctypes.c_void_p)
 
 # every symbol include/wkv7.h declares
 EXPORTS = (
     "wkv7_abi_version", "wkv7_strerror", "wkv7_last_hip_error", "wkv7_checkpoint_numel",
-    "wkv7_forward", "wkv7_backward",
+    "wkv7_forward", "wkv7_backward", "wkv7_forward_ex", "wkv7_backward_ex", "wkv7_take_faults",
     "wkv7_pretrain_forward", "wkv7_pretrain_backward",
     "wkv7_statepass_forward", "wkv7_statepass_backward",
     "wkv7_statetune_forward", "wkv7_statetune_backward",
@@ -52,6 +65,9 @@ _SIGNATURES = {
     "wkv7_checkpoint_numel": ([_I64] * 5, _I64),
     "wkv7_forward": ([_P] * 7 + [_I64] * 5 + [_INT] * 3 + [_P] * 5, _INT),
     "wkv7_backward": ([_P] * 10 + [_I64] * 5 + [_INT] * 3 + [_P] * 8, _INT),
+    "wkv7_forward_ex": ([_P] * 7 + [_I64] * 5 + [_INT] * 3 + [_P] * 6, _INT),
+    "wkv7_backward_ex": ([_P] * 10 + [_I64] * 5 + [_INT] * 3 + [_P] * 9, _INT),
+    "wkv7_take_faults": ([_P, _P], _INT),
     "wkv7_pretrain_forward": ([_P] * 6 + [_I64] * 5 + [_INT] + [_P] * 4, _INT),
     "wkv7_pretrain_backward": ([_P] * 9 + [_I64] * 5 + [_INT] + [_P] * 7, _INT),
     "wkv7_statepass_forward": ([_P] * 7 + [_I64] * 5 + [_INT] + [_P] * 5, _INT),

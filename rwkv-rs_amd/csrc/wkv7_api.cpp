@@ -16,13 +16,6 @@
 
 #include "wkv7_launch.hpp"
 
-namespace wkv7 {
-bool force_step_kernels() {
-  const char* v = std::getenv("WKV7_BF16_PATH");
-  return v && std::strcmp(v, "valu") == 0;
-}
-}  // namespace wkv7
-
 namespace {
 
 thread_local int g_last_hip_error = 0;
@@ -79,6 +72,15 @@ int check_shape(int64_t B, int64_t T, int64_t H, int64_t N, int64_t C, int dtype
 
 int check_flag(int f) { return (f == 0 || f == 1) ? WKV7_OK : WKV7_ERR_FLAGS; }
 
+int kernel_choice(const wkv7_options* o, wkv7::KernelChoice* kc) {
+  *kc = wkv7::KernelChoice{};
+  if (!o) return WKV7_OK;
+  if (o->kernels != WKV7_KERNELS_AUTO && o->kernels != WKV7_KERNELS_STEP) return WKV7_ERR_FLAGS;
+  kc->step_only = o->kernels == WKV7_KERNELS_STEP;
+  kc->spin_limit = o->handover_spin_limit;
+  return WKV7_OK;
+}
+
 }  // namespace
 
 namespace wkv7 {
@@ -97,6 +99,14 @@ int wkv7_abi_version(void) { return WKV7_ABI_VERSION; }
 
 int wkv7_last_hip_error(void) { return g_last_hip_error; }
 
+int wkv7_take_faults(void* stream, uint32_t* count) {
+  if (!count) return WKV7_ERR_NULL_POINTER;
+  *count = 0;
+  if (int rc = hip_status(wkv7::take_handover_faults(static_cast<hipStream_t>(stream), count)))
+    return rc;
+  return *count > 0 ? WKV7_ERR_HANDOVER : WKV7_OK;
+}
+
 const char* wkv7_strerror(int status) {
   switch (status) {
     case WKV7_OK: return "ok";
@@ -110,6 +120,8 @@ const char* wkv7_strerror(int status) {
     case WKV7_ERR_FLAGS:
       return "invalid flag value, flag/pointer mismatch, or dither asked for an fp32 state";
     case WKV7_ERR_HIP: return "HIP kernel launch failed";
+    case WKV7_ERR_HANDOVER:
+      return "a chunked forward gave up an internal hand-over wait; its outputs are NaN";
     case WKV7_ERR_SCRATCH_LIMIT:
       return "the call needs more scratch memory than the library's fixed device array holds";
     default: return "unknown wkv7 status";
@@ -129,6 +141,21 @@ int wkv7_forward(const void* weight_decay, const void* receptance, const void* k
                  int64_t num_heads, int64_t head_size, int64_t chunk_len, int dtype,
                  int use_initial_state, int return_final_state, float* state,
                  float* removal_state, void* output, float* final_state, void* stream) {
+  return wkv7_forward_ex(weight_decay, receptance, key, value, removal, replacement,
+                         initial_state, batch_size, context_len, num_heads, head_size,
+                         chunk_len, dtype, use_initial_state, return_final_state, state,
+                         removal_state, output, final_state, nullptr, stream);
+}
+
+int wkv7_forward_ex(const void* weight_decay, const void* receptance, const void* key,
+                    const void* value, const void* removal, const void* replacement,
+                    const float* initial_state, int64_t batch_size, int64_t context_len,
+                    int64_t num_heads, int64_t head_size, int64_t chunk_len, int dtype,
+                    int use_initial_state, int return_final_state, float* state,
+                    float* removal_state, void* output, float* final_state,
+                    const wkv7_options* options, void* stream) {
+  wkv7::KernelChoice kc;
+  if (int rc = kernel_choice(options, &kc)) return rc;
   if (int rc = check_shape(batch_size, context_len, num_heads, head_size, chunk_len, dtype))
     return rc;
   if (int rc = check_flag(use_initial_state)) return rc;
@@ -175,6 +202,7 @@ int wkv7_forward(const void* weight_decay, const void* receptance, const void* k
   d.sa = removal_state;
   d.y = output;
   d.sT = return_final_state ? final_state : nullptr;
+  d.kc = kc;
   return hip_status(wkv7::launch_forward(d, static_cast<hipStream_t>(stream)));
 }
 
@@ -187,6 +215,25 @@ int wkv7_backward(const void* weight_decay, const void* receptance, const void* 
                   void* weight_decay_grad, void* receptance_grad, void* key_grad,
                   void* value_grad, void* removal_grad, void* replacement_grad,
                   float* initial_state_grad, void* stream) {
+  return wkv7_backward_ex(weight_decay, receptance, key, value, removal, replacement, state,
+                          removal_state, output_grad, final_state_grad, batch_size, context_len,
+                          num_heads, head_size, chunk_len, dtype, use_final_state_grad,
+                          write_initial_state_grad, weight_decay_grad, receptance_grad,
+                          key_grad, value_grad, removal_grad, replacement_grad,
+                          initial_state_grad, nullptr, stream);
+}
+
+int wkv7_backward_ex(const void* weight_decay, const void* receptance, const void* key,
+                     const void* value, const void* removal, const void* replacement,
+                     const float* state, const float* removal_state, const void* output_grad,
+                     const float* final_state_grad, int64_t batch_size, int64_t context_len,
+                     int64_t num_heads, int64_t head_size, int64_t chunk_len, int dtype,
+                     int use_final_state_grad, int write_initial_state_grad,
+                     void* weight_decay_grad, void* receptance_grad, void* key_grad,
+                     void* value_grad, void* removal_grad, void* replacement_grad,
+                     float* initial_state_grad, const wkv7_options* options, void* stream) {
+  wkv7::KernelChoice kc;
+  if (int rc = kernel_choice(options, &kc)) return rc;
   if (int rc = check_shape(batch_size, context_len, num_heads, head_size, chunk_len, dtype))
     return rc;
   if (int rc = check_flag(use_final_state_grad)) return rc;
@@ -241,6 +288,7 @@ int wkv7_backward(const void* weight_decay, const void* receptance, const void* 
   d.dw = weight_decay_grad; d.dr = receptance_grad; d.dk = key_grad; d.dv = value_grad;
   d.da = removal_grad; d.db = replacement_grad;
   d.ds0 = write_initial_state_grad ? initial_state_grad : nullptr;
+  d.kc = kc;
   return hip_status(wkv7::launch_backward(d, static_cast<hipStream_t>(stream)));
 }
 

@@ -504,7 +504,7 @@ hipError_t launch_bwd_t(const BackwardDesc& d, hipStream_t stream) {
 
 hipError_t launch_backward(const BackwardDesc& d, hipStream_t stream) {
   if (d.B == 0 || d.H == 0) return hipSuccess;
-  if (chunk_backward_supported(d) && !force_step_kernels()) return launch_backward_chunked(d, stream);
+  if (chunk_backward_supported(d) && !d.kc.step_only) return launch_backward_chunked(d, stream);
   return d.dtype == Dtype::BF16 ? launch_bwd_t<bf16_t>(d, stream) : launch_bwd_t<float>(d, stream);
 }
 

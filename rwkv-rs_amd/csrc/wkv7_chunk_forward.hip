@@ -26,7 +26,11 @@
 // A prep wave overwrites its slot only after all four chain waves have taken
 // the chunk in it, so preparing chunk c overlaps the chain of chunks c-4 ..
 // c-1. The hand-over uses two LDS flags per slot and no barriers; every wait
-// is bounded, so a kernel whose flags went wrong ends instead of hanging.
+// is bounded, so a kernel whose flags went wrong ends instead of hanging. A
+// wave that gives up a wait raises a workgroup fault flag; after a final
+// barrier the workgroup then overwrites all of its (batch, head)'s outputs
+// with NaN and counts the event in a device counter the host reads back
+// (wkv7_take_faults), so a broken hand-over is never silent.
 #include "wkv7_chunk.hpp"
 #include "wkv7_launch.hpp"
 
@@ -44,8 +48,14 @@ enum { S_X, S_R, S_K, S_A, S_B, S_V };
 constexpr int kPieces = kVecs * kL * 8 / 64;   // 16-byte loads per prep lane and chunk
 // polls of a hand-over flag before a wave gives up (each poll sleeps ~64
 // cycles): about 0.1 s, far beyond any legitimate wait in a kernel that runs
-// for well under a millisecond
-constexpr int kSpinLimit = 1 << 22;
+// for well under a millisecond. The caller may lower it (tests force the
+// fault path with a single poll).
+constexpr uint32_t kSpinLimit = 1u << 22;
+
+// hand-over faults on this device since the host last took them, and the
+// value the last take read
+__device__ unsigned int handover_faults;
+__device__ unsigned int handover_faults_taken;
 
 // Phase-1 products of one chunk, each in the fragment order its phase-2
 // consumer loads (index [lane] last). K~ and B~ are kept without the chunk's
@@ -71,6 +81,7 @@ struct FwdChunkParams {
   bf16_t* y;
   float* sT;
   int T, H, C;
+  uint32_t spin_limit;       // polls per hand-over wait (> 0)
 };
 
 // The preparation of one chunk, run by one wave. `stg` holds the chunk's raw
@@ -252,6 +263,7 @@ struct PrepLds {
 struct Flags {
   int ready[kSlots];
   int taken[kSlots][kChainWaves];
+  int fault;                 // a wave gave up a wait
 };
 
 __device__ __forceinline__ int lds_load_flag(const int* f) {
@@ -259,6 +271,14 @@ __device__ __forceinline__ int lds_load_flag(const int* f) {
 }
 __device__ __forceinline__ void lds_store_flag(int* f, int v) {
   __atomic_store_n(f, v, __ATOMIC_RELAXED);
+}
+// poll *f until it reaches v, at most `limit` times; false if it gave up
+__device__ __forceinline__ bool wait_flag(const int* f, int v, uint32_t limit) {
+  for (uint32_t n = 0; n < limit; ++n) {
+    if (lds_load_flag(f) >= v) return true;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  return lds_load_flag(f) >= v;
 }
 // the wave's earlier LDS writes are complete before its later LDS accesses
 __device__ __forceinline__ void lds_release() {
@@ -296,6 +316,7 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_fwd_chunk_kernel(const FwdChun
   const int nchunks = T / kL;
 
   if (tid < kSlots) flags.ready[tid] = -1;
+  if (tid == 0) flags.fault = 0;
   if (tid < kSlots * kChainWaves) flags.taken[tid / kChainWaves][tid % kChainWaves] = tid / kChainWaves - kSlots;
   __syncthreads();
 
@@ -307,7 +328,7 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_fwd_chunk_kernel(const FwdChun
     // is prepared (one chunk of loads in flight hides their latency; LDS has no
     // room for a second staging region per wave).
     static_assert(kPieces == 12, "twelve 16-byte pieces per lane and chunk");
-    if (s >= nchunks) return;
+    if (s < nchunks) {
 #define RWKV_RAW_LOAD(c) \
   r0 = *raw_piece(p, tok0, tstride, c, lane, 0); r1 = *raw_piece(p, tok0, tstride, c, lane, 1); \
   r2 = *raw_piece(p, tok0, tstride, c, lane, 2); r3 = *raw_piece(p, tok0, tstride, c, lane, 3); \
@@ -315,104 +336,125 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_fwd_chunk_kernel(const FwdChun
   r6 = *raw_piece(p, tok0, tstride, c, lane, 6); r7 = *raw_piece(p, tok0, tstride, c, lane, 7); \
   r8 = *raw_piece(p, tok0, tstride, c, lane, 8); r9 = *raw_piece(p, tok0, tstride, c, lane, 9); \
   r10 = *raw_piece(p, tok0, tstride, c, lane, 10); r11 = *raw_piece(p, tok0, tstride, c, lane, 11);
-    uint4 r0, r1, r2, r3, r4, r5, r6, r7, r8, r9, r10, r11;
-    RWKV_RAW_LOAD(s)
-    for (int c = s; c < nchunks; c += kSlots) {
-      uint4* const dst = reinterpret_cast<uint4*>(&my.stg[0][0][0]) + lane;
-      dst[0] = r0; dst[64] = r1; dst[128] = r2; dst[192] = r3; dst[256] = r4; dst[320] = r5;
-      dst[384] = r6; dst[448] = r7; dst[512] = r8; dst[576] = r9; dst[640] = r10; dst[704] = r11;
-      // the last chunk reloads itself (harmless) so that the loads need no branch
-      const int cn = c + kSlots < nchunks ? c + kSlots : c;
-      RWKV_RAW_LOAD(cn)
-      // the slot is free once every chain wave has taken chunk c - kSlots
-      for (int w = 0; w < kChainWaves; ++w) {
-        for (int n = 0; n < kSpinLimit && lds_load_flag(&flags.taken[s][w]) < c - kSlots; ++n)
-          __builtin_amdgcn_s_sleep(1);
+      uint4 r0, r1, r2, r3, r4, r5, r6, r7, r8, r9, r10, r11;
+      RWKV_RAW_LOAD(s)
+      for (int c = s; c < nchunks; c += kSlots) {
+        uint4* const dst = reinterpret_cast<uint4*>(&my.stg[0][0][0]) + lane;
+        dst[0] = r0; dst[64] = r1; dst[128] = r2; dst[192] = r3; dst[256] = r4; dst[320] = r5;
+        dst[384] = r6; dst[448] = r7; dst[512] = r8; dst[576] = r9; dst[640] = r10; dst[704] = r11;
+        // the last chunk reloads itself (harmless) so that the loads need no branch
+        const int cn = c + kSlots < nchunks ? c + kSlots : c;
+        RWKV_RAW_LOAD(cn)
+        // the slot is free once every chain wave has taken chunk c - kSlots
+        bool ok = true;
+        for (int w = 0; w < kChainWaves; ++w) ok &= wait_flag(&flags.taken[s][w], c - kSlots, p.spin_limit);
+        if (!ok && lane == 0) lds_store_flag(&flags.fault, 1);
+        lds_acquire();
+        prepare_chunk(my.stg, my.scr, ops[s], lane);
+        lds_release();
+        if (lane == 0) lds_store_flag(&flags.ready[s], c);
       }
-      lds_acquire();
-      prepare_chunk(my.stg, my.scr, ops[s], lane);
-      lds_release();
-      if (lane == 0) lds_store_flag(&flags.ready[s], c);
-    }
 #undef RWKV_RAW_LOAD
-    return;
-  }
-
-  // ===================================================== chain wave: value tile jb
-  // state: key tiles ib = 0..3 in the result layout (rows = key i =
-  // 16 ib + 4 qd + r, columns = value j = 16 jb + t)
-  const int jb = wave, jcol = 16 * jb + t;
-  f32x4 S[4];
-#pragma unroll
-  for (int ib = 0; ib < 4; ++ib) {
-    if (kHasS0)
-      S[ib] = *reinterpret_cast<const f32x4*>(p.s0 + bh * (kHead * kHead) + jcol * kHead + 16 * ib + 4 * qd);
-    else
-      S[ib] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
-  const uint32_t tok_row = (uint32_t)tstride;                       // one step
-  const uint32_t tok_off = 4 * qd * tok_row + jcol;                  // row 4 qd, column jcol
-  const uint32_t ck_off = 4 * qd * kHead + jcol;
-  const uint32_t yt_off = t * tok_row + 16 * jb + 4 * qd;            // row t, 4 values
-  // the checkpoint after chunk c (chunk_len is 16 here: one per chunk),
-  // transposed ([key][value]): rows = keys 16 ib + 4 qd + r, column jcol
-  auto store_ckpt = [&](int c, const f32x4 (&st)[4]) {
-    float* const ck = p.ckpt + (bh * nchunks + c) * (kHead * kHead);
-#pragma unroll
-    for (int ib = 0; ib < 4; ++ib)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) ck[ck_off + (16 * ib + r) * kHead] = st[ib][r];
-  };
-
-  for (int cidx = 0; cidx < nchunks; ++cidx) {
-    const int slot = cidx % kSlots;
-    for (int n = 0; n < kSpinLimit && lds_load_flag(&flags.ready[slot]) < cidx; ++n)
-      __builtin_amdgcn_s_sleep(1);
-    lds_acquire();
-    const ChainOps cur = load_chain_ops(ops[slot], jb, lane);
-
-    const Split8 Sx0 = split8(S[0], S[1]), Sx1 = split8(S[2], S[3]);
-    // the previous chunk's checkpoint (the state this chunk starts from),
-    // stored here so that the stores overlap this chunk's products
-    if (cidx > 0) store_ckpt(cidx - 1, S);
-    f32x4 sa = mma32x3(cur.w[0], Sx0, cur.u);
-    sa = mma32x3(cur.w[1], Sx1, sa);
-    // Y^T = S0 R^T + V^T A_rk^T + SA^T A_rb^T: the same registers with the
-    // operand roles swapped (a result tile as the A operand is its
-    // transpose), so each lane holds 4 consecutive values of one step
-    f32x4 yt = mma32x3(Sx0, cur.r[0], f32x4{0.f, 0.f, 0.f, 0.f});
-    yt = mma32x3(Sx1, cur.r[1], yt);
-    yt = mma32(twice(cur.v), cur.ark, yt);
-    const Split4 sas = split4(sa);
-    yt = mma32(cat8(sas.lo, bf16x4{0, 0, 0, 0}), cur.arb, yt);
-    yt = mma32(twice(sas.hi), cur.arb, yt);
+    }
+  } else {
+    // ===================================================== chain wave: value tile jb
+    // state: key tiles ib = 0..3 in the result layout (rows = key i =
+    // 16 ib + 4 qd + r, columns = value j = 16 jb + t)
+    const int jb = wave, jcol = 16 * jb + t;
+    f32x4 S[4];
 #pragma unroll
     for (int ib = 0; ib < 4; ++ib) {
-      f32x4 st = mma_s2(cur.kt[ib], cur.v, S[ib]);
-      st = mma_s3(cur.bt[ib], sas, st);
-      S[ib] = st * cur.gl[ib];
+      if (kHasS0)
+        S[ib] = *reinterpret_cast<const f32x4*>(p.s0 + bh * (kHead * kHead) + jcol * kHead + 16 * ib + 4 * qd);
+      else
+        S[ib] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    // every operand has been used, so its load has completed (the wait costs
-    // nothing here); the slot goes back to its prep wave
-    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
-    lds_release();
-    if (lane == 0) lds_store_flag(&flags.taken[slot][jb], cidx);
-    // outputs: sa rows = steps 16 cidx + 4 qd + r, column = value jcol;
-    // y at step 16 cidx + t, values 16 jb + 4 qd .. + 3 (one 8-byte store)
-    const int64_t cbase = tok0 + (int64_t)kL * cidx * tstride;
-    float* const sa_c = p.sa + cbase;
-    bf16_t* const y_c = p.y + cbase;
+    const uint32_t tok_row = (uint32_t)tstride;                       // one step
+    const uint32_t tok_off = 4 * qd * tok_row + jcol;                  // row 4 qd, column jcol
+    const uint32_t ck_off = 4 * qd * kHead + jcol;
+    const uint32_t yt_off = t * tok_row + 16 * jb + 4 * qd;            // row t, 4 values
+    // the checkpoint after chunk c (chunk_len is 16 here: one per chunk),
+    // transposed ([key][value]): rows = keys 16 ib + 4 qd + r, column jcol
+    auto store_ckpt = [&](int c, const f32x4 (&st)[4]) {
+      float* const ck = p.ckpt + (bh * nchunks + c) * (kHead * kHead);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) sa_c[tok_off + r * tok_row] = sa[r];
-    *reinterpret_cast<bf16x4*>(y_c + yt_off) = to_bf16x4(yt);
-  }
-  if (nchunks > 0) store_ckpt(nchunks - 1, S);
+      for (int ib = 0; ib < 4; ++ib)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ck[ck_off + (16 * ib + r) * kHead] = st[ib][r];
+    };
 
-  if (p.sT) {
+    for (int cidx = 0; cidx < nchunks; ++cidx) {
+      const int slot = cidx % kSlots;
+      for (int n = 0; n < kSpinLimit && lds_load_flag(&flags.ready[slot]) < cidx; ++n)
+        __builtin_amdgcn_s_sleep(1);
+      lds_acquire();
+      const ChainOps cur = load_chain_ops(ops[slot], jb, lane);
+
+      const Split8 Sx0 = split8(S[0], S[1]), Sx1 = split8(S[2], S[3]);
+      // the previous chunk's checkpoint (the state this chunk starts from),
+      // stored here so that the stores overlap this chunk's products
+      if (cidx > 0) store_ckpt(cidx - 1, S);
+      f32x4 sa = mma32x3(cur.w[0], Sx0, cur.u);
+      sa = mma32x3(cur.w[1], Sx1, sa);
+      // Y^T = S0 R^T + V^T A_rk^T + SA^T A_rb^T: the same registers with the
+      // operand roles swapped (a result tile as the A operand is its
+      // transpose), so each lane holds 4 consecutive values of one step
+      f32x4 yt = mma32x3(Sx0, cur.r[0], f32x4{0.f, 0.f, 0.f, 0.f});
+      yt = mma32x3(Sx1, cur.r[1], yt);
+      yt = mma32(twice(cur.v), cur.ark, yt);
+      const Split4 sas = split4(sa);
+      yt = mma32(cat8(sas.lo, bf16x4{0, 0, 0, 0}), cur.arb, yt);
+      yt = mma32(twice(sas.hi), cur.arb, yt);
 #pragma unroll
-    for (int ib = 0; ib < 4; ++ib)
-      *reinterpret_cast<f32x4*>(p.sT + bh * (kHead * kHead) + jcol * kHead + 16 * ib + 4 * qd) = S[ib];
+      for (int ib = 0; ib < 4; ++ib) {
+        f32x4 st = mma_s2(cur.kt[ib], cur.v, S[ib]);
+        st = mma_s3(cur.bt[ib], sas, st);
+        S[ib] = st * cur.gl[ib];
+      }
+      // every operand has been used, so its load has completed (the wait costs
+      // nothing here); the slot goes back to its prep wave
+      __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+      lds_release();
+      if (lane == 0) lds_store_flag(&flags.taken[slot][jb], cidx);
+      // outputs: sa rows = steps 16 cidx + 4 qd + r, column = value jcol;
+      // y at step 16 cidx + t, values 16 jb + 4 qd .. + 3 (one 8-byte store)
+      const int64_t cbase = tok0 + (int64_t)kL * cidx * tstride;
+      float* const sa_c = p.sa + cbase;
+      bf16_t* const y_c = p.y + cbase;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sa_c[tok_off + r * tok_row] = sa[r];
+      *reinterpret_cast<bf16x4*>(y_c + yt_off) = to_bf16x4(yt);
+    }
+    if (nchunks > 0) store_ckpt(nchunks - 1, S);
+
+    if (p.sT) {
+#pragma unroll
+      for (int ib = 0; ib < 4; ++ib)
+        *reinterpret_cast<f32x4*>(p.sT + bh * (kHead * kHead) + jcol * kHead + 16 * ib + 4 * qd) = S[ib];
+    }
   }
+
+  // every wave ends here: if any wave gave up a wait, the whole (batch,
+  // head)'s outputs are unreliable, so they are overwritten with NaN and the
+  // event is counted for the host
+  __syncthreads();
+  if (lds_load_flag(&flags.fault)) {
+    const float nan = __builtin_nanf("");
+    for (int64_t i = tid; i < (int64_t)T * kHead; i += kBlock) {
+      const int64_t off = tok0 + (i >> 6) * tstride + (i & 63);
+      p.y[off] = 0x7fc0;
+      p.sa[off] = nan;
+    }
+    float* const ck = p.ckpt + bh * nchunks * (kHead * kHead);
+    for (int64_t i = tid; i < (int64_t)nchunks * kHead * kHead; i += kBlock) ck[i] = nan;
+    if (p.sT)
+      for (int i = tid; i < kHead * kHead; i += kBlock) p.sT[bh * (kHead * kHead) + i] = nan;
+    if (tid == 0) atomicAdd(&handover_faults, 1u);
+  }
+}
+
+__global__ void take_faults_kernel() {
+  handover_faults_taken = atomicExch(&handover_faults, 0u);
 }
 
 }  // namespace
@@ -444,12 +486,23 @@ hipError_t launch_forward_chunked(const ForwardDesc& d, hipStream_t stream) {
   p.T = d.T;
   p.H = d.H;
   p.C = d.C;
+  p.spin_limit = d.kc.spin_limit ? d.kc.spin_limit : kSpinLimit;
   const dim3 grid(d.H, d.B, 1), block(kBlock, 1, 1);
   if (d.s0)
     hipLaunchKernelGGL(wkv7_fwd_chunk_kernel<true>, grid, block, 0, stream, p);
   else
     hipLaunchKernelGGL(wkv7_fwd_chunk_kernel<false>, grid, block, 0, stream, p);
   return hipGetLastError();
+}
+
+hipError_t take_handover_faults(hipStream_t stream, uint32_t* count) {
+  hipLaunchKernelGGL(take_faults_kernel, dim3(1), dim3(1), 0, stream);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  e = hipMemcpyFromSymbolAsync(count, HIP_SYMBOL(handover_faults_taken), sizeof(uint32_t), 0,
+                               hipMemcpyDeviceToHost, stream);
+  if (e != hipSuccess) return e;
+  return hipStreamSynchronize(stream);
 }
 
 }  // namespace wkv7

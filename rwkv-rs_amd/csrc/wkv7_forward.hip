@@ -326,7 +326,7 @@ hipError_t launch_fwd_t(const ForwardDesc& d, hipStream_t stream) {
 
 hipError_t launch_forward(const ForwardDesc& d, hipStream_t stream) {
   if (d.B == 0 || d.H == 0) return hipSuccess;
-  if (chunk_forward_supported(d) && !force_step_kernels()) return launch_forward_chunked(d, stream);
+  if (chunk_forward_supported(d) && !d.kc.step_only) return launch_forward_chunked(d, stream);
   return d.dtype == Dtype::BF16 ? launch_fwd_t<bf16_t>(d, stream) : launch_fwd_t<float>(d, stream);
 }
 

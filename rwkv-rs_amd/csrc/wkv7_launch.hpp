@@ -11,6 +11,12 @@ constexpr int kHeadSize = 64;   // the kernels are specialised for N = 64
 
 enum class Dtype : int { F32 = 0, BF16 = 1 };
 
+// kernel family (WKV7_KERNELS_*) and the chunked forward's hand-over bound
+struct KernelChoice {
+  bool step_only = false;       // WKV7_KERNELS_STEP
+  uint32_t spin_limit = 0;      // 0 = default
+};
+
 // Forward pass, mirrors wkv7_forward_impl (wkv7_common/host.rs:29-183).
 struct ForwardDesc {
   Dtype dtype;
@@ -21,6 +27,7 @@ struct ForwardDesc {
   float* sa;                    // [B,T,H,64] removal_state
   void* y;                      // [B,T,H,64] in dtype
   float* sT;                    // [B,H,64,64] or nullptr
+  KernelChoice kc;
 };
 
 // Backward pass, mirrors wkv7_backward_impl (wkv7_common/host.rs:185-369).
@@ -34,6 +41,7 @@ struct BackwardDesc {
   const float* dsT;             // [B,H,64,64] or nullptr (zeros)
   void *dw, *dr, *dk, *dv, *da, *db;   // [B,T,H,64] in dtype
   float* ds0;                   // [B,H,64,64] or nullptr
+  KernelChoice kc;
 };
 
 // Slot-mapped inference, mirrors wkv7_infer_forward_impl
@@ -54,16 +62,17 @@ struct InferDesc {
 hipError_t launch_forward(const ForwardDesc& d, hipStream_t stream);
 
 // Chunked matrix-core forward (wkv7_chunk_forward.hip): bf16 operands,
-// chunk_len 16. launch_forward picks it when supported unless
-// the environment variable WKV7_BF16_PATH is "valu" (a diagnostic switch that
-// keeps the step-by-step kernels for every dtype).
+// chunk_len 16. launch_forward picks it when supported, unless the caller
+// asked for the step kernels (KernelChoice::step_only).
 bool chunk_forward_supported(const ForwardDesc& d);
 hipError_t launch_forward_chunked(const ForwardDesc& d, hipStream_t stream);
-bool force_step_kernels();
+// the chunked forward's hand-over fault counter on the current device: read
+// and reset on `stream`, then wait for it
+hipError_t take_handover_faults(hipStream_t stream, uint32_t* count);
 
 // Chunked matrix-core backward (wkv7_chunk_backward.hip): bf16 operands,
 // chunk_len 16, T a positive multiple of 16; picked by launch_backward under
-// the same switch.
+// the same choice.
 bool chunk_backward_supported(const BackwardDesc& d);
 hipError_t launch_backward_chunked(const BackwardDesc& d, hipStream_t stream);
 hipError_t launch_backward(const BackwardDesc& d, hipStream_t stream);

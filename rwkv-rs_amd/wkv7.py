@@ -183,7 +183,19 @@ def _check_chunk(T: int, chunk_len: int) -> None:
 
 
 # ---------------------------------------------------------- forward / backward
-def _forward(w, r, k, v, a, b, initial_state, chunk_len, use_initial_state, return_final_state):
+def _options(kernels: str = "auto", handover_spin_limit: int = 0):
+    """A ``wkv7_options`` for the ``_ex`` entry points (kernels "auto" or
+    "step"), or None for the defaults."""
+    codes = {"auto": _native.KERNELS_AUTO, "step": _native.KERNELS_STEP}
+    if kernels not in codes:
+        raise ValueError(f"kernels must be one of {sorted(codes)}")
+    if kernels == "auto" and handover_spin_limit == 0:
+        return None
+    return _native.Wkv7Options(codes[kernels], int(handover_spin_limit))
+
+
+def _forward(w, r, k, v, a, b, initial_state, chunk_len, use_initial_state, return_final_state,
+             options=None):
     w, r, k, v, a, b = _tokens(w, r, k, v, a, b)
     B, T, H, N = w.shape
     _check_chunk(T, chunk_len)
@@ -195,16 +207,16 @@ def _forward(w, r, k, v, a, b, initial_state, chunk_len, use_initial_state, retu
     final_state = (torch.empty((B, H, N, N), dtype=torch.float32, device=dev)
                    if return_final_state else None)
     end = _mark("forward", dev)
-    _native.call("wkv7_forward", _ptr(w), _ptr(r), _ptr(k), _ptr(v), _ptr(a), _ptr(b), _ptr(s0),
-                 B, T, H, N, chunk_len, _dtype_code(w), int(use_initial_state),
+    _native.call("wkv7_forward_ex", _ptr(w), _ptr(r), _ptr(k), _ptr(v), _ptr(a), _ptr(b),
+                 _ptr(s0), B, T, H, N, chunk_len, _dtype_code(w), int(use_initial_state),
                  int(return_final_state), _ptr(state), _ptr(removal_state), _ptr(output),
-                 _ptr(final_state), _stream(dev))
+                 _ptr(final_state), _native.options_ref(options), _stream(dev))
     _close(end, dev)
     return state, removal_state, output, final_state
 
 
 def _backward(w, r, k, v, a, b, state, removal_state, output_grad, final_state_grad, chunk_len,
-              use_final_state_grad, write_initial_state_grad):
+              use_final_state_grad, write_initial_state_grad, options=None):
     w, r, k, v, a, b, output_grad = _tokens(w, r, k, v, a, b, output_grad)
     B, T, H, N = w.shape
     _check_chunk(T, chunk_len)
@@ -216,13 +228,52 @@ def _backward(w, r, k, v, a, b, state, removal_state, output_grad, final_state_g
     ds0 = (torch.empty((B, H, N, N), dtype=torch.float32, device=dev)
            if write_initial_state_grad else None)
     end = _mark("backward", dev)
-    _native.call("wkv7_backward", _ptr(w), _ptr(r), _ptr(k), _ptr(v), _ptr(a), _ptr(b),
+    _native.call("wkv7_backward_ex", _ptr(w), _ptr(r), _ptr(k), _ptr(v), _ptr(a), _ptr(b),
                  _ptr(state), _ptr(removal_state), _ptr(output_grad), _ptr(dsT),
                  B, T, H, N, chunk_len, _dtype_code(w), int(use_final_state_grad),
                  int(write_initial_state_grad), *(_ptr(g) for g in grads), _ptr(ds0),
-                 _stream(dev))
+                 _native.options_ref(options), _stream(dev))
     _close(end, dev)
     return grads, ds0
+
+
+# ----------------------------------------------- explicit kernel choice (_ex)
+def wkv7_forward_ex(weight_decay, receptance, key, value, removal, replacement, initial_state,
+                    chunk_len, use_initial_state=True, return_final_state=True,
+                    kernels: str = "auto", handover_spin_limit: int = 0
+                    ) -> Wkv7StatePassForwardOutput:
+    """wkv7_forward_ex (include/wkv7.h): the generic forward with an explicit
+    kernel family ("auto", or "step" for the step-by-step fp32 kernels in
+    every case) and hand-over bound. No counterpart in the reference."""
+    state, sa, y, sT = _forward(weight_decay, receptance, key, value, removal, replacement,
+                                initial_state, chunk_len, use_initial_state, return_final_state,
+                                _options(kernels, handover_spin_limit))
+    return Wkv7StatePassForwardOutput(state=state, removal_state=sa, output=y, final_state=sT)
+
+
+def wkv7_backward_ex(weight_decay, receptance, key, value, removal, replacement, state,
+                     removal_state, output_grad, final_state_grad, chunk_len,
+                     use_final_state_grad=True, write_initial_state_grad=True,
+                     kernels: str = "auto") -> Wkv7StateBackwardOutput:
+    """wkv7_backward_ex (include/wkv7.h) with an explicit kernel family."""
+    g, ds0 = _backward(weight_decay, receptance, key, value, removal, replacement, state,
+                       removal_state, output_grad, final_state_grad, chunk_len,
+                       use_final_state_grad, write_initial_state_grad, _options(kernels))
+    return Wkv7StateBackwardOutput(*g, initial_state_grad=ds0)
+
+
+def take_faults(device=None) -> int:
+    """wkv7_take_faults: waits for the current stream and returns the number of
+    chunked-forward launches on the device that gave up a hand-over wait since
+    the last call (their outputs are NaN); raises Wkv7Error
+    (WKV7_ERR_HANDOVER) when there were any."""
+    import ctypes
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else device
+    n = ctypes.c_uint32(0)
+    status = _native.lib().wkv7_take_faults(_stream(dev), ctypes.byref(n))
+    if status not in (_native.WKV7_OK, _native.WKV7_ERR_HANDOVER):
+        _native.check(status)
+    return int(n.value)
 
 
 # ------------------------------------------------- Wkv7PretrainBackend (mirror)

@@ -33,7 +33,7 @@ def declared_functions(header=HEADER, prefix="wkv7_"):
 
 def test_header_declares_expected_entry_points():
     names = declared_functions()
-    assert len(names) == 13, names
+    assert len(names) == 16, names
     assert len(declared_functions(NEIGHBORS_HEADER, "rwkv_")) == 10
     assert len(declared_functions(LOSS_HEADER, "rwkv_")) == 2
 
@@ -53,6 +53,25 @@ def test_version_and_strings(native):
     assert lib.wkv7_strerror(3).decode() == "chunk_len must divide sequence length"
     assert lib.wkv7_strerror(4).decode() == "head_size must be 64"
     assert lib.wkv7_strerror(123).decode() == "unknown wkv7 status"
+
+
+def test_options_and_fault_query_validation(native):
+    lib = native.lib()
+    assert lib.wkv7_take_faults(None, None) == 1          # count pointer required
+    msg = lib.wkv7_strerror(11).decode()
+    assert "hand-over" in msg and "NaN" in msg
+    bad = native.Wkv7Options(7, 0)                        # unknown kernel family
+    assert lib.wkv7_forward_ex(*([FAKE] * 7), 1, 64, 4, 64, 16, 0, 1, 1, FAKE * 10,
+                               FAKE * 20, FAKE * 30, FAKE * 40, native.options_ref(bad),
+                               None) == 8
+    assert lib.wkv7_backward_ex(*([FAKE] * 10), 1, 64, 4, 64, 16, 0, 1, 1,
+                                *([FAKE * 10] * 7), native.options_ref(bad), None) == 8
+    # the options are checked before anything else; valid options leave the
+    # usual checks in place
+    ok = native.Wkv7Options(native.KERNELS_STEP, 0)
+    assert lib.wkv7_forward_ex(*([FAKE] * 7), 1, 60, 4, 64, 16, 0, 1, 1, FAKE * 10,
+                               FAKE * 20, FAKE * 30, FAKE * 40, native.options_ref(ok),
+                               None) == 3
 
 
 def test_checkpoint_numel(native):

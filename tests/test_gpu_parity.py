@@ -9,6 +9,8 @@ initial-state gradient) are also held to 1e-4: the chunked matrix-core forward
 forms its products from hi/lo bf16 splits (about 16 significant bits) and
 measures 2e-6 to 7e-6 against the fp32 oracle."""
 
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -328,20 +330,18 @@ def test_full_size_config2_every_pair(wk, oracle):
     (1, 80, 2, 0.1, 33),     # a partial last batch (one chunk)
     (3, 48, 2, None, 34),    # three chunks, no initial state
 ])
-def test_bf16_chunked_forward_matches_step_forward(wk, case, monkeypatch):
-    # bf16, chunk_len 16 runs the chunked matrix-core forward; WKV7_BF16_PATH=valu
-    # switches the same call to the step-by-step fp32 kernel. Same inputs, both
-    # paths: outputs within bf16 rounding, fp32 state family within 1e-4.
+def test_bf16_chunked_forward_matches_step_forward(wk, case):
+    # bf16, chunk_len 16 runs the chunked matrix-core forward; kernels="step"
+    # (wkv7_forward_ex) runs the step-by-step fp32 kernel on the same call.
+    # Outputs within bf16 rounding, fp32 state family within 1e-4.
     B, T, H, s0_std, seed = case
     announce("bf16 chunked vs step forward", case)
     pkg = load_pkg()
     d = pkg.synthetic.make_inputs(B, T, H, 64, seed=seed, s0_std=s0_std, bf16=True)
     ins = [to_dev(d[n], torch.bfloat16) for n in NAMES]
     s0 = to_dev(d["s0"]) if d["s0"] is not None else torch.zeros(B, H, 64, 64, device="cuda")
-    monkeypatch.delenv("WKV7_BF16_PATH", raising=False)
     ch = wk.wkv7_statepass_forward(*ins, s0, 16)
-    monkeypatch.setenv("WKV7_BF16_PATH", "valu")
-    st = wk.wkv7_statepass_forward(*ins, s0, 16)
+    st = wk.wkv7_forward_ex(*ins, s0, 16, kernels="step")
     torch.cuda.synchronize()
     assert rel_l2(to_np(ch.output), to_np(st.output)) < 1e-3
     for name in ("removal_state", "state", "final_state"):
@@ -356,8 +356,8 @@ def test_bf16_chunked_forward_matches_step_forward(wk, case, monkeypatch):
     (2, 64, 3, 0.1, 43),     # carried state gradient across chunks
     (1, 80, 2, None, 44),
 ])
-def test_bf16_chunked_backward_matches_step_backward(wk, case, monkeypatch):
-    # bf16, chunk_len 16 runs the chunked matrix-core backward; WKV7_BF16_PATH=valu
+def test_bf16_chunked_backward_matches_step_backward(wk, case):
+    # bf16, chunk_len 16 runs the chunked matrix-core backward; kernels="step"
     # the step-by-step fp32 kernel. Both get the same forward outputs and a
     # nonzero final-state gradient; gradients agree within bf16 rounding, the
     # fp32 initial-state gradient within 1e-4.
@@ -369,10 +369,8 @@ def test_bf16_chunked_backward_matches_step_backward(wk, case, monkeypatch):
     s0 = to_dev(d["s0"]) if d["s0"] is not None else torch.zeros(B, H, 64, 64, device="cuda")
     dy = to_dev(d["dy"], torch.bfloat16)
     dsT = 0.1 * torch.randn(B, H, 64, 64, device="cuda", generator=torch.Generator("cuda").manual_seed(seed))
-    monkeypatch.setenv("WKV7_BF16_PATH", "valu")
-    f = wk.wkv7_statepass_forward(*ins, s0, 16)
-    st = wk.wkv7_statepass_backward(*ins, f.state, f.removal_state, dy, dsT, 16)
-    monkeypatch.delenv("WKV7_BF16_PATH")
+    f = wk.wkv7_forward_ex(*ins, s0, 16, kernels="step")
+    st = wk.wkv7_backward_ex(*ins, f.state, f.removal_state, dy, dsT, 16, kernels="step")
     ch = wk.wkv7_statepass_backward(*ins, f.state, f.removal_state, dy, dsT, 16)
     torch.cuda.synchronize()
     for gn in GRAD_NAMES:
@@ -380,3 +378,49 @@ def test_bf16_chunked_backward_matches_step_backward(wk, case, monkeypatch):
         assert err < 2e-3, (gn, err)
     err = rel_l2(to_np(ch.initial_state_grad), to_np(st.initial_state_grad))
     assert err < BF16_STATE_TOL, err
+
+
+def test_handover_fault_poisons_outputs_and_is_reported(wk):
+    """The chunked forward's waves hand chunks over through LDS flags with
+    bounded waits. With the bound forced down to a single poll (the
+    handover_spin_limit option) waves give up waits, which a correct run never
+    does: every (batch, head) whose launch saw that must come back entirely
+    NaN (output, removal_state, checkpoints, final state), the count of such
+    launches must be reported by wkv7_take_faults as WKV7_ERR_HANDOVER, and
+    every other (batch, head) must equal the normal run bit for bit. A
+    normal run afterwards reports no fault."""
+    announce("hand-over fault path (forced from the host)")
+    pkg = load_pkg()
+    B, T, H = 2, 256, 8
+    d = pkg.synthetic.make_inputs(B, T, H, 64, seed=51, s0_std=0.1, bf16=True)
+    ins = [to_dev(d[n], torch.bfloat16) for n in NAMES]
+    s0 = to_dev(d["s0"])
+    assert wk.take_faults() == 0
+    good = wk.wkv7_statepass_forward(*ins, s0, 16)
+    assert wk.take_faults() == 0
+    bad = wk.wkv7_forward_ex(*ins, s0, 16, handover_spin_limit=1)
+    faults = wk.take_faults()
+    poisoned = 0
+    for b in range(B):
+        for h in range(H):
+            parts = (bad.output[b, :, h], bad.removal_state[b, :, h], bad.state[b, h],
+                     bad.final_state[b, h])
+            if torch.isnan(bad.final_state[b, h]).any():
+                assert all(torch.isnan(x.float()).all() for x in parts), (b, h)
+                poisoned += 1
+            else:
+                assert torch.equal(bad.output[b, :, h], good.output[b, :, h]), (b, h)
+                assert torch.equal(bad.state[b, h], good.state[b, h]), (b, h)
+                assert torch.equal(bad.final_state[b, h], good.final_state[b, h]), (b, h)
+    print("forced hand-over faults:", faults, "poisoned pairs:", poisoned, flush=True)
+    assert faults == poisoned and faults > 0
+    again = wk.wkv7_statepass_forward(*ins, s0, 16)
+    assert wk.take_faults() == 0
+    assert torch.equal(again.output, good.output)
+    # the C ABI's own status for the same event
+    native = load_pkg()._native
+    wk.wkv7_forward_ex(*ins, s0, 16, handover_spin_limit=1)
+    n = ctypes.c_uint32(0)
+    rc = native.lib().wkv7_take_faults(torch.cuda.current_stream().cuda_stream, ctypes.byref(n))
+    assert rc == native.WKV7_ERR_HANDOVER and n.value > 0, (rc, n.value)
+    assert wk.take_faults() == 0
