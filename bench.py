@@ -1,27 +1,35 @@
 """WKV7 fwd+bwd benchmark on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg1|cfg2|cfg3|cfg0]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg0|cfg1|cfg2|cfg3|cfg4]
 
 A step is one forward and one backward pass of the WKV7 statepass operator
 (initial state in, final-state gradient zero, 16-step checkpoints) over one
 batch of synthetic operands, called through the C ABI with device-resident
 buffers allocated once. The default workload is the headline one:
-B=8, T=4096, H=32, N=64, bf16 operands, fp32 state and arithmetic,
+B=8, T=4096, H=32, N=64, bf16 operands, fp32 state and accumulation,
 initial state ~ N(0, 0.1).
 
-Printed JSON line: whole-job Mtokens/s, ms per step, the roofline of the
-dominant kernel (the backward: algorithmic FP32 FLOPs per launch / mean launch
-time from HIP events recorded on the launch stream, against MI355X's 157.3
-TFLOP/s FP32 peak, which is both the packed-VALU and the dense fp32-MFMA
-figure; with bf16 operands and chunk_len 16 the kernels are the chunked
-matrix-core ones, which form the fp32 products from split bf16 MFMAs), and
-the CPU baseline (the oracle's reference-order fp32 restatement,
-OpenMP over (batch, head) pairs, timed on a bounded sample of the same
-workload on the host cores). config cfg3 is the batched decode step (T=1),
-which is HBM-bound. config cfg4 is a whole RWKV-7 0.1B training step (12
-cells, C=768, vocab 65536, B=16, T=512) with the WKV7 operator on the HIP
-kernels and every other op in PyTorch; it reports the step time and the
-WKV7 share.
+Printed JSON line: whole-job Mtokens/s (wall clock over the K timed steps),
+ms per step, and:
+- "dtype"/"arithmetic": what the kernels compute in. With bf16 operands and
+  chunk_len 16 the chunked matrix-core kernels run: fp32 state and
+  accumulation, products of fp32 operands from bf16 hi/lo halves
+  (hi*hi + hi*lo + lo*hi);
+- "roofline": the dominant kernel (the backward): algorithmic FP32 FLOPs per
+  launch / mean launch time (HIP events on the launch stream) against
+  MI355X's 157.3 TFLOP/s FP32 peak, with "traffic" (HBM bytes per launch from
+  rocprofv3 FETCH_SIZE / WRITE_SIZE, profiles/) and "units": the issued bf16
+  MFMA FLOPs against the 2.5 PFLOP/s dense bf16 peak and the VALU issue
+  share, from rocprofv3 SQ counters recorded in profiles/;
+- "cpu_baseline": the oracle (the reference's fp32 algorithm in its
+  operation order, built -march=native, OpenMP over (batch, head) pairs) on
+  the GPU run's operand bytes, forward and backward timed separately, median
+  of 3 after a warm-up, with the host CPU model and thread count.
+config cfg3 is the batched decode step (T=1), which is HBM-bound
+(--state-dtype bf16: the reference's bf16 instantiation). config cfg4 is a
+whole RWKV-7 0.1B training step (12 cells, C=768, vocab 65536, B=16, T=512)
+with the WKV7 operator on the HIP kernels and every other op in PyTorch; it
+reports the step time and the WKV7 share.
 """
 
 from __future__ import annotations
@@ -41,11 +49,16 @@ FLOP_FWD = 9 * N_HEAD * N_HEAD      # per head-step: sa 2N^2, update 5N^2, y 2N^
 FLOP_BWD = 24 * N_HEAD * N_HEAD     # per head-step, non-redundant backward
 PEAK_FP32 = 157.3e12                # MI355X FP32 peak (packed VALU; also dense fp32 MFMA)
 PEAK_HBM = 8.0e12                   # MI355X HBM3E
+PEAK_BF16 = 2.5e15                  # MI355X dense bf16 MFMA
+CLOCK_HZ = 2.4e9                    # MI355X peak engine clock
+N_SIMDS = 256 * 4                   # 256 CUs of 4 SIMDs
 COPY_PROBE_BYTES = 512 << 20        # fp32 stream (read once, write once) of --copy-probe
 # HBM traffic of the dominant kernel per launch, from rocprofv3 FETCH_SIZE /
 # WRITE_SIZE passes scaled by the copy probe; written by --pmc-summary
 TRAFFIC_FILE = os.path.join(HERE, "profiles", "wkv7_bwd_cfg1_traffic.md")
 TRAFFIC_FILE_DECODE = os.path.join(HERE, "profiles", "wkv7_infer_cfg3_traffic.md")
+# issued MFMA FLOPs and VALU instructions per launch, from rocprofv3 SQ counters
+COUNTER_FILE = os.path.join(HERE, "profiles", "wkv7_cfg1_sq_counters.md")
 METRIC = "WKV7 fwd+bwd Mtokens/s (B=8,T=4096,C=2048) + % FP32-VALU / HBM roofline"
 
 CONFIGS = {
@@ -65,41 +78,80 @@ def cpu_cores() -> int:
     return max(1, min(n, 16))   # the box's CPU share for one GPU is 16
 
 
-def cpu_baseline(cfg, seconds_target=12.0):
-    """Oracle (reference-order fp32 restatement) on a bounded sample of the
-    workload: whole sequences of a few (batch, head) pairs, OpenMP over pairs."""
-    import numpy as np
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(cfg, d, budget_s=24.0, reps=3):
+    """The oracle (the reference's fp32 algorithm in its operation order,
+    oracle/wkv7_oracle.c, built here with -march=native, OpenMP over (batch,
+    head) pairs) on the same seeded operand bytes as the GPU run (copied from
+    the device). Forward and backward are timed separately: one warm-up pass,
+    then the median of `reps` passes each. When a pass over the whole batch
+    would exceed the budget the leading batch rows are the sample."""
+    import statistics
+    import tempfile
 
     import oracle
-    pkg = importlib.import_module("rwkv-rs_amd")
     B, T, H = cfg["B"], cfg["T"], cfg["H"]
     cores = cpu_cores()
+    build = "native"
+    try:
+        oracle.build_native(os.path.join(tempfile.mkdtemp(prefix="wkv7_cpu_"), "libwkv7_oracle.so"))
+    except Exception as e:   # no compiler: the prebuilt x86-64-v3 library
+        build = f"prebuilt x86-64-v3 ({type(e).__name__})"
     names = ("w", "r", "k", "v", "a", "b")
 
-    d = pkg.synthetic.make_inputs(1, T, cores, N_HEAD, seed=7, s0_std=0.1,
-                                  bf16=cfg["io"] == "bf16")
-    ins = [d[n] for n in names]
+    def host(t):
+        return None if t is None else t.float().cpu().numpy()
 
-    def run():
-        t0 = time.perf_counter()
-        f = oracle.forward_f32(*ins, s0=d["s0"], chunk_len=16, nthreads=cores)
-        oracle.backward_f32(*ins, f["state"], f["removal_state"], d["dy"], chunk_len=16,
-                            nthreads=cores)
-        return time.perf_counter() - t0
+    def sample(nb):
+        ins = [host(d[n][:nb]) for n in names]
+        s0 = host(d["s0"][:nb]) if d["s0"] is not None else None
+        return ins, s0, host(d["dy"][:nb])
 
-    # one (batch, head) pair per core; repeat the pass to ~seconds_target
-    dt1 = run()
-    reps = max(1, int(round(seconds_target / max(dt1, 1e-3))))
+    def fwd(ins, s0):
+        return oracle.forward_f32(*ins, s0=s0, chunk_len=16, nthreads=cores)
+
+    def bwd(ins, f, dy):
+        return oracle.backward_f32(*ins, f["state"], f["removal_state"], dy, chunk_len=16,
+                                   nthreads=cores)
+
+    # size the sample from one batch row, then warm up on the sample
+    ins, s0, dy = sample(1)
     t0 = time.perf_counter()
+    bwd(ins, fwd(ins, s0), dy)
+    per_row = time.perf_counter() - t0
+    nb = max(1, min(B, int(budget_s / (reps + 1) / max(per_row, 1e-6))))
+    ins, s0, dy = sample(nb)
+    f = fwd(ins, s0)
+    bwd(ins, f, dy)
+    tf, tb = [], []
     for _ in range(reps):
-        run()
-    dt = time.perf_counter() - t0
-    nheads = reps * cores
-    tokens = nheads * T / H   # one token covers all H heads
-    return {"value": tokens / dt / 1e6, "unit": "Mtokens/s", "cores": cores,
+        t0 = time.perf_counter()
+        f = fwd(ins, s0)
+        t1 = time.perf_counter()
+        bwd(ins, f, dy)
+        t2 = time.perf_counter()
+        tf.append(t1 - t0)
+        tb.append(t2 - t1)
+    mf, mb = statistics.median(tf), statistics.median(tb)
+    tokens = nb * T
+    return {"value": tokens / (mf + mb) / 1e6, "unit": "Mtokens/s", "cores": cores,
             "kind": "port",
-            "sample": f"{nheads} (batch, head) pairs x T={T}, fwd+bwd, chunk 16, "
-                      f"{dt:.1f} s on {cores} threads (oracle/wkv7_oracle.c, reference order)"}
+            "fwd_s": mf, "bwd_s": mb, "cpu_model": cpu_model(), "nproc": os.cpu_count(),
+            "sample": f"{nb} of {B} batch rows x {H} heads x T={T} (the GPU run's operand "
+                      f"bytes), chunk 16; forward and backward timed separately, median of "
+                      f"{reps} after one warm-up: fwd {mf:.3f} s, bwd {mb:.3f} s on {cores} "
+                      f"OpenMP threads of '{cpu_model()}'; oracle/wkv7_oracle.c "
+                      f"(reference operation order, fp32, {build} build)"}
 
 
 def recorded_traffic(kernel: str, path: str = TRAFFIC_FILE):
@@ -109,6 +161,18 @@ def recorded_traffic(kernel: str, path: str = TRAFFIC_FILE):
         with open(path) as f:
             for line in f:
                 if line.startswith(f"traffic_bytes {kernel}:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
+def recorded_counter(name: str, kernel: str, path: str):
+    """A "<name> <kernel>: <int>" line of `path`, or None."""
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith(f"{name} {kernel}:"):
                     return int(line.split(":")[1])
     except OSError:
         pass
@@ -172,6 +236,14 @@ def pmc_summary(dirs):
     print()
     for k, b in totals.items():
         print(f"traffic_bytes {k}: {int(round(b))}")
+    # the hardware units' view: issued bf16 MFMA FLOPs (the MOPS counter
+    # counts in units of 512 FLOPs) and VALU instructions per dispatch
+    for k in keys:
+        cs = mean.get(k, {})
+        if "SQ_INSTS_VALU_MFMA_MOPS_BF16" in cs:
+            print(f"mfma_flop_issued {k}: {int(round(cs['SQ_INSTS_VALU_MFMA_MOPS_BF16'] * 512))}")
+        if "SQ_INSTS_VALU" in cs:
+            print(f"valu_insts {k}: {int(round(cs['SQ_INSTS_VALU']))}")
 
 
 def bench_train(cfg, steps, warmup, with_cpu, probe=False, kernels="auto"):
@@ -230,23 +302,45 @@ def bench_train(cfg, steps, warmup, with_cpu, probe=False, kernels="auto"):
         e2.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    fwd_ms = sum(a.elapsed_time(b) for a, b, _ in ev) / steps
-    bwd_ms = sum(b.elapsed_time(c) for _, b, c in ev) / steps
+    fwd_each = sorted(a.elapsed_time(b) for a, b, _ in ev)
+    bwd_each = sorted(b.elapsed_time(c) for _, b, c in ev)
+    fwd_ms = sum(fwd_each) / steps          # mean launch time, as rocprofv3's average
+    bwd_ms = sum(bwd_each) / steps
     ms_per_step = wall * 1e3 / steps
     head_steps = B * T * H
     tok = B * T
     bwd_flops = FLOP_BWD * head_steps
     fwd_flops = FLOP_FWD * head_steps
     achieved = bwd_flops / (bwd_ms * 1e-3)
-    # algorithmic HBM bytes per head-step (bf16 io): fwd 7 vectors in/out + sa
-    # out + 1/16 of a checkpoint; bwd 7 vectors + sa in, 6 gradients out,
-    # 1/16 of a checkpoint in
     e = 2 if io == torch.bfloat16 else 4
     # which kernels ran (launch_forward / launch_backward dispatch)
     chunked = io == torch.bfloat16 and C == 16 and T % 16 == 0 and kernels == "auto"
     bwd_kernel = "wkv7_bwd_chunk_kernel" if chunked else "wkv7_bwd_kernel"
+    fwd_kernel = "wkv7_fwd_chunk_kernel" if chunked else "wkv7_fwd_kernel"
+    # algorithmic HBM bytes per head-step: fwd 7 rows in/out (e bytes) + sa
+    # out + 1/16 of a checkpoint; bwd 7 rows + sa in, 6 gradients out, 1/16
+    # of a checkpoint in
     fwd_bytes = head_steps * (7 * N_HEAD * e + N_HEAD * 4 + N_HEAD * N_HEAD * 4 / C)
     bwd_bytes = head_steps * (13 * N_HEAD * e + N_HEAD * 4 + N_HEAD * N_HEAD * 4 / C)
+    if chunked:
+        arithmetic = ("fp32 state, checkpoints and accumulation; matrix products of two fp32 "
+                      "operands formed from bf16 hi/lo halves as hi*hi + hi*lo + lo*hi on the "
+                      "bf16 matrix cores (about 16 significant bits per product), products with "
+                      "a bf16 input exact; bf16 operands and outputs")
+        dtype = "f32-acc/split-bf16-mfma"
+    else:
+        arithmetic = "fp32 VALU throughout (fp32 products and sums); operands and outputs " + cfg["io"]
+        dtype = "f32"
+    # the hardware units' view of the dominant kernel: issued MFMA FLOPs and
+    # VALU instructions per launch (rocprofv3 counters recorded in profiles/)
+    units = {}
+    mops = recorded_counter("mfma_flop_issued", bwd_kernel, COUNTER_FILE)
+    valu = recorded_counter("valu_insts", bwd_kernel, COUNTER_FILE)
+    if mops:
+        units["mfma_bf16_tflops"] = mops / (bwd_ms * 1e-3) / 1e12
+        units["mfma_bf16_frac"] = mops / (bwd_ms * 1e-3) / PEAK_BF16
+    if valu:
+        units["valu_issue_frac"] = valu * 4 / (bwd_ms * 1e-3 * CLOCK_HZ * N_SIMDS)
     out = {
         "metric": METRIC,
         "value": tok / (ms_per_step * 1e-3) / 1e6,
@@ -258,7 +352,8 @@ def bench_train(cfg, steps, warmup, with_cpu, probe=False, kernels="auto"):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": dtype,
+        "arithmetic": arithmetic,
         "data": "synthetic",
         "config": {"workload": "wkv7_statepass_fwd_bwd", "batch": B, "context_len": T,
                    "num_heads": H, "head_size": N_HEAD, "chunk_len": C, "io_dtype": cfg["io"],
@@ -268,21 +363,28 @@ def bench_train(cfg, steps, warmup, with_cpu, probe=False, kernels="auto"):
                      "peak": PEAK_FP32 / 1e12, "unit": "TFLOP/s", "frac": achieved / PEAK_FP32,
                      "traffic": recorded_traffic(bwd_kernel),
                      "algorithmic_bytes": bwd_bytes,
-                     "flop_per_launch": bwd_flops, "launch_ms": bwd_ms},
+                     "flop_per_launch": bwd_flops, "launch_ms": bwd_ms,
+                     "launch_ms_median": bwd_each[steps // 2],
+                     "peak_note": "FP32-equivalent: the metric's algorithmic fp32 FLOPs "
+                                  "against MI355X's 157.3 TFLOP/s FP32 peak",
+                     "units": units},
         "kernels": "chunked-mfma" if chunked else "step-valu",
         "fwd_ms": fwd_ms,
+        "fwd_ms_median": fwd_each[steps // 2],
         "bwd_ms": bwd_ms,
+        "bwd_ms_median": bwd_each[steps // 2],
         "fwd_roofline_frac": fwd_flops / (fwd_ms * 1e-3) / PEAK_FP32,
         "fwd_bwd_roofline_frac": (fwd_flops + bwd_flops) / ((fwd_ms + bwd_ms) * 1e-3) / PEAK_FP32,
         "fwd_hbm_frac_algorithmic": fwd_bytes / (fwd_ms * 1e-3) / PEAK_HBM,
         "bwd_hbm_frac_algorithmic": bwd_bytes / (bwd_ms * 1e-3) / PEAK_HBM,
+        "fwd_traffic": recorded_traffic(fwd_kernel),
     }
     if with_cpu:
-        out["cpu_baseline"] = cpu_baseline(cfg)
+        out["cpu_baseline"] = cpu_baseline(cfg, d)
     return out
 
 
-def bench_decode(cfg, steps, warmup, probe=False):
+def bench_decode(cfg, steps, warmup, probe=False, state_dtype="f32"):
     import torch
     pkg = importlib.import_module("rwkv-rs_amd")
     native = importlib.import_module("rwkv-rs_amd._native")
@@ -291,7 +393,8 @@ def bench_decode(cfg, steps, warmup, probe=False):
     dev = torch.device("cuda:0")
     d = pkg.synthetic.make_inputs_torch(B, T, H, N_HEAD, seed=0x5EED0003, s0_std=0.1,
                                         dtype=torch.bfloat16, device=dev)
-    state = d["s0"].contiguous()
+    bf16_state = state_dtype == "bf16"
+    state = d["s0"].to(torch.bfloat16 if bf16_state else torch.float32).contiguous()
     ids = torch.arange(B, dtype=torch.int32, device=dev)
     et = torch.zeros(B, dtype=torch.int32, device=dev)
     y = torch.empty(B, T, H, N_HEAD, device=dev, dtype=torch.bfloat16)
@@ -301,8 +404,9 @@ def bench_decode(cfg, steps, warmup, probe=False):
     def step():
         native.check(lib.wkv7_infer_forward(*(d[n].data_ptr() for n in names), ids.data_ptr(),
                                             state.data_ptr(), None, et.data_ptr(), B, T, H,
-                                            N_HEAD, B, native.DTYPE_BF16, native.DTYPE_F32, 0,
-                                            y.data_ptr(), stream.cuda_stream))
+                                            N_HEAD, B, native.DTYPE_BF16,
+                                            native.DTYPE_BF16 if bf16_state else native.DTYPE_F32,
+                                            int(bf16_state), y.data_ptr(), stream.cuda_stream))
 
     for _ in range(warmup):
         step()
@@ -318,19 +422,22 @@ def bench_decode(cfg, steps, warmup, probe=False):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     launch_ms = e0.elapsed_time(e1) / steps
-    nbytes = B * H * (2 * N_HEAD * N_HEAD * 4 + 7 * T * N_HEAD * 2)
+    nbytes = B * H * (2 * N_HEAD * N_HEAD * (2 if bf16_state else 4) + 7 * T * N_HEAD * 2)
     return {
         "metric": "WKV7 batched decode Mtokens/s (B=256, T=1, H=40)",
         "value": B * T / (wall / steps) / 1e6, "unit": "Mtokens/s", "n_gpus": 1,
         "steps": steps, "warmup": warmup, "ms_per_step": wall * 1e3 / steps,
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16" if bf16_state else "f32",
         "data": "synthetic",
         "config": {"workload": "wkv7_infer_decode", "batch": B, "context_len": T,
-                   "num_heads": H, "head_size": N_HEAD, "io_dtype": "bf16", "state_dtype": "f32"},
-        "roofline": {"bound": "hbm", "kernel": "wkv7_infer_kernel",
+                   "num_heads": H, "head_size": N_HEAD, "io_dtype": "bf16",
+                   "state_dtype": state_dtype, "dither": bool(bf16_state)},
+        "roofline": {"bound": "hbm",
+                     "kernel": "wkv7_infer_bf16_kernel" if bf16_state else "wkv7_infer_kernel",
                      "achieved": nbytes / (launch_ms * 1e-3) / 1e9, "peak": PEAK_HBM / 1e9,
                      "unit": "GB/s", "frac": nbytes / (launch_ms * 1e-3) / PEAK_HBM,
-                     "traffic": recorded_traffic("wkv7_infer_kernel", TRAFFIC_FILE_DECODE),
+                     "traffic": None if bf16_state else recorded_traffic("wkv7_infer_kernel", TRAFFIC_FILE_DECODE),
                      "algorithmic_bytes": nbytes, "launch_ms": launch_ms},
     }
 
@@ -396,6 +503,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="cfg1", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--state-dtype", default="f32", choices=("f32", "bf16"),
+                    help="cfg3: the decode state's element type")
     ap.add_argument("--kernels", default="auto", choices=("auto", "step"),
                     help="cfg0-cfg2: the library's choice, or the step-by-step kernels throughout")
     ap.add_argument("--neighbor-ops", default="hip", choices=("hip", "torch"),
@@ -418,7 +527,8 @@ def main():
     if args.config == "cfg4":
         out = bench_lm(cfg, args.steps, args.warmup, args.neighbor_ops)
     elif args.config == "cfg3":
-        out = bench_decode(cfg, args.steps, args.warmup, probe=args.copy_probe)
+        out = bench_decode(cfg, args.steps, args.warmup, probe=args.copy_probe,
+                           state_dtype=args.state_dtype)
     else:
         out = bench_train(cfg, args.steps, args.warmup,
                           with_cpu=(not args.no_cpu and args.config == "cfg1"),

@@ -63,6 +63,15 @@ def build(force: bool = False) -> str:
     return _LIB_PATH
 
 
+def build_native(out_path: str) -> str:
+    """Compile the same source with -march=native for the host it runs on
+    (the CPU baseline's build), to ``out_path``, and use it from then on."""
+    global _LIB_PATH, _lib
+    subprocess.run(["make", "-s", "-C", _HERE, "native", f"NATIVE_OUT={out_path}"], check=True)
+    _LIB_PATH, _lib = out_path, None
+    return out_path
+
+
 def _load():
     global _lib
     if _lib is not None:

@@ -55,5 +55,39 @@ def build(verbose: bool = False) -> str:
     return LIB
 
 
+def build_sanitized(out_dir: str, verbose: bool = False) -> str:
+    """A CPU-checking build: the C ABI's host code (every *_api.cpp: argument
+    validation, pointer-range arithmetic) compiled by g++ with AddressSanitizer
+    and UndefinedBehaviorSanitizer, linked with the unchanged gfx950 kernels.
+    Load it into a process that preloads gcc's libasan and libubsan. Returns
+    the library path (out_dir/libwkv7_hip.so)."""
+    os.makedirs(out_dir, exist_ok=True)
+    objs = []
+    rocm = os.path.dirname(os.path.dirname(os.path.realpath(hipcc())))
+    for src in SOURCES:
+        obj = os.path.join(out_dir, src + ".o")
+        if src.endswith(".cpp"):
+            cmd = ["g++", "-std=c++17", "-O1", "-g", "-fPIC", "-fno-omit-frame-pointer",
+                   "-fsanitize=address,undefined", "-fno-sanitize-recover=undefined",
+                   "-D__HIP_PLATFORM_AMD__", f"-I{rocm}/include", "-c",
+                   os.path.join(CSRC, src), "-o", obj]
+        else:
+            cmd = [hipcc(), *flags(), "-c", os.path.join(CSRC, src), "-o", obj]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        subprocess.run(cmd, check=True, capture_output=not verbose)
+        objs.append(obj)
+    lib = os.path.join(out_dir, "libwkv7_hip.so")
+    cmd = ["g++", "-shared", "-fsanitize=address,undefined", "-o", lib, *objs,
+           f"-L{rocm}/lib", "-lamdhip64", f"-Wl,-rpath,{rocm}/lib"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+    return lib
+
+
 if __name__ == "__main__":
-    print(build(verbose=True))
+    if len(sys.argv) > 2 and sys.argv[1] == "--sanitize":
+        print(build_sanitized(sys.argv[2], verbose=True))
+    else:
+        print(build(verbose=True))

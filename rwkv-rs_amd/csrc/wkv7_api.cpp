@@ -10,8 +10,7 @@
 
 #include <algorithm>
 #include <cstdint>
-#include <cstdlib>
-#include <cstring>
+#include <initializer_list>
 #include <vector>
 
 #include "wkv7_launch.hpp"
@@ -60,13 +59,25 @@ int check_dtype(int dtype) {
 
 int elem_bytes(int dtype) { return dtype == WKV7_DTYPE_BF16 ? 2 : 4; }
 
-// shape checks shared by forward and backward; C is the chunk length
+// true when the product of the non-negative factors fits in int64
+bool product_fits(std::initializer_list<int64_t> factors) {
+  int64_t acc = 1;
+  for (int64_t f : factors)
+    if (__builtin_mul_overflow(acc, f, &acc)) return false;
+  return true;
+}
+
+// shape checks shared by forward and backward; C is the chunk length. Every
+// byte count the checks below form (per-token tensors, checkpoints) must fit
+// in int64.
 int check_shape(int64_t B, int64_t T, int64_t H, int64_t N, int64_t C, int dtype) {
   if (int rc = check_dtype(dtype)) return rc;
   if (N != kN) return WKV7_ERR_HEAD_SIZE;
   if (B < 0 || T < 0 || H < 0) return WKV7_ERR_SHAPE;
   if (B > kMaxGridDim || H > kMaxGridDim || T > INT32_MAX) return WKV7_ERR_SHAPE;
   if (C <= 0 || C > INT32_MAX || T % C != 0) return WKV7_ERR_CHUNK_LEN;
+  if (!product_fits({B, T, H, kN, 4}) || !product_fits({B, H, T / C, kN * kN, 4}))
+    return WKV7_ERR_SHAPE;
   return WKV7_OK;
 }
 
@@ -372,6 +383,9 @@ int wkv7_infer_forward(const void* weight_decay, const void* receptance, const v
   if (active_batch_size < 0 || context_len < 0 || num_heads < 0 || full_batch_size < 0 ||
       active_batch_size > kMaxGridDim || num_heads > kMaxGridDim || context_len > INT32_MAX ||
       full_batch_size > INT32_MAX || active_batch_size > full_batch_size)
+    return WKV7_ERR_SHAPE;
+  if (!product_fits({active_batch_size, context_len, num_heads, kN, 4}) ||
+      !product_fits({full_batch_size, num_heads, kN * kN, 4}))
     return WKV7_ERR_SHAPE;
   if (int rc = check_flag(use_dither)) return rc;
   // the reference dithers only when the element type is not f32 (host.rs:157)

@@ -16,8 +16,15 @@ def pytest_configure(config):
 
 def load_pkg():
     """The product package lives in the directory ``rwkv-rs_amd``; its name is
-    not a Python identifier, so it is imported by string."""
-    return importlib.import_module("rwkv-rs_amd")
+    not a Python identifier, so it is imported by string. RWKV_AMD_TEST_LIB
+    points the tests at another build of the library (the sanitizer build of
+    ``rwkv-rs_amd/build.py --sanitize``)."""
+    pkg = importlib.import_module("rwkv-rs_amd")
+    other = os.environ.get("RWKV_AMD_TEST_LIB")
+    if other:
+        native = importlib.import_module("rwkv-rs_amd._native")
+        native.LIB_PATH = other
+    return pkg
 
 
 @pytest.fixture(scope="session")

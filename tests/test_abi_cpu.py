@@ -170,3 +170,20 @@ def test_python_mirror_checks_chunk_len_before_the_gpu():
     wk = load_pkg().wkv7
     with pytest.raises(ValueError, match="chunk_len must divide sequence length"):
         wk._check_chunk(60, 16)
+
+
+def test_sizes_whose_byte_counts_overflow_are_refused(native):
+    # batch 65535 x heads 65535 x 2^31 - 1 steps x 64 channels exceeds int64;
+    # the checks must refuse it (not wrap around) before touching any pointer
+    lib = native.lib()
+    big_t = 2 ** 31 - 1
+    fwd = lib.wkv7_forward(*([FAKE] * 6), None, 65535, big_t, 65535, 64, 1, 1, 0, 0,
+                           FAKE * 10, FAKE * 20, FAKE * 30, None, None)
+    assert fwd == 2
+    bwd = lib.wkv7_backward(*([FAKE] * 9), None, 65535, big_t, 65535, 64, 1, 1, 0, 0,
+                            *([FAKE * 10] * 6), None, None)
+    assert bwd == 2
+    assert lib.wkv7_checkpoint_numel(65535, big_t, 65535, 64, 1) == -1
+    inf = lib.wkv7_infer_forward(*([FAKE] * 6), FAKE * 10, FAKE * 20, None, None, 65535, big_t,
+                                 65535, 64, 65535, 1, 0, 0, FAKE * 30, None)
+    assert inf == 2
