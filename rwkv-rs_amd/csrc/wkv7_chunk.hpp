@@ -129,25 +129,30 @@ __device__ __forceinline__ f32x4 mma_s3(bf16x8 a_stacked, const Split4& b, f32x4
 
 // X Y in the result layout from X^T and Y in the result layout (lane l holds
 // M[4 qd + r][l % 16]): X^T's lanes are X as an A operand, Y's are Y as a B
-// operand; split-bf16 product, contraction length 16
-__device__ __forceinline__ f32x4 mma_tiles(f32x4 xt, f32x4 y, f32x4 c) {
-  return mma_s3(stack(split4(xt)), split4(y), c);
+// operand; split-bf16 product, contraction length 16. The operands come
+// split (split4) so that a tile used several times is split once.
+__device__ __forceinline__ f32x4 mma_tiles(const Split4& xt, const Split4& y, f32x4 c) {
+  return mma_s3(stack(xt), y, c);
 }
 // P = (I - A)^-1 for a strictly triangular 16x16 A (lower or upper), from A
 // and A^T in the result layout (t = l % 16, qd = l / 16); P in the result
-// layout. Since A^16 = 0, P = (I + A)(I + A^2)(I + A^4)(I + A^8): five
-// dependent products, all operands in registers.
+// layout. Since A^16 = 0, P = (I + A)(I + A^2)(I + A^4)(I + A^8): eight
+// products, five of them dependent, all operands in registers, each tile
+// split into bf16 halves once.
 __device__ __forceinline__ f32x4 unit_lower_inverse(f32x4 a, f32x4 at, int t, int qd) {
   const f32x4 z = {0.f, 0.f, 0.f, 0.f};
   f32x4 id;
 #pragma unroll
   for (int r = 0; r < 4; ++r) id[r] = (4 * qd + r == t) ? 1.0f : 0.0f;
-  const f32x4 a2 = mma_tiles(at, a, z), a2t = mma_tiles(a, at, z);
-  const f32x4 a4 = mma_tiles(a2t, a2, z), a4t = mma_tiles(a2, a2t, z);
-  const f32x4 a8 = mma_tiles(a4t, a4, z);
-  const f32x4 qt = mma_tiles(a2, at, id + at + a2t);   // ((I + A)(I + A^2))^T
-  const f32x4 r = mma_tiles(a4t, a8, id + a4 + a8);    // (I + A^4)(I + A^8)
-  return mma_tiles(qt, r, z);
+  const Split4 sa = split4(a), sat = split4(at);
+  const f32x4 a2 = mma_tiles(sat, sa, z), a2t = mma_tiles(sa, sat, z);
+  const Split4 sa2 = split4(a2), sa2t = split4(a2t);
+  const f32x4 a4 = mma_tiles(sa2t, sa2, z), a4t = mma_tiles(sa2, sa2t, z);
+  const Split4 sa4t = split4(a4t);
+  const f32x4 a8 = mma_tiles(sa4t, split4(a4), z);
+  const f32x4 qt = mma_tiles(sa2, sat, id + at + a2t);   // ((I + A)(I + A^2))^T
+  const f32x4 r = mma_tiles(sa4t, split4(a8), id + a4 + a8);    // (I + A^4)(I + A^8)
+  return mma_tiles(split4(qt), split4(r), z);
 }
 
 // B operand of the 16x16 identity: multiplying an A fragment by it returns
@@ -232,6 +237,29 @@ __device__ __forceinline__ float row_scan16(float x) {
 __device__ __forceinline__ float row_last16(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
       0, __builtin_bit_cast(int, x), 0x15F, 0xf, 0xf, false));   // row_newbcast:15
+}
+
+// Sums over the four 16-lane rows of a wave (the quads qd of the MFMA
+// layouts) without LDS, by gfx950's row-swapping moves (lane layout measured
+// on the box): permlane16_swap(x, x) returns rows (0, 0, 2, 2) and (1, 1, 3,
+// 3) of x, permlane32_swap(x, x) rows (0, 1, 0, 1) and (2, 3, 2, 3).
+__device__ __forceinline__ float as_f(uint32_t u) { return __uint_as_float(u); }
+__device__ __forceinline__ uint32_t as_u(float x) { return __float_as_uint(x); }
+// x_0 + x_1 + x_2 + x_3 over the rows, in every lane
+__device__ __forceinline__ float rows_total(float x) {
+  const auto p = __builtin_amdgcn_permlane32_swap(as_u(x), as_u(x), false, false);
+  const float s = as_f(p[0]) + as_f(p[1]);   // x_r + x_(r^2)
+  const auto q = __builtin_amdgcn_permlane16_swap(as_u(s), as_u(s), false, false);
+  return as_f(q[0]) + as_f(q[1]);
+}
+// sum of x over the rows below row qd (rows qd + 1 .. 3), in every lane of row qd
+__device__ __forceinline__ float rows_after(float x, int qd) {
+  const auto q = __builtin_amdgcn_permlane16_swap(as_u(x), as_u(x), false, false);
+  const float pair = as_f(q[0]) + as_f(q[1]);   // x_0 + x_1 in rows 0, 1; x_2 + x_3 in rows 2, 3
+  const auto p = __builtin_amdgcn_permlane32_swap(as_u(pair), as_u(pair), false, false);
+  const float upper = as_f(p[1]);               // x_2 + x_3
+  const float odd = as_f(q[1]);                 // x_1 in row 0, x_3 in row 2
+  return qd == 0 ? odd + upper : qd == 1 ? upper : qd == 2 ? odd : 0.0f;
 }
 
 __device__ __forceinline__ float exp2_f(float x) { return __builtin_amdgcn_exp2f(x); }

@@ -32,15 +32,19 @@
 // waves", key tile w - 4) do the per-chunk work that does not depend on it,
 // one chunk ahead, so each SIMD interleaves two instruction streams:
 //   phase A: gradient waves: state-gradient chain and dV of chunk c; set-up
-//            waves: staging loads, the finished decay gradient of chunk c+1;
-//            all waves: decays and decayed rows of chunk c-1 (keys 8w..8w+7)
-//   phase B: gradient waves: gradient flush of chunk c+1, step products of
-//            v, dy, sa and with dSA of chunk c; set-up waves: staging
-//            stores, step products of the decayed rows of chunk c-1 and
-//            P = (I - A_ab)^-1 (wave 4)
+//            waves: staging loads, the finished decay gradient of chunk c+1,
+//            the step products of v, dy, sa of chunk c (one per wave), and
+//            the decays and decayed rows of chunk c-1 (keys of their own
+//            slice and of their SIMD's gradient wave)
+//   phase B: gradient waves: gradient flush of chunk c+1, the step products
+//            with dSA of chunk c; set-up waves: step products of the decayed
+//            rows of chunk c-1 and P = (I - A_ab)^-1 (wave 4), staging stores
 //   phase C: key-indexed gradients of chunk c, key tile w: dK, dB and their
 //            part of the decay gradient on the gradient wave, dR, dA and the
 //            rest on the set-up wave, which finishes dw after the barrier
+// Phase C's operands that phase B does not write are read at the end of
+// phase B, so their latency overlaps the barrier; sums over the four quads of
+// a wave use gfx950's row-swapping moves instead of LDS.
 // Within a phase each wave first issues its LDS reads, then computes. Inputs
 // are staged through registers, loaded in phase A and written to LDS in
 // phase B: the rows only the decays read (x, r, k, a, b) in one buffer, two
@@ -91,7 +95,6 @@ struct BwdLds {
   bf16x8 frag[G_COUNT][64];         // step products with v, dy, sa, dsa (stacked)
   bf16_t xds[2][64][64];            // dS' hi/lo, [value j][key i]
   bf16_t xdsa[2][64][kL];           // dSA hi/lo, [value j][step t]
-  float red[kWaves][2][4][16];      // cross-quad scratch of the key-gradient stage
   f32x4 kx[4][64];                  // the gradient waves' part of the decay gradient, per key tile
   bf16_t outs[2][O_COUNT][kL][64];  // a chunk's bf16 gradients, written out as whole rows (out_at), double-buffered
   bf16_t zero[kL][64];              // an all-zero row tile
@@ -461,7 +464,6 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
         }
       *reinterpret_cast<bf16x4*>(xdsa_at(L.xdsa[0], jcol, qd)) = dsas.hi;
       *reinterpret_cast<bf16x4*>(xdsa_at(L.xdsa[1], jcol, qd)) = dsas.lo;
-      if constexpr (kFull) setup_decays(Pn, decay_load(L.dec, wave, t, qd), wave, t, qd);
     } else {
       if (c < last) finish(c + 1);
       if constexpr (kFull) {
@@ -469,7 +471,40 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
         // the reversal of chunk 0 reads them)
         pre = fetch(c >= 2 ? c - 2 : 0, c - 1);
         load_s0(c, S0row);
+      }
+      // step products of v, dy, sa of chunk c (one per wave), which do not
+      // depend on the state gradient, as D = X1 Y1^T + X2 Y2^T:
+      // B_yv^T = dy v^T (s >= t), C_dyv^T = v dy^T (s <= t),
+      // B_ysa^T = dy sa^T (s >= t), C_dysa^T = sa dy^T (s <= t)
+      {
+        const int x1 = wq == 1 ? S_V : wq == 3 ? S_SAH : S_DY;
+        const int y1 = wq == 0 ? S_V : wq == 2 ? S_SAH : S_DY;
+        const int y2 = wq == 0 ? S_V : wq == 2 ? S_SAL : S_DY;
+        const bf16_t (*const x2)[64] = wq == 2 ? stg[S_DY] : wq == 3 ? stg[S_SAL] : L.zero;
+        bf16x8 px1[2], py1[2], px2[2], py2[2];
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+          px1[m] = row_frag(stg[x1], t, m, qd);
+          py1[m] = row_frag(stg[y1], t, m, qd);
+          px2[m] = row_frag(x2, t, m, qd);
+          py2[m] = row_frag(stg[y2], t, m, qd);
+        }
+        const int sgn = (wq & 1) ? -1 : 1;   // keep s >= t (B_), s <= t (C_)
+        f32x4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+          d = mma32(px2[m], py2[m], d);
+          d = mma32(px1[m], py1[m], d);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) d[r] = sgn * (4 * qd + r - t) >= 0 ? d[r] : 0.f;
+        L.frag[G_BYV + wq][lane] = stack_f(d);
+      }
+      // decays and decayed rows of chunk c - 1, all 64 keys: the set-up
+      // wave's own slice and that of the gradient wave of its SIMD
+      if constexpr (kFull) {
         setup_decays(Pn, decay_load(L.dec, wave, t, qd), wave, t, qd);
+        setup_decays(Pn, decay_load(L.dec, wq, t, qd), wq, t, qd);
       }
     }
     lds_barrier();
@@ -484,21 +519,6 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
       if (c < last) flush(c + 1);
 #pragma unroll
       for (int r = 0; r < 4; ++r) out_at(outs[O_DV], 4 * qd + r, jcol) = __builtin_bit_cast(bf16_t, (__bf16)dv[r]);
-      // step products of v, dy, sa (one per wave), as D = X1 Y1^T + X2 Y2^T:
-      // B_yv^T = dy v^T (s >= t), C_dyv^T = v dy^T (s <= t),
-      // B_ysa^T = dy sa^T (s >= t), C_dysa^T = sa dy^T (s <= t)
-      const int x1 = wq == 1 ? S_V : wq == 3 ? S_SAH : S_DY;
-      const int y1 = wq == 0 ? S_V : wq == 2 ? S_SAH : S_DY;
-      const int y2 = wq == 0 ? S_V : wq == 2 ? S_SAL : S_DY;
-      const bf16_t (*const x2)[64] = wq == 2 ? stg[S_DY] : wq == 3 ? stg[S_SAL] : L.zero;
-      bf16x8 px1[2], py1[2], px2[2], py2[2];
-#pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        px1[m] = row_frag(stg[x1], t, m, qd);
-        py1[m] = row_frag(stg[y1], t, m, qd);
-        px2[m] = row_frag(x2, t, m, qd);
-        py2[m] = row_frag(stg[y2], t, m, qd);
-      }
       // step products with dSA (one per wave): B_sav^T = dsa v^T (s > t),
       // C_dsav^T = v dsa^T (s < t), B_sasa^T = dsa sa^T (s > t),
       // C_dsasa^T = sa dsa^T (s < t)
@@ -511,16 +531,7 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
         for (int m = 0; m < 2; ++m) g[m] = Split8{row_frag(stg[yhi], t, m, qd), row_frag(ylo, t, m, qd)};
       }
       __builtin_amdgcn_sched_barrier(0);
-      const int sgn = (wq & 1) ? -1 : 1;   // keep s >= t / s > t (B_), s <= t / s < t (C_)
-      f32x4 d = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        d = mma32(px2[m], py2[m], d);
-        d = mma32(px1[m], py1[m], d);
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) d[r] = sgn * (4 * qd + r - t) >= 0 ? d[r] : 0.f;
-      L.frag[G_BYV + wq][lane] = stack_f(d);
+      const int sgn = (wq & 1) ? -1 : 1;   // keep s > t (B_), s < t (C_)
       // both orientations, the wave keeps one (no branch in the phase)
       f32x4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = d0;
       d0 = mma32x3(q[0], g[0], d0);
@@ -533,9 +544,49 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
       L.frag[G_BSAV + wq][lane] = stack_f(e);
     } else {
       if constexpr (kFull) {
+        // the decayed rows first: the staging waits for phase A's global loads
+        const GramIn gi = products_load(Pn, wq, t, qd);
+        __builtin_amdgcn_sched_barrier(0);
         stage_dec(pre);             // decay rows of chunk c - 2 (the decays of phase A are done)
         stage_grad(pre, sb ^ 1);    // gradient rows of chunk c - 1 (free buffer)
-        setup_products(Pn, products_load(Pn, wq, t, qd), wq, t, qd, lane);
+        setup_products(Pn, gi, wq, t, qd, lane);
+      }
+    }
+    // Phase C's operands that phase B does not write, read before the
+    // barrier so that their latency overlaps the wait (the decayed rows and
+    // the step products with v, dy, sa of chunk c, dS' and dSA from phase A,
+    // the staged rows); only the products with dSA from phase B are read after.
+    const int kb = wq;
+    Split4 Rc, Ac, Kc, Bc;   // decayed rows as B operands (k = step, column = key), split
+    Split8 Db[2];            // dS' as B operand (k = value j, column = key ki)
+    f32x4 g4;
+    bf16x8 cv0, cv1, f_b0, f_b1;   // gradient wave: v rows, B_yv, B_ysa; set-up wave: dy rows, C_dyv, C_dysa
+    Split8 cs0, cs1;               // gradient wave: sa rows; set-up wave: dSA rows
+    f32x4 lw4;
+    {
+      Rc = Split4{tr_frag(P.rows[T_RH], 0, 16 * kb, lane), tr_frag(P.rows[T_RL], 0, 16 * kb, lane)};
+      Ac = Split4{tr_frag(P.rows[T_AH], 0, 16 * kb, lane), tr_frag(P.rows[T_AL], 0, 16 * kb, lane)};
+      Kc = Split4{tr_frag(P.rows[T_KH], 0, 16 * kb, lane), tr_frag(P.rows[T_KL], 0, 16 * kb, lane)};
+      Bc = Split4{tr_frag(P.rows[T_BH], 0, 16 * kb, lane), tr_frag(P.rows[T_BL], 0, 16 * kb, lane)};
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+        Db[m] = Split8{tr_frag32(L.xds[0], m, 16 * kb, lane), tr_frag32(L.xds[1], m, 16 * kb, lane)};
+      g4 = *reinterpret_cast<const f32x4*>(&P.gT[ki][4 * qd]);
+      if (grad) {
+        cv0 = row_frag(stg[S_V], t, 0, qd);
+        cv1 = row_frag(stg[S_V], t, 1, qd);
+        cs0 = row_pair(stg[S_SAH], stg[S_SAL], t, 0, qd);
+        cs1 = row_pair(stg[S_SAH], stg[S_SAL], t, 1, qd);
+        f_b0 = L.frag[G_BYV][lane];
+        f_b1 = L.frag[G_BYSA][lane];
+      } else {
+        cv0 = row_frag(stg[S_DY], t, 0, qd);
+        cv1 = row_frag(stg[S_DY], t, 1, qd);
+        cs0 = Split8{dsa_frag(0, 0), dsa_frag(1, 0)};
+        cs1 = Split8{dsa_frag(0, 1), dsa_frag(1, 1)};
+        f_b0 = L.frag[G_CDYV][lane];
+        f_b1 = L.frag[G_CDYSA][lane];
+        lw4 = *reinterpret_cast<const f32x4*>(&P.lwT[ki][4 * qd]);
       }
     }
     lds_barrier();
@@ -544,27 +595,14 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
     // result layout rows = step 4 qd + r, column = key ki; the gradient wave
     // forms dK and dB, the set-up wave dR, dA and the decay gradient's parts
     {
-      const int kb = wq;
-      // decayed rows as B operands (k = step, column = key), split
-      const Split4 Rc{tr_frag(P.rows[T_RH], 0, 16 * kb, lane), tr_frag(P.rows[T_RL], 0, 16 * kb, lane)};
-      const Split4 Ac{tr_frag(P.rows[T_AH], 0, 16 * kb, lane), tr_frag(P.rows[T_AL], 0, 16 * kb, lane)};
-      const Split4 Kc{tr_frag(P.rows[T_KH], 0, 16 * kb, lane), tr_frag(P.rows[T_KL], 0, 16 * kb, lane)};
-      const Split4 Bc{tr_frag(P.rows[T_BH], 0, 16 * kb, lane), tr_frag(P.rows[T_BL], 0, 16 * kb, lane)};
-      // dS' as B operand (k = value j, column = key ki)
-      Split8 Db[2];
-#pragma unroll
-      for (int m = 0; m < 2; ++m)
-        Db[m] = Split8{tr_frag32(L.xds[0], m, 16 * kb, lane), tr_frag32(L.xds[1], m, 16 * kb, lane)};
-      const f32x4 g4 = *reinterpret_cast<const f32x4*>(&P.gT[ki][4 * qd]);
       const f32x4 z = {0.f, 0.f, 0.f, 0.f};
       float epart = 0.f;
       f32x4 f, suf;
       if (grad) {
-        const bf16x8 v0 = row_frag(stg[S_V], t, 0, qd), v1 = row_frag(stg[S_V], t, 1, qd);
-        const Split8 s0f = row_pair(stg[S_SAH], stg[S_SAL], t, 0, qd);
-        const Split8 s1f = row_pair(stg[S_SAH], stg[S_SAL], t, 1, qd);
-        const bf16x8 f_byv = L.frag[G_BYV][lane], f_bsav = L.frag[G_BSAV][lane];
-        const bf16x8 f_bysa = L.frag[G_BYSA][lane], f_bsasa = L.frag[G_BSASA][lane];
+        const bf16x8 v0 = cv0, v1 = cv1;
+        const Split8 s0f = cs0, s1f = cs1;
+        const bf16x8 f_byv = f_b0, f_bysa = f_b1;
+        const bf16x8 f_bsav = L.frag[G_BSAV][lane], f_bsasa = L.frag[G_BSASA][lane];
         __builtin_amdgcn_sched_barrier(0);
         // V dS' (= d k- gamma_L) and SA dS' (= d b- gamma_L)
         f32x4 x1 = mma32(v0, Db[0].lo, z);
@@ -601,11 +639,10 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
             S0v[m][1] = *reinterpret_cast<const f32x4*>(&s0r[ki][32 * m + 16 + 4 * qd]);
           }
         }
-        const bf16x8 y0 = row_frag(stg[S_DY], t, 0, qd), y1 = row_frag(stg[S_DY], t, 1, qd);
-        const Split8 q0{dsa_frag(0, 0), dsa_frag(1, 0)}, q1{dsa_frag(0, 1), dsa_frag(1, 1)};
-        const bf16x8 f_cdyv = L.frag[G_CDYV][lane], f_cdysa = L.frag[G_CDYSA][lane];
+        const bf16x8 y0 = cv0, y1 = cv1;
+        const Split8 q0 = cs0, q1 = cs1;
+        const bf16x8 f_cdyv = f_b0, f_cdysa = f_b1;
         const bf16x8 f_cdsav = L.frag[G_CDSAV][lane], f_cdsasa = L.frag[G_CDSASA][lane];
-        const f32x4 lw4 = *reinterpret_cast<const f32x4*>(&P.lwT[ki][4 * qd]);
         __builtin_amdgcn_sched_barrier(0);
         Split8 S0b[2];
 #pragma unroll
@@ -651,16 +688,7 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
       suf[2] = f[2] + suf[3];
       suf[1] = f[1] + suf[2];
       suf[0] = f[0] + suf[1];
-      L.red[wave][0][qd][t] = suf[0];
-      L.red[wave][1][qd][t] = epart;
-      wave_lds_sync();
-      float above = 0.f, etot = 0.f;
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const float fq = L.red[wave][0][q4][t];
-        above += q4 > qd ? fq : 0.f;
-        etot += L.red[wave][1][q4][t];
-      }
+      const float above = rows_after(suf[0], qd), etot = rows_total(epart);
       // dlw = (R^ o dr' + A^ o da' suffix) - (K~ o dk' + B~ o db' suffix)
       //       - a da + E: the gradient wave leaves its part, the set-up wave
       //       keeps its own and combines after the next barrier
