@@ -209,15 +209,47 @@ __device__ __forceinline__ F4 diff_grad_at(const ShiftMixArgs& a, const F4 (&mu)
   return dd;
 }
 
+// Raw 4-element loads, widened later, so that a group of rows can have all
+// its loads in flight before any is used
+template <bool BF> struct Raw4;
+template <> struct Raw4<true> {
+  typedef uint2 type;
+  static __device__ __forceinline__ type load(const void* base, int64_t i) {
+    return *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + i);
+  }
+  static __device__ __forceinline__ F4 widen(type r) {
+    return F4{{bf16_to_f32(r.x & 0xffffu), bf16_to_f32(r.x >> 16), bf16_to_f32(r.y & 0xffffu),
+               bf16_to_f32(r.y >> 16)}};
+  }
+};
+template <> struct Raw4<false> {
+  typedef float4 type;
+  static __device__ __forceinline__ type load(const void* base, int64_t i) {
+    return *reinterpret_cast<const float4*>(static_cast<const float*>(base) + i);
+  }
+  static __device__ __forceinline__ F4 widen(type r) { return F4{{r.x, r.y, r.z, r.w}}; }
+};
+
+// The backward of a wave's rows: dx_t = sum_i g_i - m_t dd_t + m_t m_(t+1)
+// dd_(t+1), with dd_t = sum_i g_i scale_i (+ the diff gradient), the last
+// term only within a sequence. Rows are independent except for that term, so
+// the rows go in groups of kGroup whose loads (row indices clamped to the
+// tensor, so that they need no branch) are all issued before any is used; a
+// row's dx is stored when the next row's masked dd is known. (One row's loads
+// in flight per wave left the kernel bound by HBM latency.)
 template <bool XB, bool OB, int KM>
 __global__ __launch_bounds__(256) void shift_mix_backward_kernel(ShiftMixArgs a) {
   __shared__ float red[4][KM][kMixColsPerBlock];
+  constexpr int R = kMixRowsPerWave, kGroup = 4;
+  static_assert(R % kGroup == 0, "whole groups of rows");
+  typedef Raw4<XB> RX;
+  typedef Raw4<OB> RG;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t C = a.C;
   const int64_t c = (static_cast<int64_t>(blockIdx.y) * 64 + lane) * 4;
   const int64_t rows = a.batch * a.T;
-  const int64_t r0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * kMixRowsPerWave;
-  const int64_t r1 = r0 + kMixRowsPerWave < rows ? r0 + kMixRowsPerWave : rows;
+  const int64_t r0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * R;
+  const int64_t r1 = r0 + R < rows ? r0 + R : rows;
   const bool active = c < C;
   F4 mu[KM], acc[KM];
 #pragma unroll
@@ -226,59 +258,91 @@ __global__ __launch_bounds__(256) void shift_mix_backward_kernel(ShiftMixArgs a)
     acc[i] = zero4();
   }
   if (active && r0 < r1) {
-    const int64_t rl = r1 - 1;
-    int64_t b = rl / a.T, t = rl - b * a.T;
-    // masked diff gradient of the step after the run, when it is in the same sequence
-    F4 mdd_next = zero4();
-    if (t + 1 < a.T) {
-      const float m = a.mask ? load1<XB>(a.mask, r1) : 1.f;
-      const F4 dd = diff_grad_at<OB, KM>(a, mu, r1, c);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) mdd_next.v[j] = m * dd.v[j];
+    const int n = static_cast<int>(r1 - r0);
+    const int64_t b0 = r0 / a.T, t0 = r0 - b0 * a.T;
+    // the row before the first, for the first row's difference
+    F4 xprev = zero4();
+    bool prev_valid = false;
+    if (t0 > 0) {
+      xprev = load4<XB>(a.x, (r0 - 1) * C + c);
+      prev_valid = valid<XB>(a, r0 - 1);
     }
-    F4 xt = load4<XB>(a.x, rl * C + c);
-    for (int64_t r = rl; r >= r0; --r) {
-      const float m = a.mask ? load1<XB>(a.mask, r) : 1.f;
-      // the forward's difference at this step, for the scale gradients
-      const F4 xp = t > 0 ? load4<XB>(a.x, (r - 1) * C + c) : zero4();
-      const F4 prev = (t > 0 && valid<XB>(a, r - 1)) ? xp : external_shift<XB>(a, b, c);
-      F4 d;
+    // the previous row, whose dx waits for this row's masked dd
+    F4 p_gs = zero4(), p_mdd = zero4();
+    float p_m = 0.f;
+    int64_t b = b0, t = t0;
+    auto store_prev = [&](int i, const F4& next_mdd, bool has_next) {
+      F4 dx;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) d.v[j] = m != 0.f ? prev.v[j] - xt.v[j] : 0.f;
-      // each mix gradient is read once and folded into dd, their sum and
-      // the scale gradients
-      F4 dd = a.diff_grad ? load4<OB>(a.diff_grad, r * C + c) : zero4();
-      F4 gs = zero4();
+      for (int j = 0; j < 4; ++j)
+        dx.v[j] = p_gs.v[j] - p_mdd.v[j] + (has_next ? p_m * next_mdd.v[j] : 0.f);
+      store4<XB>(a.x_grad, (r0 + i) * C + c, dx);
+    };
 #pragma unroll
-      for (int i = 0; i < KM; ++i) {
-        if (i < a.num_mixes) {
-          const F4 g = load4<OB>(a.mix_grads[i], r * C + c);
+    for (int g0 = 0; g0 < R; g0 += kGroup) {
+      typename RX::type xr[kGroup];
+      typename RG::type gr[kGroup][KM], dr[kGroup];
+      float mr[kGroup];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            dd.v[j] += g.v[j] * mu[i].v[j];
-            gs.v[j] += g.v[j];
-            acc[i].v[j] += g.v[j] * d.v[j];
+      for (int i = 0; i < kGroup; ++i) {
+        const int64_t r = r0 + (g0 + i < n ? g0 + i : n - 1);   // clamped: in bounds, no branch
+        xr[i] = RX::load(a.x, r * C + c);
+        mr[i] = a.mask ? load1<XB>(a.mask, r) : 1.f;
+        if (a.diff_grad) dr[i] = RG::load(a.diff_grad, r * C + c);
+#pragma unroll
+        for (int k = 0; k < KM; ++k)
+          if (k < a.num_mixes) gr[i][k] = RG::load(a.mix_grads[k], r * C + c);
+      }
+#pragma unroll
+      for (int i = 0; i < kGroup; ++i) {
+        if (g0 + i < n) {
+          const float m = mr[i];
+          const F4 xt = RX::widen(xr[i]);
+          const F4 prev = (t > 0 && prev_valid) ? xprev : external_shift<XB>(a, b, c);
+          F4 d;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) d.v[j] = m != 0.f ? prev.v[j] - xt.v[j] : 0.f;
+          F4 dd = a.diff_grad ? RG::widen(dr[i]) : zero4();
+          F4 gs = zero4();
+#pragma unroll
+          for (int k = 0; k < KM; ++k) {
+            if (k < a.num_mixes) {
+              const F4 g = RG::widen(gr[i][k]);
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                dd.v[j] += g.v[j] * mu[k].v[j];
+                gs.v[j] += g.v[j];
+                acc[k].v[j] += g.v[j] * d.v[j];
+              }
+            }
+          }
+          F4 mdd;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) mdd.v[j] = m * dd.v[j];
+          // the previous row is in this row's sequence unless this row starts one
+          if (g0 + i > 0) store_prev(g0 + i - 1, mdd, t > 0);
+          p_gs = gs;
+          p_mdd = mdd;
+          p_m = m;
+          xprev = xt;
+          prev_valid = m != 0.f;
+          if (++t == a.T) {
+            t = 0;
+            ++b;
           }
         }
       }
-      const bool has_next = t + 1 < a.T;
-      F4 mdd, dx;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        mdd.v[j] = m * dd.v[j];
-        dx.v[j] = gs.v[j] - mdd.v[j] + (has_next ? m * mdd_next.v[j] : 0.f);
-      }
-      store4<XB>(a.x_grad, r * C + c, dx);
-      mdd_next = mdd;
-      if (t > 0) {
-        xt = xp;
-        --t;
-      } else {
-        t = a.T - 1;
-        --b;
-        if (r - 1 >= r0) xt = load4<XB>(a.x, (r - 1) * C + c);
-      }
     }
+    // the last row: the row after it, when it is in the same sequence (t is
+    // now that row's step, 0 when a new sequence starts there)
+    F4 after = zero4();
+    if (t > 0) {
+      const float m = a.mask ? load1<XB>(a.mask, r1) : 1.f;
+      const F4 dd = diff_grad_at<OB, KM>(a, mu, r1, c);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) after.v[j] = m * dd.v[j];
+    }
+    store_prev(n - 1, after, t > 0);
   }
   // block partial of the scale gradients: the four waves hold the same channels
 #pragma unroll
@@ -301,9 +365,13 @@ __global__ __launch_bounds__(256) void shift_mix_backward_kernel(ShiftMixArgs a)
   }
 }
 
-// the external shift's gradient: the masked diff gradient at every valid step
-// whose previous step is not valid (t = 0 included); rows of the full batch
-// that no batch id names are zero (filled before)
+// the external shift's gradient as the reference's autodiff forms it
+// (token_shift_diff/backward.rs:51-97): the masked diff gradient m_t dd_t
+// weighted by m_t (1 - m_(t-1)) (m_(-1) = 0), summed over the steps, and
+// added into the row's slot (select_assign with Add): rows whose batch ids
+// repeat add up. The buffer is zero-filled before; with distinct ids each
+// slot receives one addition, so the result does not depend on order. For
+// 0/1 masks the weight picks the valid steps whose previous step is masked.
 template <bool XB, bool OB, int KM>
 __global__ __launch_bounds__(256) void shift_grad_kernel(ShiftMixArgs a) {
   const int64_t c = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
@@ -314,19 +382,24 @@ __global__ __launch_bounds__(256) void shift_grad_kernel(ShiftMixArgs a) {
   for (int i = 0; i < KM; ++i)
     mu[i] = i < a.num_mixes ? load4<false>(a.scales, i * a.C + c) : zero4();
   F4 acc = zero4();
+  float mprev = 0.f;
   for (int64_t t = 0; t < a.T; ++t) {
     const int64_t r = b * a.T + t;
     const float m = a.mask ? load1<XB>(a.mask, r) : 1.f;
-    const bool start = m != 0.f && (t == 0 || !valid<XB>(a, r - 1));
-    if (start) {
+    const float w = m * (1.f - mprev);   // use_external_shift
+    if (w != 0.f) {
       const F4 dd = diff_grad_at<OB, KM>(a, mu, r, c);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc.v[j] += m * m * dd.v[j];
+      for (int j = 0; j < 4; ++j) acc.v[j] += (dd.v[j] * m) * w;
     }
-    if (!a.mask) break;  // without a mask only t = 0 starts a run
+    mprev = m;
+    if (!a.mask) break;  // without a mask only t = 0 has a weight
   }
   const int64_t slot = slot_of(a, b);
-  if (slot >= 0) store4<false>(a.shift_grad, slot * a.C + c, acc);
+  if (slot >= 0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) atomicAdd(a.shift_grad + slot * a.C + c + j, acc.v[j]);
+  }
 }
 
 __global__ __launch_bounds__(256) void fill_zero_kernel(float* p, int64_t n) {

@@ -120,6 +120,68 @@ def test_token_shift_mix_matches_torch(case):
         assert _err(got_next, want_next) == 0.0        # a copy of x or of the shift
 
 
+def _reference_shift_backward(x, scales, shift_rows, mask, grads):
+    """The token shift + mixes' gradients as the reference's autodiff forms
+    them, restated in float64 (token_shift_diff/backward.rs:51-97 for x and
+    the external shift, addcmul's backward for the mixes), for any mask
+    values: the forward treats a step as valid when its mask is not 0
+    (token_shift_diff/kernel.rs:51-60); the backward weights with the mask
+    values. Returns dx, dscales (one per scale), dshift_rows."""
+    B, T, C = x.shape
+    m = mask.double()
+    valid = (m != 0).double()
+    ext = shift_rows.double()
+    prev = torch.cat([ext.unsqueeze(1), x[:, :-1]], 1)
+    prev_valid = torch.cat([torch.zeros(B, 1, dtype=torch.float64), valid[:, :-1]], 1)
+    prev = prev_valid.unsqueeze(2) * prev + (1 - prev_valid.unsqueeze(2)) * ext.unsqueeze(1)
+    diff = valid.unsqueeze(2) * (prev - x)
+    dd = sum(g * s.reshape(1, 1, C) for g, s in zip(grads, scales))   # gradient of diff
+    gs = sum(grads)                                                    # of x through x + ...
+    dscales = [(g * diff).sum(dim=(0, 1)) for g in grads]
+    masked = dd * m.unsqueeze(2)
+    shifted_next = torch.cat([masked[:, 1:], torch.zeros(B, 1, C, dtype=torch.float64)], 1)
+    dx = gs - masked + m.unsqueeze(2) * shifted_next
+    prev_m = torch.cat([torch.zeros(B, 1, dtype=torch.float64), m[:, :-1]], 1)
+    use_ext = m * (1 - prev_m)
+    dshift_rows = (masked * use_ext.unsqueeze(2)).sum(1)
+    return dx, dscales, dshift_rows
+
+
+def test_token_shift_backward_with_fractional_mask_values_and_repeated_slots():
+    """Mask values other than 0 and 1 and repeated batch ids, which the
+    reference's autodiff handles by weighting with the mask values and by
+    adding each row's shift gradient into its slot (select_assign with Add):
+    dx, the scale gradients and the external shift's gradient against
+    ``_reference_shift_backward`` in float64; the forward mixes are unchanged
+    by the values (a step is valid when its mask is not 0)."""
+    nb = _nb()
+    B, T, C, K = 4, 13, 128, 6
+    g = torch.Generator().manual_seed(77)
+    x = torch.randn(B, T, C, generator=g, dtype=torch.float64)
+    scales = [torch.rand(C, generator=g, dtype=torch.float64) for _ in range(K)]
+    mask = torch.tensor([0.0, 0.5, 1.0, 0.25, 2.0, 0.0, 0.0, 1.0, 0.75, 1.0, 0.0, 0.5, 1.0],
+                        dtype=torch.float64)
+    mask = torch.stack([mask, mask.roll(3), mask.roll(5), torch.ones(T, dtype=torch.float64)])
+    full = 3
+    ids = torch.tensor([2, 0, 2, 1])          # slot 2 twice
+    shift = torch.randn(full, C, generator=g, dtype=torch.float64)
+    grads = [torch.randn(B, T, C, generator=g, dtype=torch.float64) for _ in range(K)]
+    want_dx, want_dsc, want_rows = _reference_shift_backward(x, scales, shift[ids], mask, grads)
+    want_dshift = torch.zeros(full, C, dtype=torch.float64).index_add_(0, ids, want_rows)
+    dev = torch.device("cuda:0")
+    xg = x.float().to(dev).requires_grad_(True)
+    scg = [s.float().to(dev).requires_grad_(True) for s in scales]
+    shg = shift.float().to(dev).requires_grad_(True)
+    announce("token_shift_mix backward, fractional mask, repeated slots")
+    mixes = nb.token_shift_mix(xg, scg, shg, ids.to(dev), mask.float().to(dev), torch.float32)
+    sum((mx * gg.float().to(dev)).sum() for mx, gg in zip(mixes, grads)).backward()
+    torch.cuda.synchronize()
+    assert _err(xg.grad, want_dx) <= F32_TOL
+    for i in range(K):
+        assert _err(scg[i].grad, want_dsc[i]) <= F32_TOL, i
+    assert _err(shg.grad, want_dshift) <= F32_TOL
+
+
 # --------------------------------------------------------------- gated readout
 READOUT_CASES = [
     dict(B=2, T=24, H=3, op="f32", act="f32"),
