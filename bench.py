@@ -202,7 +202,7 @@ def pmc_summary(dirs):
     import glob
     from collections import defaultdict
     keys = ("wkv7_fwd_chunk_kernel", "wkv7_bwd_chunk_kernel", "wkv7_fwd_kernel",
-            "wkv7_bwd_kernel", "wkv7_infer_kernel", "AbsFunctor")
+            "wkv7_bwd_kernel", "wkv7_infer_kernel", "wkv7_infer_bf16_kernel", "AbsFunctor")
     per = defaultdict(lambda: defaultdict(lambda: defaultdict(float)))
     for d in dirs:
         for path in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
@@ -244,6 +244,113 @@ def pmc_summary(dirs):
             print(f"mfma_flop_issued {k}: {int(round(cs['SQ_INSTS_VALU_MFMA_MOPS_BF16'] * 512))}")
         if "SQ_INSTS_VALU" in cs:
             print(f"valu_insts {k}: {int(round(cs['SQ_INSTS_VALU']))}")
+
+
+def short_kernel_name(name: str) -> str:
+    """A rocprofv3 kernel name without return type, namespaces and arguments."""
+    name = name.replace("void ", "").replace("(anonymous namespace)::", "")
+    for ns in ("wkv7::", "rwkv_nb::", "rwkv_loss::"):
+        name = name.replace(ns, "")
+    return name.split("(")[0]
+
+
+def neighbor_bytes(cfg):
+    """Algorithmic HBM bytes per dispatch of the fused kernels beside the
+    operator in the config[4] step (R tokens x C channels; fp32 residual
+    stream, bf16 mixes, operands and gradients; bf16 logits)."""
+    R, C, V = cfg["B"] * cfg["T"], cfg["H"] * N_HEAD, cfg["vocab"]
+    rc = R * C
+    return {
+        "shift_mix_forward_kernel<false, true, 6>": (rc * 4 + 6 * rc * 2, "x fp32 in, 6 bf16 mixes out"),
+        "shift_mix_forward_kernel<false, true, 1>": (rc * 4 + rc * 2, "x fp32 in, 1 bf16 mix out"),
+        "shift_mix_backward_kernel<false, true, 6>": (6 * rc * 2 + 2 * rc * 4, "6 bf16 mix grads + x in, dx fp32 out"),
+        "shift_mix_backward_kernel<false, true, 1>": (rc * 2 + 2 * rc * 4, "1 bf16 mix grad + x in, dx fp32 out"),
+        "readout_forward_kernel<true, true>": (6 * rc * 2, "y, r, k~, v, gate bf16 in, out bf16"),
+        "readout_backward_kernel<true, true>": (11 * rc * 2, "+ dout in; dy, dr, dk~, dv, dgate out"),
+        "prepare_forward_kernel<true, true, true>": (11 * rc * 2, "6 bf16 products in, 5 bf16 operands out"),
+        "prepare_forward_kernel<true, true, false>": (9 * rc * 2, "first cell: 4 in, 5 out"),
+        "prepare_backward_kernel<true, true, true>": (17 * rc * 2, "6 products + 5 operand grads in, 6 grads out"),
+        "prepare_backward_kernel<true, true, false>": (13 * rc * 2, "first cell: 4 + 5 in, 4 out"),
+        "xent_forward_kernel<true, true>": (R * V * 2, f"bf16 logits in ({R} x {V})"),
+        "xent_backward_kernel<true, true>": (2 * R * V * 2, "bf16 logits in, bf16 gradient out"),
+    }
+
+
+def kernel_category(name: str) -> str:
+    if "wkv7::" in name:
+        return "WKV7 (this library)"
+    if "rwkv_nb::" in name:
+        return "fused neighbours (this library)"
+    if "rwkv_loss::" in name:
+        return "fused loss (this library)"
+    if name.startswith(("Cijk", "Custom_Cijk")):
+        return "GEMM (hipBLASLt)"
+    if "elementwise" in name or "Functor" in name:
+        return "element-wise (torch)"
+    if "reduce_kernel" in name:
+        return "reductions (torch)"
+    if "norm" in name.lower() or "GammaBeta" in name:
+        return "layer/group norm (torch)"
+    if "multi_tensor_apply" in name:
+        return "optimizer (torch fused AdamW)"
+    if "copyBuffer" in name or "fillBuffer" in name:
+        return "runtime copies / fills"
+    return "other (torch)"
+
+
+def stats_summary(directory, config, traced_steps):
+    """Markdown tables from a rocprofv3 --kernel-trace --stats CSV directory:
+    this library's kernels (dispatches per traced step, mean / median / min /
+    max duration); for cfg4 also GPU time by category and the fused
+    neighbour kernels against their algorithmic bytes."""
+    import csv
+    import glob
+    from collections import defaultdict
+
+    def one(pattern):
+        paths = glob.glob(os.path.join(directory, "**", pattern), recursive=True)
+        if not paths:
+            raise SystemExit(f"no {pattern} under {directory}")
+        with open(paths[0]) as f:
+            return list(csv.DictReader(f))
+
+    stats, trace = one("*kernel_stats.csv"), one("*kernel_trace.csv")
+    durs = defaultdict(list)
+    for r in trace:
+        durs[r["Kernel_Name"]].append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+    mine = [r for r in stats if any(s in r["Name"] for s in ("wkv7::", "rwkv_nb::", "rwkv_loss::"))]
+    print(f"Traced steps: {traced_steps} (warm-up + timed).\n")
+    print("| kernel | dispatches / step | mean µs | median µs | min µs | max µs | ms / step |")
+    print("|---|---|---|---|---|---|---|")
+    for r in sorted(mine, key=lambda r: -float(r["TotalDurationNs"])):
+        d = sorted(durs[r["Name"]])
+        print(f"| `{short_kernel_name(r['Name'])}` | {int(r['Calls']) / traced_steps:g} | "
+              f"{float(r['AverageNs']) / 1e3:.1f} | {d[len(d) // 2] / 1e3:.1f} | "
+              f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | "
+              f"{float(r['TotalDurationNs']) / 1e6 / traced_steps:.3f} |")
+    if config != "cfg4":
+        return
+    total = sum(float(r["TotalDurationNs"]) for r in stats)
+    cats = defaultdict(float)
+    for r in stats:
+        cats[kernel_category(r["Name"])] += float(r["TotalDurationNs"])
+    print(f"\nTraced GPU kernel time: {total / 1e6 / traced_steps:.2f} ms per step.\n")
+    print("| category | ms / step | share |\n|---|---|---|")
+    for c, v in sorted(cats.items(), key=lambda kv: -kv[1]):
+        print(f"| {c} | {v / 1e6 / traced_steps:.2f} | {100 * v / total:.1f}% |")
+    alg = neighbor_bytes(CONFIGS[config])
+    print("\nFused neighbour and loss kernels against their algorithmic bytes (median "
+          "dispatch; MI355X HBM peak 8 TB/s):\n")
+    print("| kernel | median µs | algorithmic MB | achieved TB/s | of peak | bytes |")
+    print("|---|---|---|---|---|---|")
+    for name, d in durs.items():
+        k = short_kernel_name(name)
+        if k in alg:
+            d = sorted(d)
+            med = d[len(d) // 2] * 1e-9
+            nb, what = alg[k]
+            print(f"| `{k}` | {med * 1e6:.1f} | {nb / 1e6:.1f} | {nb / med / 1e12:.2f} | "
+                  f"{nb / med / PEAK_HBM:.2f} | {what} |")
 
 
 def bench_train(cfg, steps, warmup, with_cpu, probe=False, kernels="auto"):
@@ -513,9 +620,18 @@ def main():
                     help="also launch one plain copy of known size (counter calibration)")
     ap.add_argument("--pmc-summary", nargs="+", metavar="DIR",
                     help="summarise rocprofv3 --pmc CSV output directories and exit")
+    ap.add_argument("--stats-summary", metavar="DIR",
+                    help="summarise a rocprofv3 --kernel-trace --stats CSV directory of a "
+                         "--config run and exit")
+    ap.add_argument("--traced-steps", type=int, default=0,
+                    help="--stats-summary: steps the trace holds (default warm-up + steps)")
     args = ap.parse_args()
     if args.pmc_summary:
         pmc_summary(args.pmc_summary)
+        return
+    if args.stats_summary:
+        stats_summary(args.stats_summary, args.config,
+                      args.traced_steps or (args.steps + args.warmup))
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the WKV7 operator needs no collective, and "
