@@ -8,6 +8,7 @@
 
 #include <cmath>
 #include <cstdint>
+#include <initializer_list>
 #include <vector>
 
 #include "neighbors_launch.hpp"
@@ -43,6 +44,23 @@ bool any_overlap(const std::vector<Range>& outs, const std::vector<Range>& ins) 
 }
 
 bool valid_dtype(int d) { return d == WKV7_DTYPE_F32 || d == WKV7_DTYPE_BF16; }
+
+// the product of the factors fits int64 (no wrap-around)
+bool product_fits(std::initializer_list<int64_t> factors) {
+  int64_t acc = 1;
+  for (int64_t f : factors)
+    if (__builtin_mul_overflow(acc, f, &acc)) return false;
+  return true;
+}
+// Every byte count these checks and the workspace sizes form is at most
+// elements x 8 x (sums per element) of one of the shapes below, so shapes
+// for which those products fit int64 never overflow.
+bool mix_sizes_fit(int64_t rows, int64_t C, int64_t full_batch) {
+  return product_fits({rows, C, 8, rwkv_nb::kMaxMixes}) && product_fits({full_batch, C, 8});
+}
+bool head_rows_fit(int64_t rows, int64_t H, int64_t sums) {
+  return product_fits({rows, H, 64, 8, sums});
+}
 int64_t esize(int d) { return d == WKV7_DTYPE_BF16 ? 2 : 4; }
 bool aligned_for(const void* p, int d) {
   return (reinterpret_cast<uintptr_t>(p) % (d == WKV7_DTYPE_BF16 ? 8 : 16)) == 0;
@@ -58,6 +76,7 @@ int check_shift_mix(const void* x, const void* shift, const int32_t* batch_ids,
   if (B > kMaxGridY || C / rwkv_nb::kMixColsPerBlock + 1 > kMaxGridY) return WKV7_ERR_SHAPE;
   if (T > 0 && B > INT64_MAX / T) return WKV7_ERR_SHAPE;
   const int64_t rows = B * T;
+  if (!mix_sizes_fit(rows, C, full_batch)) return WKV7_ERR_SHAPE;
   if (rwkv_nb::mix_row_blocks(rows) > kMaxGridX) return WKV7_ERR_SHAPE;
   if (rows > 0 && !x) return WKV7_ERR_NULL_POINTER;
   if (K > 0 && !scales) return WKV7_ERR_NULL_POINTER;
@@ -79,6 +98,7 @@ int check_readout(const void* y, const void* r, const void* k, const void* v, co
   if (!valid_dtype(dtype) || !valid_dtype(act_dtype)) return WKV7_ERR_DTYPE;
   if (N != 64) return WKV7_ERR_HEAD_SIZE;
   if (rows < 0 || H <= 0 || H > kMaxGridY) return WKV7_ERR_SHAPE;
+  if (!head_rows_fit(rows, H, rwkv_nb::kReadoutSums)) return WKV7_ERR_SHAPE;
   if (rwkv_nb::readout_row_blocks(rows) > kMaxGridX) return WKV7_ERR_SHAPE;
   if (!(eps >= 0.f) || !std::isfinite(eps)) return WKV7_ERR_SHAPE;
   if (!bonus || !weight || !bias) return WKV7_ERR_NULL_POINTER;
@@ -100,6 +120,7 @@ int check_prepare(const void* key, const void* value, const void* value_first, c
   if (!valid_dtype(dtype) || !valid_dtype(out_dtype)) return WKV7_ERR_DTYPE;
   if (N != 64) return WKV7_ERR_HEAD_SIZE;
   if (rows < 0 || H <= 0 || H > kMaxGridY) return WKV7_ERR_SHAPE;
+  if (!head_rows_fit(rows, H, rwkv_nb::kPrepareSums)) return WKV7_ERR_SHAPE;
   if (rwkv_nb::prepare_row_blocks(rows) > kMaxGridX) return WKV7_ERR_SHAPE;
   if (!lr_bias || !wd_bias || !ka || !kk) return WKV7_ERR_NULL_POINTER;
   const bool res = vr_bias != nullptr;
@@ -156,6 +177,7 @@ int64_t rwkv_token_shift_mix_workspace_bytes(int64_t num_mixes, int64_t batch_si
       embedded_dim <= 0 || embedded_dim % 4 != 0)
     return -1;
   if (context_len > 0 && batch_size > INT64_MAX / context_len) return -1;
+  if (!mix_sizes_fit(batch_size * context_len, embedded_dim, 0)) return -1;
   return shift_mix_workspace(num_mixes, batch_size, context_len, embedded_dim);
 }
 
@@ -292,6 +314,7 @@ int rwkv_token_shift_mix_backward(const void* embedded_context, const void* embe
 
 int64_t rwkv_gated_readout_workspace_bytes(int64_t rows, int64_t num_heads, int64_t head_size) {
   if (rows < 0 || num_heads <= 0 || head_size != 64) return -1;
+  if (!head_rows_fit(rows, num_heads, rwkv_nb::kReadoutSums)) return -1;
   return readout_workspace(rows, num_heads);
 }
 
@@ -457,6 +480,7 @@ int rwkv_gated_readout_backward_noalloc(
 
 int64_t rwkv_weight_prepare_workspace_bytes(int64_t rows, int64_t num_heads, int64_t head_size) {
   if (rows < 0 || num_heads <= 0 || num_heads > kMaxGridY || head_size != 64) return -1;
+  if (!head_rows_fit(rows, num_heads, rwkv_nb::kPrepareSums)) return -1;
   return prepare_workspace(rows, num_heads);
 }
 

@@ -221,6 +221,18 @@ def test_cross_entropy_l2wrap_validation(lib):
     assert bwd(dx=FAKE * 5) == 7                     # gradient over a row array
 
 
+def test_sizes_whose_byte_counts_overflow_are_refused(lib):
+    # shapes valid per dimension whose byte counts (tensors or workspaces)
+    # exceed int64: refused before any product wraps around
+    assert lib.rwkv_token_shift_mix_workspace_bytes(6, 2 ** 20, 2 ** 20, 2 ** 24) == -1
+    assert lib.rwkv_gated_readout_workspace_bytes(2 ** 62, 12, 64) == -1
+    assert lib.rwkv_weight_prepare_workspace_bytes(2 ** 62, 12, 64) == -1
+    # 2^40 slots x 2^23 channels x 4 bytes of token shift
+    assert mix_fwd(lib, ids=FAKE * 3, shift=FAKE * 4, full=2 ** 40, C=2 ** 23) == 2
+    assert ro_fwd(lib, rows=2 ** 37 - 64, H=65535) == 2
+    assert prep_fwd(lib, rows=2 ** 37 - 64, H=65535) == 2
+
+
 def test_hip_neighbour_ops_refuse_cpu_tensors():
     import torch
     nb = load_pkg().neighbors
