@@ -78,12 +78,21 @@ __device__ __forceinline__ f32x4 mma32x3(const Split8& a, const Split8& b, f32x4
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
-// two values to bf16 hi and lo parts, one packed conversion each
+// two values to bf16 hi and lo parts, one packed conversion each. The
+// residual x - hi comes from one bf16 dot product per value, x + hi_pair .
+// (-1, -0), instead of widening hi and subtracting (two instructions). x - hi
+// is exact in fp32, so this matches the subtraction bit for bit (measured on
+// 2^24 random fp32 values) except where |x| rounds to infinity in bf16 or the
+// residual is below fp32's smallest normal (flushed: an error below 2^-126).
+// The constants hold -0 rather than 0: this toolchain encodes (-1, 0) as the
+// inline constant -1.0, which the instruction reads as another 16-bit value
+// (measured: products of about hi / 128), while (-1, -0) stays a literal.
 __device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t& lo) {
-  const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
-  const float ah = __uint_as_float(h << 16), bh = __uint_as_float(h & 0xffff0000u);
-  hi = h;
-  lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a - ah, b - bh}, bf16x2));
+  const bf16x2 h = __builtin_convertvector(f32x2{a, b}, bf16x2);
+  const float la = __builtin_amdgcn_fdot2_f32_bf16(h, bf16x2{(__bf16)-1.0f, (__bf16)-0.0f}, a, false);
+  const float lb = __builtin_amdgcn_fdot2_f32_bf16(h, bf16x2{(__bf16)-0.0f, (__bf16)-1.0f}, b, false);
+  hi = __builtin_bit_cast(uint32_t, h);
+  lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{la, lb}, bf16x2));
 }
 __device__ __forceinline__ Split4 split4(f32x4 x) {
   uint32_t h0, l0, h1, l1;

@@ -532,13 +532,15 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
       }
       __builtin_amdgcn_sched_barrier(0);
       const int sgn = (wq & 1) ? -1 : 1;   // keep s > t (B_), s < t (C_)
-      // both orientations, the wave keeps one (no branch in the phase)
-      f32x4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = d0;
-      d0 = mma32x3(q[0], g[0], d0);
-      d0 = mma32x3(q[1], g[1], d0);
-      d1 = mma32x3(g[0], q[0], d1);
-      d1 = mma32x3(g[1], q[1], d1);
-      f32x4 e = (wq & 1) ? d1 : d0;
+      // the wave's orientation (wq is wave-uniform: a scalar branch)
+      f32x4 e = {0.f, 0.f, 0.f, 0.f};
+      if (wq & 1) {
+        e = mma32x3(g[0], q[0], e);
+        e = mma32x3(g[1], q[1], e);
+      } else {
+        e = mma32x3(q[0], g[0], e);
+        e = mma32x3(q[1], g[1], e);
+      }
 #pragma unroll
       for (int r = 0; r < 4; ++r) e[r] = sgn * (4 * qd + r - t) > 0 ? e[r] : 0.f;
       L.frag[G_BSAV + wq][lane] = stack_f(e);
