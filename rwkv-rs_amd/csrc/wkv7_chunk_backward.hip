@@ -143,6 +143,12 @@ __device__ __forceinline__ Split8 row_pair(const bf16_t (*hi)[64], const bf16_t 
 }
 __device__ __forceinline__ float hi_lo(bf16x4 h, bf16x4 l, int r) { return (float)h[r] + (float)l[r]; }
 
+// The checkpoints and removal_state are read once and the gradients written
+// once per launch: those accesses carry the non-temporal hint (measured: about
+// 1.5% faster at config[1]; the same hint on the forward's checkpoint stores
+// made the forward 18% slower, so the forward does not use it).
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
 // ---- set-up of one chunk, step 1: decays and decayed rows. Each of the 8
 // waves takes keys 8 w .. 8 w + 7, two per lane (keys 8 w + 2 qd, + 1).
 struct DecayIn { uint32_t x, a, r, k, b; };   // two bf16 each
@@ -273,7 +279,7 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
 #pragma unroll
     for (int k = 0; k < kDecayRounds; ++k) pr.dec[k] = *reinterpret_cast<const uint4*>(src[k] + od);
     pr.vy = *reinterpret_cast<const uint4*>(src[kDecayRounds] + (int64_t)kL * cg * tstride + piece_off);
-    pr.sa = *reinterpret_cast<const f32x4*>(sa_src + (int64_t)kL * cg * tstride);
+    pr.sa = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(sa_src + (int64_t)kL * cg * tstride));
     return pr;
   };
   auto stage_dec = [&](const Pre& pr) {
@@ -308,8 +314,8 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
     const float* ck = ckbh + (int64_t)(c - 1) * (kHead * kHead);
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
-      rowv[m][0] = *reinterpret_cast<const f32x4*>(ck + ki * kHead + 32 * m + 4 * qd);
-      rowv[m][1] = *reinterpret_cast<const f32x4*>(ck + ki * kHead + 32 * m + 16 + 4 * qd);
+      rowv[m][0] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(ck + ki * kHead + 32 * m + 4 * qd));
+      rowv[m][1] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(ck + ki * kHead + 32 * m + 16 + 4 * qd));
     }
   };
 
@@ -331,7 +337,7 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
     for (int k = 0; k < kOutRounds; ++k) {
       const int tile = 2 * k + (wq >> 1), row = (utid >> 3) & 15;
       const uint4 v = *reinterpret_cast<const uint4*>(&out_at(L.outs[cc & 1][tile], row, 8 * (utid & 7)));
-      *reinterpret_cast<uint4*>(dst[k] + (int64_t)kL * cc * tstride) = v;
+      __builtin_nontemporal_store(u32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4*>(dst[k] + (int64_t)kL * cc * tstride));
     }
   };
 

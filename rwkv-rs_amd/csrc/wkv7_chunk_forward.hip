@@ -300,6 +300,15 @@ __device__ __forceinline__ const uint4* raw_piece(const FwdChunkParams& p, int64
   return reinterpret_cast<const uint4*>(p.in[vec] + tok0 + (int64_t)(kL * c + step) * tstride +
                                         8 * oct);
 }
+// The raw rows are read once per launch: loaded with the non-temporal hint
+// (measured at config[1]: forward 0.503 -> 0.477 ms, the following backward
+// 1% slower, the pair 1.2% faster; the same hint on the checkpoint stores made
+// the forward 18% slower).
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 load_stream(const uint4* q) {
+  const u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(q));
+  return make_uint4(x[0], x[1], x[2], x[3]);
+}
 
 template <bool kHasS0>
 __global__ __launch_bounds__(kBlock, 1) void wkv7_fwd_chunk_kernel(const FwdChunkParams p) {
@@ -330,12 +339,12 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_fwd_chunk_kernel(const FwdChun
     static_assert(kPieces == 12, "twelve 16-byte pieces per lane and chunk");
     if (s < nchunks) {
 #define RWKV_RAW_LOAD(c) \
-  r0 = *raw_piece(p, tok0, tstride, c, lane, 0); r1 = *raw_piece(p, tok0, tstride, c, lane, 1); \
-  r2 = *raw_piece(p, tok0, tstride, c, lane, 2); r3 = *raw_piece(p, tok0, tstride, c, lane, 3); \
-  r4 = *raw_piece(p, tok0, tstride, c, lane, 4); r5 = *raw_piece(p, tok0, tstride, c, lane, 5); \
-  r6 = *raw_piece(p, tok0, tstride, c, lane, 6); r7 = *raw_piece(p, tok0, tstride, c, lane, 7); \
-  r8 = *raw_piece(p, tok0, tstride, c, lane, 8); r9 = *raw_piece(p, tok0, tstride, c, lane, 9); \
-  r10 = *raw_piece(p, tok0, tstride, c, lane, 10); r11 = *raw_piece(p, tok0, tstride, c, lane, 11);
+  r0 = load_stream(raw_piece(p, tok0, tstride, c, lane, 0)); r1 = load_stream(raw_piece(p, tok0, tstride, c, lane, 1)); \
+  r2 = load_stream(raw_piece(p, tok0, tstride, c, lane, 2)); r3 = load_stream(raw_piece(p, tok0, tstride, c, lane, 3)); \
+  r4 = load_stream(raw_piece(p, tok0, tstride, c, lane, 4)); r5 = load_stream(raw_piece(p, tok0, tstride, c, lane, 5)); \
+  r6 = load_stream(raw_piece(p, tok0, tstride, c, lane, 6)); r7 = load_stream(raw_piece(p, tok0, tstride, c, lane, 7)); \
+  r8 = load_stream(raw_piece(p, tok0, tstride, c, lane, 8)); r9 = load_stream(raw_piece(p, tok0, tstride, c, lane, 9)); \
+  r10 = load_stream(raw_piece(p, tok0, tstride, c, lane, 10)); r11 = load_stream(raw_piece(p, tok0, tstride, c, lane, 11));
       uint4 r0, r1, r2, r3, r4, r5, r6, r7, r8, r9, r10, r11;
       RWKV_RAW_LOAD(s)
       for (int c = s; c < nchunks; c += kSlots) {
