@@ -80,8 +80,17 @@ static_assert(kL * 16 == kSetup, "removal_state rows: four values per set-up thr
 static_assert(O_COUNT * kL * 8 % kSetup == 0, "whole rounds of gradient stores");
 
 // per-chunk set-up, double-buffered (chunk c & 1)
+// a bf16 row tile followed by 64 bytes, so that consecutive tiles (a value's
+// hi and lo halves) start 16 banks apart: a lane's reads of the two halves
+// then hit different banks
+struct PadTile {
+  bf16_t r[kL][64];
+  bf16_t pad[32];
+};
+static_assert(sizeof(PadTile) % 16 == 0, "16-byte aligned tiles");
+
 struct Prep {
-  bf16_t rows[T_COUNT][kL][64];     // decayed rows, rotated
+  PadTile rows[T_COUNT];            // decayed rows, rotated
   float gT[64][kL + 4];             // log2 prefix decay, [key][step]
   float lwT[64][kL + 4];            // log2 step decay, [key][step]
   float gl[64];                     // gamma_L
@@ -90,7 +99,7 @@ struct Prep {
 
 struct BwdLds {
   bf16_t dec[kDecayIn][kL][64];     // x, r, k, a, b rows of the next chunk to set up
-  bf16_t stg[2][S_COUNT][kL][64];   // v, dy, sa hi, sa lo rows, double-buffered
+  PadTile stg[2][S_COUNT];          // v, dy, sa hi, sa lo rows, double-buffered
   Prep prep[2];                     // chunk 0 also keeps its rebuilt start state in prep[1]
   bf16x8 frag[G_COUNT][64];         // step products with v, dy, sa, dsa (stacked)
   bf16_t xds[2][64][64];            // dS' hi/lo, [value j][key i]
@@ -184,17 +193,17 @@ __device__ __forceinline__ void setup_decays(Prep& P, const DecayIn& in, int wav
   }
   uint32_t hi, lo;
   split2(bf_lo(in.a) * gpv[0], bf_hi(in.a) * gpv[1], hi, lo);
-  write2(P.rows[T_AH], t, c0, hi);
-  write2(P.rows[T_AL], t, c0, lo);
+  write2(P.rows[T_AH].r, t, c0, hi);
+  write2(P.rows[T_AL].r, t, c0, lo);
   split2(bf_lo(in.r) * gam[0], bf_hi(in.r) * gam[1], hi, lo);
-  write2(P.rows[T_RH], t, c0, hi);
-  write2(P.rows[T_RL], t, c0, lo);
+  write2(P.rows[T_RH].r, t, c0, hi);
+  write2(P.rows[T_RL].r, t, c0, lo);
   split2(bf_lo(in.k) * gin[0], bf_hi(in.k) * gin[1], hi, lo);
-  write2(P.rows[T_KH], t, c0, hi);
-  write2(P.rows[T_KL], t, c0, lo);
+  write2(P.rows[T_KH].r, t, c0, hi);
+  write2(P.rows[T_KL].r, t, c0, lo);
   split2(bf_lo(in.b) * gin[0], bf_hi(in.b) * gin[1], hi, lo);
-  write2(P.rows[T_BH], t, c0, hi);
-  write2(P.rows[T_BL], t, c0, lo);
+  write2(P.rows[T_BH].r, t, c0, hi);
+  write2(P.rows[T_BL].r, t, c0, lo);
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
     P.gT[c0 + e][t] = g2[e];
@@ -216,8 +225,8 @@ __device__ __forceinline__ GramIn products_load(const Prep& P, int wave, int t, 
   GramIn g;
 #pragma unroll
   for (int m = 0; m < 2; ++m) {
-    g.X[m] = row_pair(P.rows[xa], P.rows[xa + 1], t, m, qd);
-    g.Y[m] = row_pair(P.rows[yb], P.rows[yb + 1], t, m, qd);
+    g.X[m] = row_pair(P.rows[xa].r, P.rows[xa + 1].r, t, m, qd);
+    g.Y[m] = row_pair(P.rows[yb].r, P.rows[yb + 1].r, t, m, qd);
   }
   return g;
 }
@@ -288,10 +297,10 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
       if (2 * k + (wq >> 1) < kDecayIn) reinterpret_cast<uint4*>(&L.dec[0][0][0])[kSetup * k + utid] = pr.dec[k];
   };
   auto stage_grad = [&](const Pre& pr, int sb) {
-    reinterpret_cast<uint4*>(&L.stg[sb][0][0][0])[utid] = pr.vy;   // v rows, then dy rows
+    reinterpret_cast<uint4*>(&L.stg[sb][utid >> 7].r[0][0])[utid & 127] = pr.vy;   // v rows, then dy rows
     const Split4 s = split4(pr.sa);
-    write4(L.stg[sb][S_SAH], utid >> 4, 4 * (utid & 15), s.hi);
-    write4(L.stg[sb][S_SAL], utid >> 4, 4 * (utid & 15), s.lo);
+    write4(L.stg[sb][S_SAH].r, utid >> 4, 4 * (utid & 15), s.hi);
+    write4(L.stg[sb][S_SAL].r, utid >> 4, 4 * (utid & 15), s.lo);
   };
 
   // ---- state gradient (gradient waves): value tile jb = wq, key tiles ib,
@@ -383,7 +392,7 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
     const int sb = c & 1;
     Prep& P = L.prep[sb];
     Prep& Pn = L.prep[sb ^ 1];   // set-up of chunk c - 1
-    const bf16_t (*const stg)[kL][64] = L.stg[sb];
+    const PadTile* const stg = L.stg[sb];
     bf16_t (*const outs)[kL][64] = L.outs[sb];
     S0Rows& s0r = *reinterpret_cast<S0Rows*>(&L.prep[1]);   // used at c == 0 only
     lds_barrier();
@@ -404,7 +413,7 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
 #pragma unroll
           for (int r = 0; r < 4; ++r) S0t[ib][r] = ck[(16 * ib + 4 * qd + r) * kHead + jcol];
         for (int tt = kL - 1; tt >= 0; --tt) {
-          const float vj = __uint_as_float((uint32_t)__builtin_bit_cast(uint16_t, *tile_at(stg[S_V], tt, jcol)) << 16);
+          const float vj = __uint_as_float((uint32_t)__builtin_bit_cast(uint16_t, *tile_at(stg[S_V].r, tt, jcol)) << 16);
           const float sj = p.sa[tok0 + (int64_t)tt * tstride + jcol];
 #pragma unroll
           for (int ib = 0; ib < 4; ++ib) {
@@ -426,18 +435,18 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
       f32x4 glv[4];
 #pragma unroll
       for (int ib = 0; ib < 4; ++ib) glv[ib] = *reinterpret_cast<const f32x4*>(&P.gl[16 * ib + 4 * qd]);
-      const Split8 Bt0 = row_pair(P.rows[T_BH], P.rows[T_BL], t, 0, qd);
-      const Split8 Bt1 = row_pair(P.rows[T_BH], P.rows[T_BL], t, 1, qd);
-      const Split8 Kt0 = row_pair(P.rows[T_KH], P.rows[T_KL], t, 0, qd);
-      const Split8 Kt1 = row_pair(P.rows[T_KH], P.rows[T_KL], t, 1, qd);
-      const bf16x4 dycf = tr_frag(stg[S_DY], 0, 16 * jb, lane);   // dY[s][j] (k = s)
+      const Split8 Bt0 = row_pair(P.rows[T_BH].r, P.rows[T_BL].r, t, 0, qd);
+      const Split8 Bt1 = row_pair(P.rows[T_BH].r, P.rows[T_BL].r, t, 1, qd);
+      const Split8 Kt0 = row_pair(P.rows[T_KH].r, P.rows[T_KL].r, t, 0, qd);
+      const Split8 Kt1 = row_pair(P.rows[T_KH].r, P.rows[T_KL].r, t, 1, qd);
+      const bf16x4 dycf = tr_frag(stg[S_DY].r, 0, 16 * jb, lane);   // dY[s][j] (k = s)
       const bf16x8 f_rbt = P.frag[F_RBT][lane], f_pt = P.frag[F_PT][lane];
       const bf16x8 f_rkt = P.frag[F_RKT][lane], f_akt = P.frag[F_AKT][lane];
       bf16x8 rT[4], aT[4];
 #pragma unroll
       for (int ib = 0; ib < 4; ++ib) {
-        rT[ib] = cat8(tr_frag(P.rows[T_RH], 0, 16 * ib, lane), tr_frag(P.rows[T_RL], 0, 16 * ib, lane));
-        aT[ib] = cat8(tr_frag(P.rows[T_AH], 0, 16 * ib, lane), tr_frag(P.rows[T_AL], 0, 16 * ib, lane));
+        rT[ib] = cat8(tr_frag(P.rows[T_RH].r, 0, 16 * ib, lane), tr_frag(P.rows[T_RL].r, 0, 16 * ib, lane));
+        aT[ib] = cat8(tr_frag(P.rows[T_AH].r, 0, 16 * ib, lane), tr_frag(P.rows[T_AL].r, 0, 16 * ib, lane));
       }
       __builtin_amdgcn_sched_barrier(0);
       f32x4 dSp[4];
@@ -486,14 +495,14 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
         const int x1 = wq == 1 ? S_V : wq == 3 ? S_SAH : S_DY;
         const int y1 = wq == 0 ? S_V : wq == 2 ? S_SAH : S_DY;
         const int y2 = wq == 0 ? S_V : wq == 2 ? S_SAL : S_DY;
-        const bf16_t (*const x2)[64] = wq == 2 ? stg[S_DY] : wq == 3 ? stg[S_SAL] : L.zero;
+        const bf16_t (*const x2)[64] = wq == 2 ? stg[S_DY].r : wq == 3 ? stg[S_SAL].r : L.zero;
         bf16x8 px1[2], py1[2], px2[2], py2[2];
 #pragma unroll
         for (int m = 0; m < 2; ++m) {
-          px1[m] = row_frag(stg[x1], t, m, qd);
-          py1[m] = row_frag(stg[y1], t, m, qd);
+          px1[m] = row_frag(stg[x1].r, t, m, qd);
+          py1[m] = row_frag(stg[y1].r, t, m, qd);
           px2[m] = row_frag(x2, t, m, qd);
-          py2[m] = row_frag(stg[y2], t, m, qd);
+          py2[m] = row_frag(stg[y2].r, t, m, qd);
         }
         const int sgn = (wq & 1) ? -1 : 1;   // keep s >= t (B_), s <= t (C_)
         f32x4 d = {0.f, 0.f, 0.f, 0.f};
@@ -531,10 +540,10 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
       const Split8 q[2] = {{dsa_frag(0, 0), dsa_frag(1, 0)}, {dsa_frag(0, 1), dsa_frag(1, 1)}};
       Split8 g[2];
       {
-        const bf16_t (*const ylo)[64] = wq >= 2 ? stg[S_SAL] : L.zero;
+        const bf16_t (*const ylo)[64] = wq >= 2 ? stg[S_SAL].r : L.zero;
         const int yhi = wq >= 2 ? S_SAH : S_V;
 #pragma unroll
-        for (int m = 0; m < 2; ++m) g[m] = Split8{row_frag(stg[yhi], t, m, qd), row_frag(ylo, t, m, qd)};
+        for (int m = 0; m < 2; ++m) g[m] = Split8{row_frag(stg[yhi].r, t, m, qd), row_frag(ylo, t, m, qd)};
       }
       __builtin_amdgcn_sched_barrier(0);
       const int sgn = (wq & 1) ? -1 : 1;   // keep s > t (B_), s < t (C_)
@@ -572,24 +581,24 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
     Split8 cs0, cs1;               // gradient wave: sa rows; set-up wave: dSA rows
     f32x4 lw4;
     {
-      Rc = Split4{tr_frag(P.rows[T_RH], 0, 16 * kb, lane), tr_frag(P.rows[T_RL], 0, 16 * kb, lane)};
-      Ac = Split4{tr_frag(P.rows[T_AH], 0, 16 * kb, lane), tr_frag(P.rows[T_AL], 0, 16 * kb, lane)};
-      Kc = Split4{tr_frag(P.rows[T_KH], 0, 16 * kb, lane), tr_frag(P.rows[T_KL], 0, 16 * kb, lane)};
-      Bc = Split4{tr_frag(P.rows[T_BH], 0, 16 * kb, lane), tr_frag(P.rows[T_BL], 0, 16 * kb, lane)};
+      Rc = Split4{tr_frag(P.rows[T_RH].r, 0, 16 * kb, lane), tr_frag(P.rows[T_RL].r, 0, 16 * kb, lane)};
+      Ac = Split4{tr_frag(P.rows[T_AH].r, 0, 16 * kb, lane), tr_frag(P.rows[T_AL].r, 0, 16 * kb, lane)};
+      Kc = Split4{tr_frag(P.rows[T_KH].r, 0, 16 * kb, lane), tr_frag(P.rows[T_KL].r, 0, 16 * kb, lane)};
+      Bc = Split4{tr_frag(P.rows[T_BH].r, 0, 16 * kb, lane), tr_frag(P.rows[T_BL].r, 0, 16 * kb, lane)};
 #pragma unroll
       for (int m = 0; m < 2; ++m)
         Db[m] = Split8{tr_frag32(L.xds[0], m, 16 * kb, lane), tr_frag32(L.xds[1], m, 16 * kb, lane)};
       g4 = *reinterpret_cast<const f32x4*>(&P.gT[ki][4 * qd]);
       if (grad) {
-        cv0 = row_frag(stg[S_V], t, 0, qd);
-        cv1 = row_frag(stg[S_V], t, 1, qd);
-        cs0 = row_pair(stg[S_SAH], stg[S_SAL], t, 0, qd);
-        cs1 = row_pair(stg[S_SAH], stg[S_SAL], t, 1, qd);
+        cv0 = row_frag(stg[S_V].r, t, 0, qd);
+        cv1 = row_frag(stg[S_V].r, t, 1, qd);
+        cs0 = row_pair(stg[S_SAH].r, stg[S_SAL].r, t, 0, qd);
+        cs1 = row_pair(stg[S_SAH].r, stg[S_SAL].r, t, 1, qd);
         f_b0 = L.frag[G_BYV][lane];
         f_b1 = L.frag[G_BYSA][lane];
       } else {
-        cv0 = row_frag(stg[S_DY], t, 0, qd);
-        cv1 = row_frag(stg[S_DY], t, 1, qd);
+        cv0 = row_frag(stg[S_DY].r, t, 0, qd);
+        cv1 = row_frag(stg[S_DY].r, t, 1, qd);
         cs0 = Split8{dsa_frag(0, 0), dsa_frag(1, 0)};
         cs1 = Split8{dsa_frag(0, 1), dsa_frag(1, 1)};
         f_b0 = L.frag[G_CDYV][lane];
