@@ -197,6 +197,17 @@ __device__ __forceinline__ bf16x4 read_tr16(const void* lds) {
 // (32 bytes of 8 consecutive rows) hit every bank once (measured: no bank
 // conflicts, where rot(row) = row gives two-way conflicts on the row reads).
 __device__ __forceinline__ int tile_rot(int row) { return row + (row >> 3); }
+// A row tile followed by 64 bytes: consecutive tiles (a value's hi and lo
+// halves, or the rows of different inputs read by the same lanes) start 16
+// banks apart. Unpadded, the two reads of a lane at the same place in two
+// tiles hit one bank, and the compiler also pairs them into one read2/write2
+// instruction, which serialises them (measured: two-way conflicts on every
+// such pair).
+struct PadTile {
+  bf16_t r[kL][64];
+  bf16_t pad[32];
+};
+static_assert(sizeof(PadTile) % 16 == 0, "16-byte aligned tiles");
 __device__ __forceinline__ bf16_t* tile_at(bf16_t (*tile)[64], int row, int c) {
   return &tile[row][8 * (((c >> 3) + tile_rot(row)) & 7) + (c & 7)];
 }

@@ -80,15 +80,6 @@ static_assert(kL * 16 == kSetup, "removal_state rows: four values per set-up thr
 static_assert(O_COUNT * kL * 8 % kSetup == 0, "whole rounds of gradient stores");
 
 // per-chunk set-up, double-buffered (chunk c & 1)
-// a bf16 row tile followed by 64 bytes, so that consecutive tiles (a value's
-// hi and lo halves) start 16 banks apart: a lane's reads of the two halves
-// then hit different banks
-struct PadTile {
-  bf16_t r[kL][64];
-  bf16_t pad[32];
-};
-static_assert(sizeof(PadTile) % 16 == 0, "16-byte aligned tiles");
-
 struct Prep {
   PadTile rows[T_COUNT];            // decayed rows, rotated
   float gT[64][kL + 4];             // log2 prefix decay, [key][step]

@@ -88,12 +88,12 @@ struct FwdChunkParams {
 // rows; after they are read, the chunk's x, r, k, a, b rows and the wave's
 // scratch `scr` are reused for the hi/lo rows of A^, K~ and B~, from which the
 // transposed fragments are read.
-__device__ __forceinline__ void prepare_chunk(bf16_t (*stg)[kL][64], float (*scr)[kL][kL],
+__device__ __forceinline__ void prepare_chunk(PadTile* stg, float (*scr)[kL][kL],
                                               ChunkOps& o, int lane) {
   const int t = lane & 15, qd = lane >> 4;
   // the lane's step row t, keys 32 m + 16 hh + 4 qd + c (c < 4), as raw bf16
   auto raw = [&](int vec, int m, int hh) -> uint2 {
-    return *reinterpret_cast<const uint2*>(tile_at(stg[vec], t, 32 * m + 16 * hh + 4 * qd));
+    return *reinterpret_cast<const uint2*>(tile_at(stg[vec].r, t, 32 * m + 16 * hh + 4 * qd));
   };
   auto widen = [](uint2 u) -> f32x4 {
     return f32x4{__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
@@ -161,7 +161,7 @@ __device__ __forceinline__ void prepare_chunk(bf16_t (*stg)[kL][64], float (*scr
 
   // hi/lo rows of A^, K~, B~ into LDS (the chunk's raw rows are consumed),
   // then their transposed fragments (row = key, k = step) by transposed loads
-  bf16_t (*rows[6])[64] = {stg[S_X], stg[S_R], stg[S_K], stg[S_A], stg[S_B],
+  bf16_t (*rows[6])[64] = {stg[S_X].r, stg[S_R].r, stg[S_K].r, stg[S_A].r, stg[S_B].r,
                            reinterpret_cast<bf16_t (*)[64]>(&scr[0][0][0])};
 #pragma unroll
   for (int m = 0; m < 2; ++m)
@@ -207,7 +207,7 @@ __device__ __forceinline__ void prepare_chunk(bf16_t (*stg)[kL][64], float (*scr
   const bf16x8 Ps = stack(P);
 #pragma unroll
   for (int vb = 0; vb < 4; ++vb) {
-    const bf16x4 vt = tr(stg[S_V], vb);
+    const bf16x4 vt = tr(stg[S_V].r, vb);
     o.v[vb][lane] = vt;
     const f32x4 X = mma_s2(ak, vt, f32x4{0.f, 0.f, 0.f, 0.f});
     o.u[vb][lane] = mma_s3(Ps, split4(X), f32x4{0.f, 0.f, 0.f, 0.f});
@@ -254,7 +254,7 @@ __device__ __forceinline__ ChainOps load_chain_ops(const ChunkOps& o, int jb, in
 // the hi/lo rows of A^, K~, B~; 16-byte pieces of a row rotated by the step
 // index so that row and transposed reads spread over the banks
 struct PrepLds {
-  bf16_t stg[kVecs][kL][64];
+  PadTile stg[kVecs];
   float scr[2][kL][kL];
 };
 
@@ -348,9 +348,10 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_fwd_chunk_kernel(const FwdChun
       uint4 r0, r1, r2, r3, r4, r5, r6, r7, r8, r9, r10, r11;
       RWKV_RAW_LOAD(s)
       for (int c = s; c < nchunks; c += kSlots) {
-        uint4* const dst = reinterpret_cast<uint4*>(&my.stg[0][0][0]) + lane;
-        dst[0] = r0; dst[64] = r1; dst[128] = r2; dst[192] = r3; dst[256] = r4; dst[320] = r5;
-        dst[384] = r6; dst[448] = r7; dst[512] = r8; dst[576] = r9; dst[640] = r10; dst[704] = r11;
+        // piece k: rows 8 (k % 2) .. of input k / 2
+        auto dst = [&](int k) { return reinterpret_cast<uint4*>(&my.stg[k >> 1].r[8 * (k & 1)][0]) + lane; };
+        *dst(0) = r0; *dst(1) = r1; *dst(2) = r2; *dst(3) = r3; *dst(4) = r4; *dst(5) = r5;
+        *dst(6) = r6; *dst(7) = r7; *dst(8) = r8; *dst(9) = r9; *dst(10) = r10; *dst(11) = r11;
         // the last chunk reloads itself (harmless) so that the loads need no branch
         const int cn = c + kSlots < nchunks ? c + kSlots : c;
         RWKV_RAW_LOAD(cn)
