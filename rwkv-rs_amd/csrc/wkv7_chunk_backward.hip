@@ -89,7 +89,7 @@ struct Prep {
 };
 
 struct BwdLds {
-  bf16_t dec[kDecayIn][kL][64];     // x, r, k, a, b rows of the next chunk to set up
+  PadTile dec[kDecayIn];            // x, r, k, a, b rows of the next chunk to set up
   PadTile stg[2][S_COUNT];          // v, dy, sa hi, sa lo rows, double-buffered
   Prep prep[2];                     // chunk 0 also keeps its rebuilt start state in prep[1]
   bf16x8 frag[G_COUNT][64];         // step products with v, dy, sa, dsa (stacked)
@@ -158,10 +158,10 @@ __device__ __forceinline__ uint32_t read2(const bf16_t (*tile)[64], int row, int
 __device__ __forceinline__ void write2(bf16_t (*tile)[64], int row, int c, uint32_t v) {
   *reinterpret_cast<uint32_t*>(tile_at(tile, row, c)) = v;
 }
-__device__ __forceinline__ DecayIn decay_load(const bf16_t (*dec)[kL][64], int wave, int t, int qd) {
+__device__ __forceinline__ DecayIn decay_load(const PadTile* dec, int wave, int t, int qd) {
   const int c0 = 8 * wave + 2 * qd;
-  return DecayIn{read2(dec[I_X], t, c0), read2(dec[I_A], t, c0), read2(dec[I_R], t, c0),
-                 read2(dec[I_K], t, c0), read2(dec[I_B], t, c0)};
+  return DecayIn{read2(dec[I_X].r, t, c0), read2(dec[I_A].r, t, c0), read2(dec[I_R].r, t, c0),
+                 read2(dec[I_K].r, t, c0), read2(dec[I_B].r, t, c0)};
 }
 __device__ __forceinline__ float bf_lo(uint32_t u) { return __uint_as_float(u << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
@@ -285,7 +285,10 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
   auto stage_dec = [&](const Pre& pr) {
 #pragma unroll
     for (int k = 0; k < kDecayRounds; ++k)
-      if (2 * k + (wq >> 1) < kDecayIn) reinterpret_cast<uint4*>(&L.dec[0][0][0])[kSetup * k + utid] = pr.dec[k];
+      if (2 * k + (wq >> 1) < kDecayIn) {
+        const int piece = kSetup * k + utid;   // 128 pieces per input
+        reinterpret_cast<uint4*>(&L.dec[piece >> 7].r[0][0])[piece & 127] = pr.dec[k];
+      }
   };
   auto stage_grad = [&](const Pre& pr, int sb) {
     reinterpret_cast<uint4*>(&L.stg[sb][utid >> 7].r[0][0])[utid & 127] = pr.vy;   // v rows, then dy rows
@@ -408,8 +411,8 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
           const float sj = p.sa[tok0 + (int64_t)tt * tstride + jcol];
 #pragma unroll
           for (int ib = 0; ib < 4; ++ib) {
-            const f32x4 kv = widen4(read4(L.dec[I_K], tt, 16 * ib + 4 * qd));
-            const f32x4 bv = widen4(read4(L.dec[I_B], tt, 16 * ib + 4 * qd));
+            const f32x4 kv = widen4(read4(L.dec[I_K].r, tt, 16 * ib + 4 * qd));
+            const f32x4 bv = widen4(read4(L.dec[I_B].r, tt, 16 * ib + 4 * qd));
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const float winv = exp2_f(-P.lwT[16 * ib + 4 * qd + r][tt]);
