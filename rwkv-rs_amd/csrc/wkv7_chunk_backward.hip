@@ -24,7 +24,10 @@
 // dw_u = W_SCALE sigmoid(x_u)(1 - sigmoid(x_u)) sum_{t>=u} dL/dg_t.
 // Chunk 0's start state is rebuilt the way the reference rebuilds every step
 // (divide by the decay, kernel.rs:239-246); the other chunks read it from the
-// previous checkpoint.
+// previous checkpoint. With chunk_len > 16 only every (chunk_len / 16)-th
+// chunk starts at a checkpoint; the set-up waves rebuild the others' start
+// states by the same reversal, from the end state the next chunk started
+// with, carried in registers.
 //
 // Work layout: one workgroup of eight waves per (batch, head), two per SIMD,
 // chunks in reverse order. Waves 0-3 ("gradient waves", wave w owns value
@@ -98,6 +101,10 @@ struct BwdLds {
   f32x4 kx[4][64];                  // the gradient waves' part of the decay gradient, per key tile
   bf16_t outs[2][O_COUNT][kL][64];  // a chunk's bf16 gradients, written out as whole rows (out_at), double-buffered
   bf16_t zero[kL][64];              // an all-zero row tile
+  // chunk_len > 16: the chunk whose start state is rebuilt next (staged with
+  // its gradient rows): the removal_state in fp32, and the k and b rows
+  float sa32[kL][64];
+  PadTile kbt[2];
 };
 typedef float S0Rows[64][68];       // chunk 0's rebuilt start state, [key i][value j]
 static_assert(sizeof(S0Rows) <= sizeof(Prep), "start state fits the free set-up buffer");
@@ -115,6 +122,7 @@ struct BwdChunkParams {
   bf16_t* db;
   float* ds0;                  // [B,H,64,64] or null
   int T, H;
+  int C;                       // chunk_len: a multiple of 16
 };
 
 // element (row, key) of a staged gradient tile: 16-byte pieces rotated by
@@ -240,6 +248,10 @@ __device__ __forceinline__ void setup_products(Prep& P, const GramIn& g, int wav
   }
 }
 
+// kLong: chunk_len > 16. Only every (chunk_len / 16)-th start state is a
+// checkpoint; the others are rebuilt by the reference's reversal (see
+// reverse_chunk), on the set-up waves.
+template <bool kLong>
 __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChunkParams p) {
   __shared__ BwdLds L;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -253,14 +265,15 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
   const int64_t tstride = (int64_t)H * kHead;
   const int64_t tok0 = ((int64_t)b * T * H + h) * kHead;
   const int nchunks = T / kL;
-  const float* const ckbh = p.ckpt + bh * nchunks * (kHead * kHead);
+  const int q = kLong ? p.C / kL : 1;   // 16-step chunks per checkpoint
+  const float* const ckbh = p.ckpt + bh * (T / (kL * q)) * (kHead * kHead);
 
   // ---- staging through registers (set-up waves). bf16 rows as rotated
   // pieces: piece p = 256 k + utid is row (p / 8) % 16, slot p % 8 of input
   // p / 128, whose index is wave-uniform, so its pointer stays in scalar
   // registers. The removal_state: thread utid holds row utid / 16, values
   // 4 (utid % 16) .. + 3.
-  struct Pre { uint4 dec[kDecayRounds]; uint4 vy; f32x4 sa; };
+  struct Pre { uint4 dec[kDecayRounds]; uint4 vy; f32x4 sa; uint4 kb; };
   // the sources, chosen once (waves 6 and 7 have no piece in the last decay
   // round: they load input 4's again and do not stage it)
   const bf16_t* src[kDecayRounds + 1];
@@ -270,6 +283,7 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
     src[k] = p.in[in < kDecayIn ? in : kDecayIn - 1] + tok0;
   }
   src[kDecayRounds] = p.in[I_V + (wq >> 1)] + tok0;
+  const bf16_t* const kb_src = p.in[(wq >> 1) ? I_B : I_K] + tok0;   // k rows, then b rows
   const float* const sa_src = p.sa + tok0 + (int64_t)(utid >> 4) * tstride + 4 * (utid & 15);
   // piece offset within a chunk: row (utid / 8) % 16, rotated slot
   const int64_t piece_off = (int64_t)((utid >> 3) & 15) * tstride + 8 * (((utid & 7) - tile_rot((utid >> 3) & 15)) & 7);
@@ -280,6 +294,7 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
     for (int k = 0; k < kDecayRounds; ++k) pr.dec[k] = *reinterpret_cast<const uint4*>(src[k] + od);
     pr.vy = *reinterpret_cast<const uint4*>(src[kDecayRounds] + (int64_t)kL * cg * tstride + piece_off);
     pr.sa = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(sa_src + (int64_t)kL * cg * tstride));
+    if constexpr (kLong) pr.kb = *reinterpret_cast<const uint4*>(kb_src + (int64_t)kL * cg * tstride + piece_off);
     return pr;
   };
   auto stage_dec = [&](const Pre& pr) {
@@ -295,6 +310,12 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
     const Split4 s = split4(pr.sa);
     write4(L.stg[sb][S_SAH].r, utid >> 4, 4 * (utid & 15), s.hi);
     write4(L.stg[sb][S_SAL].r, utid >> 4, 4 * (utid & 15), s.lo);
+    if constexpr (kLong) {
+      // single-buffered: read in phase A of the chunk, written in phase B of
+      // the one after it
+      reinterpret_cast<uint4*>(&L.kbt[utid >> 7].r[0][0])[utid & 127] = pr.kb;
+      *reinterpret_cast<f32x4*>(&L.sa32[utid >> 4][4 * (utid & 15)]) = pr.sa;
+    }
   };
 
   // ---- state gradient (gradient waves): value tile jb = wq, key tiles ib,
@@ -313,14 +334,51 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
   // start state S0 of chunk c >= 1 (the checkpoint of chunk c - 1) as the
   // rows [key ki][value 32 m + 4 qd .., + 16 ..] of the key stage; loaded at
   // the start of the chunk, used two phases later
-  auto load_s0 = [&](int c, f32x4 (&rowv)[2][2]) {
-    const float* ck = ckbh + (int64_t)(c - 1) * (kHead * kHead);
+  auto load_ckpt = [&](int n, f32x4 (&rowv)[2][2]) {   // checkpoint n
+    const float* ck = ckbh + (int64_t)n * (kHead * kHead);
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
       rowv[m][0] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(ck + ki * kHead + 32 * m + 4 * qd));
       rowv[m][1] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(ck + ki * kHead + 32 * m + 16 + 4 * qd));
     }
   };
+  // start state of chunk c, c a multiple of q
+  auto load_s0 = [&](int c, f32x4 (&rowv)[2][2]) { load_ckpt(c / q - 1, rowv); };
+  // kLong: the start state of chunk c from its end state Se by the
+  // reference's reversal over the chunk's 16 steps (kernel.rs:239-246),
+  // S_{t-1} = (S_t - k_t v_t^T - b_t sa_t^T) / w~_t, in the key stage's
+  // layout (the lane's key ki, values 32 m + 16 h + 4 qd + e): one decay per
+  // lane and step. Every operand from LDS: v from the staged gradient rows,
+  // k, b and the fp32 removal_state from their own staging, log2 w~ from the
+  // set-up of chunk c.
+  auto reverse_chunk = [&](int c, const Prep& P, const PadTile* stg, const f32x4 (&Se)[2][2],
+                           f32x4 (&S)[2][2]) {
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      S[m][0] = Se[m][0];
+      S[m][1] = Se[m][1];
+    }
+#pragma unroll 4
+    for (int tt = kL - 1; tt >= 0; --tt) {
+      const float kv = __uint_as_float((uint32_t)*tile_at(L.kbt[0].r, tt, ki) << 16);
+      const float bv = __uint_as_float((uint32_t)*tile_at(L.kbt[1].r, tt, ki) << 16);
+      const float winv = exp2_f(-P.lwT[ki][tt]);
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const int j0 = 32 * m + 16 * hh + 4 * qd;
+          const f32x4 vv = widen4(read4(stg[S_V].r, tt, j0));
+          const f32x4 sv = *reinterpret_cast<const f32x4*>(&L.sa32[tt][j0]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) S[m][hh][e] = (S[m][hh][e] - kv * vv[e] - bv * sv[e]) * winv;
+        }
+    }
+  };
+  // kLong, set-up waves: the start state of the chunk processed last, i.e.
+  // the end state of the next one (the last checkpoint before the loop)
+  f32x4 Snext[2][2];
+  if (kLong && !grad) load_ckpt(T / (kL * q) - 1, Snext);
 
   // the staged gradient tiles of chunk cc to memory (gradient waves in the
   // loop, whose phase B is the shorter one; set-up waves after it): thread
@@ -396,7 +454,7 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
     f32x4 S0row[2][2];
     f32x4 dv;
     if (grad) {
-      if constexpr (!kFull) {
+      if constexpr (!kFull && !kLong) {
         // rebuild S0 by reversing the chunk's 16 steps from its checkpoint
         // (kernel.rs:239-246): S_{t-1} = (S_t - v_t k_t^T - sa_t b_t^T) / w~_t.
         // The decay-rows buffer still holds chunk 0's rows; sa in fp32 from memory.
@@ -479,7 +537,16 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
         // at c == 1 the decay rows of chunk 0 are fetched again (harmless, and
         // the reversal of chunk 0 reads them)
         pre = fetch(c >= 2 ? c - 2 : 0, c - 1);
-        load_s0(c, S0row);
+        if constexpr (!kLong) load_s0(c, S0row);
+      }
+      if constexpr (kLong) {
+        if (kFull && c % q == 0) load_s0(c, S0row);
+        else reverse_chunk(c, P, stg, Snext, S0row);
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+          Snext[m][0] = S0row[m][0];
+          Snext[m][1] = S0row[m][1];
+        }
       }
       // step products of v, dy, sa of chunk c (one per wave), which do not
       // depend on the state gradient, as D = X1 Y1^T + X2 Y2^T:
@@ -642,7 +709,7 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
         f32x4 S0v[2][2];
 #pragma unroll
         for (int m = 0; m < 2; ++m) {
-          if constexpr (kFull) {
+          if constexpr (kFull || kLong) {
             S0v[m][0] = S0row[m][0];
             S0v[m][1] = S0row[m][1];
           } else {
@@ -729,7 +796,7 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
 }  // namespace
 
 bool chunk_backward_supported(const BackwardDesc& d) {
-  return d.dtype == Dtype::BF16 && d.C == kL && d.T % kL == 0 && d.T > 0;
+  return d.dtype == Dtype::BF16 && d.C >= kL && d.C % kL == 0 && d.T % d.C == 0 && d.T > 0;
 }
 
 hipError_t launch_backward_chunked(const BackwardDesc& d, hipStream_t stream) {
@@ -753,8 +820,12 @@ hipError_t launch_backward_chunked(const BackwardDesc& d, hipStream_t stream) {
   p.ds0 = d.ds0;
   p.T = d.T;
   p.H = d.H;
+  p.C = d.C;
   const dim3 grid(d.H, d.B, 1), block(kBlock, 1, 1);
-  hipLaunchKernelGGL(wkv7_bwd_chunk_kernel, grid, block, 0, stream, p);
+  if (d.C == kL)
+    hipLaunchKernelGGL(wkv7_bwd_chunk_kernel<false>, grid, block, 0, stream, p);
+  else
+    hipLaunchKernelGGL(wkv7_bwd_chunk_kernel<true>, grid, block, 0, stream, p);
   return hipGetLastError();
 }
 

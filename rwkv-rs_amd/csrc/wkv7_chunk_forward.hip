@@ -395,8 +395,8 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_fwd_chunk_kernel(const FwdChun
 
     for (int cidx = 0; cidx < nchunks; ++cidx) {
       const int slot = cidx % kSlots;
-      for (int n = 0; n < kSpinLimit && lds_load_flag(&flags.ready[slot]) < cidx; ++n)
-        __builtin_amdgcn_s_sleep(1);
+      if (!wait_flag(&flags.ready[slot], cidx, p.spin_limit) && lane == 0)
+        lds_store_flag(&flags.fault, 1);
       lds_acquire();
       const ChainOps cur = load_chain_ops(ops[slot], jb, lane);
 
@@ -470,12 +470,14 @@ __global__ void take_faults_kernel() {
 }  // namespace
 
 // bf16 operands and chunk_len 16. The checkpoints feed the reference-order
-// backward, which rebuilds each step's state by dividing by the decay and so
-// amplifies a checkpoint's deviation by about 1.35x per step: from a 16-step
-// checkpoint the ~3e-6 relative deviation of the split-bf16 products stays far
-// inside the bf16 tolerance, from a 32-step one it does not (the reference
-// algorithm itself loses ~5e-4 there), so longer chunk lengths keep the
-// step-by-step fp32 forward.
+// backward, which rebuilds states between checkpoints by dividing by the
+// decay and so amplifies a checkpoint's deviation by about 1.35x per step.
+// The split-bf16 products leave the checkpoints ~2.5e-6 from the fp32
+// algorithm's (~6e-8): harmless at chunk_len 16, where no state is rebuilt
+// except chunk 0's, but measured at chunk_len 32 / 48 / 64 the rebuilt-state
+// gradients (dw, dr, da) end up 4x / 30x / 30x further from exact than the
+// reference algorithm's own. Longer chunk lengths therefore keep the
+// step-by-step fp32 forward (the chunked backward takes them).
 bool chunk_forward_supported(const ForwardDesc& d) {
   return d.dtype == Dtype::BF16 && d.C == kL && d.T % kL == 0;
 }

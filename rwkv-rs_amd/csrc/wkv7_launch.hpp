@@ -71,8 +71,8 @@ hipError_t launch_forward_chunked(const ForwardDesc& d, hipStream_t stream);
 hipError_t take_handover_faults(hipStream_t stream, uint32_t* count);
 
 // Chunked matrix-core backward (wkv7_chunk_backward.hip): bf16 operands,
-// chunk_len 16, T a positive multiple of 16; picked by launch_backward under
-// the same choice.
+// chunk_len a multiple of 16, T a positive multiple of chunk_len; picked by
+// launch_backward under the same choice.
 bool chunk_backward_supported(const BackwardDesc& d);
 hipError_t launch_backward_chunked(const BackwardDesc& d, hipStream_t stream);
 hipError_t launch_backward(const BackwardDesc& d, hipStream_t stream);

@@ -168,6 +168,69 @@ def test_bf16_inputs_fp32_state(wk, oracle, case):
     compare(fwd, bwd, ofwd, obwd, BF16_TOL, f"bf16 {case}", BF16_STATE_TOL)
 
 
+@pytest.mark.parametrize("case", [
+    (2, 128, 4, 32, 0.1, 21),   # two 16-step chunks per checkpoint
+    (1, 96, 3, 48, None, 22),   # three
+    (1, 192, 2, 64, 0.1, 23),   # four: start states rebuilt over up to 48 steps
+])
+def test_bf16_long_chunks_on_the_chunked_kernels(wk, oracle, case):
+    # chunk_len > 16 with bf16 operands: the step forward (fp32 checkpoints
+    # every chunk_len steps) and the chunked backward, which rebuilds the start
+    # states of the 16-step chunks between checkpoints by the reference's
+    # reversal (kernel.rs:239-246). The forward and the gradients that do not
+    # read a rebuilt state are held to the bf16 bars against the oracle; dw, dr
+    # and da, which do, to the reference algorithm's own accuracy (the oracle
+    # in fp32 against exact fp64 gradients, which is what grows with
+    # chunk_len) plus bf16 rounding.
+    B, T, H, C, s0_std, seed = case
+    announce("bf16 long chunk", case)
+    pkg = load_pkg()
+    d = pkg.synthetic.make_inputs(B, T, H, 64, seed=seed, s0_std=s0_std, bf16=True)
+    if d["s0"] is None:
+        d["s0"] = np.zeros((B, H, 64, 64), np.float32)
+    fwd, bwd = run_gpu(wk, d, C, torch.bfloat16)
+    ofwd, obwd = run_oracle(oracle, d, C)
+    exact = oracle.grad_f64(*(d[n] for n in NAMES), d["s0"], d["dy"])
+    assert rel_l2(to_np(fwd.output), pkg.synthetic.bf16_round(ofwd["output"])) <= BF16_TOL
+    for key in ("removal_state", "state", "final_state"):
+        assert rel_l2(to_np(getattr(fwd, key)), ofwd[key]) <= BF16_STATE_TOL, key
+    assert fwd.state.shape[2] == T // C
+    rebuilt = ("weight_decay_grad", "receptance_grad", "removal_grad")
+    for gn in GRAD_NAMES + ("initial_state_grad",):
+        got = to_np(getattr(bwd, gn))
+        if gn in rebuilt:
+            ref_err = rel_l2(obwd[gn], exact[gn])
+            err = rel_l2(got, exact[gn])
+            print(case, gn, f"gpu {err:.2e} reference-algorithm {ref_err:.2e}", flush=True)
+            assert err <= 5 * ref_err + BF16_TOL, (gn, err, ref_err)
+        elif gn == "initial_state_grad":
+            assert rel_l2(got, obwd[gn]) <= BF16_STATE_TOL, gn
+        else:
+            assert rel_l2(got, pkg.synthetic.bf16_round(obwd[gn])) <= BF16_TOL, gn
+
+
+def test_long_chunk_bf16_backward_matches_step_backward(wk):
+    # chunk_len 32 with bf16 operands: the forward runs the step kernels (their
+    # fp32 checkpoints are what the rebuild between checkpoints needs) and the
+    # backward the chunked kernels; on the same checkpoints the step backward
+    # gives the same gradients to bf16 rounding
+    announce("bf16 chunk_len 32 chunked vs step backward", (1, 64, 2, 32))
+    pkg = load_pkg()
+    d = pkg.synthetic.make_inputs(1, 64, 2, 64, seed=24, s0_std=0.1, bf16=True)
+    dev = torch.device("cuda:0")
+    ins = [torch.from_numpy(d[n]).to(dev).to(torch.bfloat16) for n in NAMES]
+    s0 = torch.from_numpy(d["s0"]).to(dev)
+    dy = torch.from_numpy(d["dy"]).to(dev).to(torch.bfloat16)
+    f = wk.wkv7_forward_ex(*ins, s0, 32)
+    a = wk.wkv7_backward_ex(*ins, f.state, f.removal_state, dy, torch.zeros_like(s0), 32)
+    b = wk.wkv7_backward_ex(*ins, f.state, f.removal_state, dy, torch.zeros_like(s0), 32,
+                            kernels="step")
+    torch.cuda.synchronize()
+    for gn in GRAD_NAMES:
+        assert rel_l2(to_np(getattr(a, gn)), to_np(getattr(b, gn))) <= BF16_TOL, gn
+    assert rel_l2(to_np(a.initial_state_grad), to_np(b.initial_state_grad)) <= BF16_STATE_TOL
+
+
 def test_variants_agree(wk):
     # pretrain == statepass(s0 = 0) == statetune(s0 = 0) on y and the six gradients
     announce("variant equivalence")
