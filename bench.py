@@ -544,7 +544,8 @@ def bench_decode(cfg, steps, warmup, probe=False, state_dtype="f32"):
                      "kernel": "wkv7_infer_bf16_kernel" if bf16_state else "wkv7_infer_kernel",
                      "achieved": nbytes / (launch_ms * 1e-3) / 1e9, "peak": PEAK_HBM / 1e9,
                      "unit": "GB/s", "frac": nbytes / (launch_ms * 1e-3) / PEAK_HBM,
-                     "traffic": None if bf16_state else recorded_traffic("wkv7_infer_kernel", TRAFFIC_FILE_DECODE),
+                     "traffic": recorded_traffic("wkv7_infer_bf16_kernel" if bf16_state else "wkv7_infer_kernel",
+                                                 TRAFFIC_FILE_DECODE),
                      "algorithmic_bytes": nbytes, "launch_ms": launch_ms},
     }
 

@@ -174,13 +174,18 @@ __global__ __launch_bounds__(kThreads) void wkv7_infer_kernel(InferParams<Tin> p
 // ------------------------------------------------------------ bf16 state
 // One wave per (active row, head); lane j owns value row j of the state, so
 // each row's sums over the key index run left to right inside one lane, as
-// the reference's thread j does (kernel.rs:81-96). The row is held as 64
-// fp32 registers carrying bf16 values. The step's key-indexed operands (the
-// rounded decay, a, b, k, r) go through LDS as fp32 and are read back as
-// broadcasts; lane j keeps its own v_j. The 8 KiB state moves between HBM and
-// the lanes' rows through LDS, with coalesced 16-byte accesses on the HBM
-// side and each row's 16-byte pieces rotated by row + row / 8 so that neither
-// the row-per-lane reads nor the contiguous writes conflict on LDS banks.
+// the reference's thread j does (kernel.rs:81-96). The row is held as 32
+// registers of bf16 pairs, as stored, and widened where an operation reads a
+// value. The step's key-indexed operands (the rounded decay, a, b, k, r) go
+// through LDS as fp32 and are read back as broadcasts; lane j keeps its own
+// v_j. The step is bound by its instruction count (64 x 64 elements of one
+// (row, head) on one wave, a rounding after every operation): each "round
+// two values, add them" is one packed conversion and one bf16 dot product
+// (add_rb), and the two new state values of a key pair are rounded by one
+// packed conversion. The 8 KiB state moves between HBM and the lanes' rows
+// through LDS, with coalesced 16-byte accesses on the HBM side and each row's
+// 16-byte pieces rotated by row + row / 8 so that neither the row-per-lane
+// reads nor the contiguous writes conflict on LDS banks.
 struct InferBf16Params {
   const bf16_t *w, *r, *k, *v, *a, *b;
   const int32_t* batch_ids;
@@ -196,6 +201,26 @@ struct InferBf16Params {
 // to fp32 and then to bf16 equals the sum rounded once (fp32 carries more
 // than twice bf16's significand bits plus two).
 __device__ __forceinline__ float rb(float x) { return (float)(__bf16)x; }
+
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+// rb(x) + rb(p) as an fp32 sum: both roundings in one packed conversion, the
+// sum of the two bf16 halves by a bf16 dot product with (1, 1). The two
+// halves are bf16 values, so the dot product's fp32 result is their sum
+// rounded once to fp32, as an fp32 addition of the two would give it, and
+// the bf16 rounding that follows (rb, or the next add_rb) sees the same
+// value. Three instructions where rounding both operands and adding takes
+// five (the conversion, the zeroed accumulator and the dot product against
+// two conversions, two widenings and the addition). The dot product flushes
+// fp32 results below 2^-126 (about 1.2e-38) to zero, where the addition
+// would keep them: the two differ only for sums of that size.
+__device__ __forceinline__ float add_rb(float x, float p) {
+  const bf16x2_t h = __builtin_convertvector(f32x2_t{x, p}, bf16x2_t);
+  return __builtin_amdgcn_fdot2_f32_bf16(h, bf16x2_t{(__bf16)1.0f, (__bf16)1.0f}, 0.0f, false);
+}
+
+__device__ __forceinline__ float bf_lo(uint32_t u) { return __uint_as_float(u << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
 
 __device__ __forceinline__ int rot_piece(int row, int q) { return row * 8 + ((q + row + (row >> 3)) & 7); }
 
@@ -222,16 +247,16 @@ __global__ __launch_bounds__(64) void wkv7_infer_bf16_kernel(InferBf16Params p) 
     srow[rot_piece(u >> 3, u & 7)] = st[u];
   }
   __syncthreads();
-  float s[kHead];
+  // the row as it is stored: keys 2 m and 2 m + 1 in the low and high half of
+  // sp[m], widened to fp32 where an operation reads them
+  uint32_t sp[kHead / 2];
 #pragma unroll
   for (int q = 0; q < 8; ++q) {
     const uint4 x = srow[rot_piece(lane, q)];
-    const uint32_t wds[4] = {x.x, x.y, x.z, x.w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      s[8 * q + 2 * e] = __uint_as_float(wds[e] << 16);
-      s[8 * q + 2 * e + 1] = __uint_as_float(wds[e] & 0xffff0000u);
-    }
+    sp[4 * q + 0] = x.x;
+    sp[4 * q + 1] = x.y;
+    sp[4 * q + 2] = x.z;
+    sp[4 * q + 3] = x.w;
   }
 
   const uint32_t elapsed = p.elapsed_t ? (uint32_t)p.elapsed_t[slot] : 0u;
@@ -267,28 +292,38 @@ __global__ __launch_bounds__(64) void wkv7_infer_bf16_kernel(InferBf16Params p) 
     opf[O_R * kHead + lane] = bf16_to_f32(cr);
     const float vj = bf16_to_f32(cv);
     __syncthreads();
-    float sa = 0.0f;
+    // Running sums are kept unrounded (z): the reference's bf16 sum after key
+    // i is rb(z_i), and z_{i+1} = rb(z_i) + rb(product_{i+1}) in fp32, so
+    // sa_{i+1} = rb(sa_i + rb(a_{i+1} S[j, i+1])) as kernel.rs:81-83 has it.
+    float z = 0.0f;
 #pragma unroll
     for (int i4 = 0; i4 < kHead / 4; ++i4) {
       const float4 a4 = ops[O_A][i4];
-      sa = rb(sa + rb(a4.x * s[4 * i4 + 0]));
-      sa = rb(sa + rb(a4.y * s[4 * i4 + 1]));
-      sa = rb(sa + rb(a4.z * s[4 * i4 + 2]));
-      sa = rb(sa + rb(a4.w * s[4 * i4 + 3]));
+      z = add_rb(z, a4.x * bf_lo(sp[2 * i4]));
+      z = add_rb(z, a4.y * bf_hi(sp[2 * i4]));
+      z = add_rb(z, a4.z * bf_lo(sp[2 * i4 + 1]));
+      z = add_rb(z, a4.w * bf_hi(sp[2 * i4 + 1]));
     }
-    float y = 0.0f;
+    const float sa = rb(z);
+    float zy = 0.0f;
 #pragma unroll
     for (int i4 = 0; i4 < kHead / 4; ++i4) {
       const float4 w4 = ops[O_W][i4], b4 = ops[O_B][i4], k4 = ops[O_K][i4], r4 = ops[O_R][i4];
       const float wv[4] = {w4.x, w4.y, w4.z, w4.w}, bv[4] = {b4.x, b4.y, b4.z, b4.w};
       const float kv[4] = {k4.x, k4.y, k4.z, k4.w}, rv[4] = {r4.x, r4.y, r4.z, r4.w};
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float& si = s[4 * i4 + e];
-        si = rb(rb(rb(si * wv[e]) + rb(sa * bv[e])) + rb(kv[e] * vj));
-        y = rb(y + rb(si * rv[e]));
+      for (int e = 0; e < 4; e += 2) {
+        // S[j,i] = rb(rb(rb(S w) + rb(sa b)) + rb(k v)) for keys i, i + 1,
+        // the two new values rounded by one packed conversion
+        uint32_t& pair = sp[2 * i4 + e / 2];
+        const float u0 = add_rb(add_rb(bf_lo(pair) * wv[e], sa * bv[e]), kv[e] * vj);
+        const float u1 = add_rb(add_rb(bf_hi(pair) * wv[e + 1], sa * bv[e + 1]), kv[e + 1] * vj);
+        pair = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{u0, u1}, bf16x2_t));
+        zy = add_rb(zy, bf_lo(pair) * rv[e]);
+        zy = add_rb(zy, bf_hi(pair) * rv[e + 1]);
       }
     }
+    const float y = rb(zy);
     p.y[off] = (bf16_t)(__float_as_uint(y) >> 16);
     ++valid_t;
   }
@@ -296,15 +331,7 @@ __global__ __launch_bounds__(64) void wkv7_infer_bf16_kernel(InferBf16Params p) 
   // write the rows back through LDS: coalesced 16-byte stores
   __syncthreads();
 #pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    uint4 x;
-    uint32_t* wds = reinterpret_cast<uint32_t*>(&x);
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      wds[e] = (__float_as_uint(s[8 * q + 2 * e]) >> 16) |
-               (__float_as_uint(s[8 * q + 2 * e + 1]) & 0xffff0000u);
-    srow[rot_piece(lane, q)] = x;
-  }
+  for (int q = 0; q < 8; ++q) srow[rot_piece(lane, q)] = make_uint4(sp[4 * q], sp[4 * q + 1], sp[4 * q + 2], sp[4 * q + 3]);
   __syncthreads();
 #pragma unroll
   for (int m = 0; m < 8; ++m) {
