@@ -448,6 +448,12 @@ def bench_train(cfg, steps, warmup, with_cpu, probe=False, kernels="auto"):
         units["mfma_bf16_frac"] = mops / (bwd_ms * 1e-3) / PEAK_BF16
     if valu:
         units["valu_issue_frac"] = valu * 4 / (bwd_ms * 1e-3 * CLOCK_HZ * N_SIMDS)
+    if mops and valu:
+        # a SIMD does not overlap VALU and MFMA instructions (measured on the
+        # box: a wave of independent FMAs and a wave of independent MFMAs on
+        # one SIMD take the sum of their times alone), so the share of the
+        # SIMDs' time spent issuing the two is the sum of the two fractions
+        units["simd_busy_frac"] = units["valu_issue_frac"] + units["mfma_bf16_frac"]
     out = {
         "metric": METRIC,
         "value": tok / (ms_per_step * 1e-3) / 1e6,
