@@ -64,10 +64,6 @@ struct Split4 { bf16x4 hi, lo; };
 __device__ __forceinline__ f32x4 mma32(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
-__device__ __forceinline__ f32x4 mma16(bf16x4 a, bf16x4 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
-      __builtin_bit_cast(i16x4, a), __builtin_bit_cast(i16x4, b), c, 0, 0, 0);
-}
 
 // hi*hi + hi*lo + lo*hi, small terms first
 __device__ __forceinline__ f32x4 mma32x3(const Split8& a, const Split8& b, f32x4 c) {
@@ -164,19 +160,6 @@ __device__ __forceinline__ f32x4 unit_lower_inverse(f32x4 a, f32x4 at, int t, in
   return mma_tiles(split4(qt), split4(r), z);
 }
 
-// B operand of the 16x16 identity: multiplying an A fragment by it returns
-// the same 16x16 tile in the result layout, i.e. with rows and lanes swapped.
-// Exact for bf16 inputs.
-__device__ __forceinline__ bf16x4 identity_b(int lane) {
-  bf16x4 o;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) o[e] = (__bf16)((4 * (lane >> 4) + e) == (lane & 15) ? 1.0f : 0.0f);
-  return o;
-}
-__device__ __forceinline__ bf16x4 transpose16(bf16x4 a, bf16x4 ident) {
-  return to_bf16x4(mma16(a, ident, f32x4{0.f, 0.f, 0.f, 0.f}));
-}
-
 // Transposed fragment load (ds_read_b64_tr_b16). Within each group of 16
 // lanes, lane c supplies the address of 4 consecutive bf16 values; lane c' of
 // the group receives value c' % 4 of the pieces addressed by lanes
@@ -236,15 +219,6 @@ __device__ __forceinline__ bf16x8 tr_frag32(const bf16_t (*tile)[64], int m, int
   return cat8(tr_frag(tile, 32 * m, c0, lane), tr_frag(tile, 32 * m + 16, c0, lane));
 }
 
-// sum over the 16 lanes of a DPP row, result in every lane of the row
-__device__ __forceinline__ float row_sum16(float x) {
-  x += dpp_mov<0x128>(x);   // row_ror:8
-  x += dpp_mov<0x124>(x);   // row_ror:4
-  x += dpp_mov<0x122>(x);   // row_ror:2
-  x += dpp_mov<0x121>(x);   // row_ror:1
-  return x;
-}
-
 // inclusive prefix sum over the 16 lanes of a DPP row
 __device__ __forceinline__ float row_scan16(float x) {
   x += dpp_mov<0x111>(x);   // row_shr:1
@@ -289,13 +263,6 @@ __device__ __forceinline__ float log2_decay(float x) {
   return (kWScale * kLog2e) * sig;
 }
 
-// wait until at most n vector-memory operations of this wave are in flight
-// (gfx9 s_waitcnt encoding; expcnt and lgkmcnt left at their maxima)
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt(((N >> 4) << 14) | (0xF << 8) | (0x7 << 4) | (N & 0xF));
-}
 // this wave's LDS writes are done and visible to its own later reads
 __device__ __forceinline__ void wave_lds_sync() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);

@@ -28,17 +28,6 @@ def bf16_round(x: np.ndarray) -> np.ndarray:
     return ((u + bias) & np.uint32(0xFFFF0000)).view(np.float32)
 
 
-def bf16_bits(x: np.ndarray) -> np.ndarray:
-    """The upper 16 bits of bf16-representable float32 values, as uint16."""
-    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
-    return (u >> 16).astype(np.uint16)
-
-
-def bits_to_f32(h: np.ndarray) -> np.ndarray:
-    """Widen raw bf16 bit patterns (uint16) to float32."""
-    return (np.asarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
-
-
 def make_inputs(B: int, T: int, H: int, N: int = 64, seed: int = 0,
                 s0_std: float | None = None, bf16: bool = False,
                 with_grad: bool = True) -> dict:

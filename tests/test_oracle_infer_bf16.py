@@ -293,3 +293,28 @@ def test_rowwise_restatement_agrees_bitwise(oracle):
     y_r = _rowwise_bf16(*(d[n] for n in NAMES), ids, s_r, mask, elapsed, True)
     np.testing.assert_array_equal(y_o, y_r)
     np.testing.assert_array_equal(s_o, s_r)
+
+
+def test_rounding_matches_an_independent_rne(oracle):
+    """The oracle's bf16 rounding (wkv7o_round_bf16, used at every rounding
+    point of the bf16 decode) against torch's float32 -> bfloat16 conversion,
+    an independent round-to-nearest-even, on exact ties (both parities, both
+    signs), values just either side of a tie, the bf16 range's ends and
+    random values."""
+    import torch
+    ties = []
+    for base in (1.0, 1.5, -3.25, 1e-3, 6.5e4):
+        b = np.float32(base)
+        ulp = np.float32(np.spacing(np.float32(bf(b)))) * np.float32(2.0 ** 16)   # one bf16 ulp
+        half = np.float32(ulp / 2)
+        ties += [b + half, b - half, b + 3 * half]
+        ties += [np.nextafter(b + half, np.float32(np.inf)), np.nextafter(b + half, np.float32(-np.inf))]
+    edge = [np.float32(3.3895314e38), np.float32(-3.3895314e38), np.float32(1.1754944e-38), np.float32(0.0),
+            np.float32(-0.0)]
+    rng = np.random.default_rng(5)
+    rand = list(rng.standard_normal(2000).astype(np.float32) * np.float32(10.0) ** rng.integers(-20, 20, 2000))
+    xs = np.array(ties + edge + rand, np.float32)
+    got = np.array([oracle.round_bf16(float(x)) for x in xs], np.float32)
+    want = torch.from_numpy(xs).to(torch.bfloat16).to(torch.float32).numpy()
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    np.testing.assert_array_equal(bf(xs).view(np.uint32), want.view(np.uint32))
