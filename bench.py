@@ -556,6 +556,118 @@ def bench_decode(cfg, steps, warmup, probe=False, state_dtype="f32"):
     }
 
 
+# The reference's own kernel benchmark cases (crates/rwkv-nn/benches/kernels/
+# mod.rs:109-113): (name, batch, context_len, heads, chunk_len), head size 64,
+# run by its Criterion benches at element type f32 (mod.rs:11-12, Cuda<f32, i32>).
+CRITERION_CASES = (("b1_t128_h8_d64_c32", 1, 128, 8, 32),
+                   ("b2_t256_h8_d64_c32", 2, 256, 8, 32),
+                   ("b4_t512_h16_d64_c64", 4, 512, 16, 64))
+
+
+def bench_criterion(steps, warmup, with_cpu):
+    """The calls the reference's Criterion benches time (benches/kernels/
+    wkv7_{pretrain,statepass,statetune}/{forward,backward}.rs and
+    wkv7_infer/forward.rs), on their three cases, through the C ABI: fp32
+    operands, every input N(0, 1) as mod.rs:115-178 draws them (initial state,
+    output and final-state gradients too), the infer call over the whole
+    context with a Bernoulli(0.95) mask, batch_ids 0..B-1 and elapsed_t 0.
+    Per call: the GPU time from HIP events around `steps` back-to-back calls,
+    and the host time per call over the same loop (enqueue included, one
+    synchronisation at the end, as a Criterion iteration without a device
+    sync inside measures)."""
+    import torch
+    native = importlib.import_module("rwkv-rs_amd._native")
+    lib = native.lib()
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    sp = stream.cuda_stream
+    F32 = native.DTYPE_F32
+    g = torch.Generator(device="cpu").manual_seed(0x5EED0005)
+    cases, cpu = {}, {}
+    total_us = 0.0
+    for name, B, T, H, C in CRITERION_CASES:
+        def rnd(*shape):
+            return torch.randn(*shape, generator=g).to(dev)
+        ins = [rnd(B, T, H, N_HEAD) for _ in range(6)]
+        ip = [t.data_ptr() for t in ins]
+        s0, dy, dsT = rnd(B, H, N_HEAD, N_HEAD), rnd(B, T, H, N_HEAD), rnd(B, H, N_HEAD, N_HEAD)
+        mask = (torch.rand(B, T, generator=g) < 0.95).float().to(dev)
+        ids = torch.arange(B, dtype=torch.int32, device=dev)
+        et = torch.zeros(B, dtype=torch.int32, device=dev)
+        ckpt = torch.empty(B, H, T // C, N_HEAD, N_HEAD, device=dev)
+        sa, y = torch.empty(B, T, H, N_HEAD, device=dev), torch.empty(B, T, H, N_HEAD, device=dev)
+        sT, ds0 = torch.empty_like(s0), torch.empty_like(s0)
+        grads = [torch.empty(B, T, H, N_HEAD, device=dev) for _ in range(6)]
+        gp = [t.data_ptr() for t in grads]
+        state = s0.clone()
+        dims = (B, T, H, N_HEAD, C)
+        calls = {
+            "pretrain_forward": lambda: lib.wkv7_pretrain_forward(
+                *ip, *dims, F32, ckpt.data_ptr(), sa.data_ptr(), y.data_ptr(), sp),
+            "pretrain_backward": lambda: lib.wkv7_pretrain_backward(
+                *ip, ckpt.data_ptr(), sa.data_ptr(), dy.data_ptr(), *dims, F32, *gp, sp),
+            "statepass_forward": lambda: lib.wkv7_statepass_forward(
+                *ip, s0.data_ptr(), *dims, F32, ckpt.data_ptr(), sa.data_ptr(), y.data_ptr(),
+                sT.data_ptr(), sp),
+            "statepass_backward": lambda: lib.wkv7_statepass_backward(
+                *ip, ckpt.data_ptr(), sa.data_ptr(), dy.data_ptr(), dsT.data_ptr(), *dims, F32,
+                *gp, ds0.data_ptr(), sp),
+            "statetune_forward": lambda: lib.wkv7_statetune_forward(
+                *ip, s0.data_ptr(), *dims, F32, ckpt.data_ptr(), sa.data_ptr(), y.data_ptr(), sp),
+            "statetune_backward": lambda: lib.wkv7_statetune_backward(
+                *ip, ckpt.data_ptr(), sa.data_ptr(), dy.data_ptr(), *dims, F32, *gp,
+                ds0.data_ptr(), sp),
+            "infer_forward": lambda: lib.wkv7_infer_forward(
+                *ip, ids.data_ptr(), state.data_ptr(), mask.data_ptr(), et.data_ptr(), B, T, H,
+                N_HEAD, B, F32, F32, 0, y.data_ptr(), sp),
+        }
+        res = {}
+        for call, fn in calls.items():
+            for _ in range(warmup):
+                native.check(fn())
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            t0 = time.perf_counter()
+            e0.record(stream)
+            for _ in range(steps):
+                native.check(fn())
+            e1.record(stream)
+            torch.cuda.synchronize()
+            host = (time.perf_counter() - t0) / steps
+            res[call] = {"gpu_us": e0.elapsed_time(e1) * 1e3 / steps, "host_us": host * 1e6}
+        cases[name] = res
+        total_us += res["statepass_forward"]["gpu_us"] + res["statepass_backward"]["gpu_us"]
+        if with_cpu:
+            import oracle
+            hn = [t.cpu().numpy() for t in ins]
+            t0 = time.perf_counter()
+            f = oracle.forward_f32(*hn, s0=s0.cpu().numpy(), chunk_len=C, nthreads=1)
+            t1 = time.perf_counter()
+            oracle.backward_f32(*hn, f["state"], f["removal_state"], dy.cpu().numpy(),
+                                ds_T=dsT.cpu().numpy(), chunk_len=C, nthreads=1)
+            t2 = time.perf_counter()
+            cpu[name] = {"statepass_forward_us": (t1 - t0) * 1e6, "statepass_backward_us": (t2 - t1) * 1e6}
+    out = {
+        "metric": "WKV7 statepass forward+backward latency on the reference's Criterion cases "
+                  "(F=f32), summed over the three cases",
+        "value": total_us, "unit": "us", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": total_us / 1e3, "higher_is_better": False, "scaling": "strong",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "wkv7_criterion_cases",
+                   "cases": [dict(zip(("name", "batch", "context_len", "num_heads", "chunk_len"), c))
+                             for c in CRITERION_CASES]},
+        "cases": cases,
+    }
+    if with_cpu:
+        out["cpu_baseline"] = {
+            "value": sum(v["statepass_forward_us"] + v["statepass_backward_us"] for v in cpu.values()),
+            "unit": "us", "cores": 1, "kind": "port", "cpu_model": cpu_model(),
+            "sample": "the same three cases and operand bytes, statepass forward and backward "
+                      "once each on one thread (oracle/wkv7_oracle.c, reference operation order)",
+            "cases": cpu}
+    return out
+
+
 def bench_lm(cfg, steps, warmup, neighbor_ops="hip"):
     """config[4]: one RWKV-7 0.1B training step (forward, loss, backward, Adam
     update) on the host framework with the WKV7 operator on the HIP kernels;
@@ -618,7 +730,9 @@ def main():
     # passes (about 30 ms of load: 1.16 ms falling to 0.89 ms at config[1],
     # the forward unchanged); the default warm-up covers that ramp
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--config", default="cfg1", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="cfg1", choices=sorted(CONFIGS) + ["criterion"],
+                    help="cfg0-cfg4: BASELINE.json's configurations; criterion: the calls of the "
+                         "reference's own Criterion benches on their three cases")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--state-dtype", default="f32", choices=("f32", "bf16"),
                     help="cfg3: the decode state's element type")
@@ -649,6 +763,9 @@ def main():
               "across GPUs is not built)",
               file=sys.stderr)
         sys.exit(2)
+    if args.config == "criterion":
+        print(json.dumps(bench_criterion(args.steps, args.warmup, with_cpu=not args.no_cpu)), flush=True)
+        return
     cfg = CONFIGS[args.config]
     if args.config == "cfg4":
         out = bench_lm(cfg, args.steps, args.warmup, args.neighbor_ops)
