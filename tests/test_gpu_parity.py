@@ -149,6 +149,7 @@ def test_fp32_long_chunks_as_accurate_as_reference(wk, oracle, case):
     (1, 48, 3, 16, 0.1, 13),    # T not a multiple of 32: partial last forward tile
     (1, 40, 2, 8, 0.1, 14),     # backward reloads inside a 16-step tile, partial first tile
     (1, 64, 2, 32, 0.1, 15),    # one checkpoint every 32-step forward tile
+    (3, 32, 100, 16, 0.1, 16),  # 300 (batch, head) pairs: more workgroups than CUs
 ])
 def test_bf16_inputs_fp32_state(wk, oracle, case):
     B, T, H, C, s0_std, seed = case
