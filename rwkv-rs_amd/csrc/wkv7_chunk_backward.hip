@@ -105,6 +105,8 @@ struct BwdLds {
   // its gradient rows): the removal_state in fp32, and the k and b rows
   float sa32[kL][64];
   PadTile kbt[2];
+  float abt[kL][20];                // A_ab on its way to A_ab^T (set-up wave 4; rows padded so
+                                    // the four quads' column writes fall on distinct banks)
 };
 typedef float S0Rows[64][68];       // chunk 0's rebuilt start state, [key i][value j]
 static_assert(sizeof(S0Rows) <= sizeof(Prep), "start state fits the free set-up buffer");
@@ -229,7 +231,8 @@ __device__ __forceinline__ GramIn products_load(const Prep& P, int wave, int t, 
   }
   return g;
 }
-__device__ __forceinline__ void setup_products(Prep& P, const GramIn& g, int wave, int t, int qd, int lane) {
+__device__ __forceinline__ void setup_products(Prep& P, const GramIn& g, int wave, int t, int qd, int lane,
+                                               float (*abt)[20]) {
   const int strict = wave < 2 ? 1 : 0;
   const Split8 (&X)[2] = g.X;
   const Split8 (&Y)[2] = g.Y;
@@ -237,10 +240,12 @@ __device__ __forceinline__ void setup_products(Prep& P, const GramIn& g, int wav
 #pragma unroll
   for (int r = 0; r < 4; ++r) d[r] = 4 * qd + r - t >= strict ? d[r] : 0.f;
   if (wave == 0) {
-    // d = A_ab[t'][s]; the swapped product is A_ab^T, masked the other way
-    f32x4 dt = gram_x3(Y, X);
+    // d = A_ab[t'][s]; A_ab^T in the same layout through LDS (this wave
+    // writes its result tile and reads it back by rows)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) dt[r] = t - (4 * qd + r) >= 1 ? dt[r] : 0.f;
+    for (int r = 0; r < 4; ++r) abt[4 * qd + r][t] = d[r];
+    wave_lds_sync();
+    const f32x4 dt = *reinterpret_cast<const f32x4*>(&abt[t][4 * qd]);
     // P^T as an A operand: lane l holds P[4 qd + e][l % 16], P's result layout
     P.frag[F_PT][lane] = stack_f(unit_lower_inverse(d, dt, t, qd));
   } else {
@@ -434,7 +439,7 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
   lds_barrier();
   if (!grad) {
     if (last >= 1) stage_dec(fetch(last - 1, last));
-    setup_products(L.prep[last & 1], products_load(L.prep[last & 1], wq, t, qd), wq, t, qd, lane);
+    setup_products(L.prep[last & 1], products_load(L.prep[last & 1], wq, t, qd), wq, t, qd, lane, L.abt);
   }
 
   // one chunk; kFull: chunk c - 1 exists and is set up alongside (c >= 1).
@@ -504,6 +509,11 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
       f32x4 dSp[4];
 #pragma unroll
       for (int ib = 0; ib < 4; ++ib) dSp[ib] = dS[ib] * glv[ib];
+      // the carried gradient's terms that do not wait for dSA first: dS'^T +
+      // R^^T dY, so that dS' is not needed afterwards and is split in place
+      f32x4 acc[4];
+#pragma unroll
+      for (int ib = 0; ib < 4; ++ib) acc[ib] = mma_s2(rT[ib], dycf, dSp[ib]);
       const Split8 Sx0 = split8(dSp[0], dSp[1]), Sx1 = split8(dSp[2], dSp[3]);
       f32x4 z = mma32x3(Bt0, Sx0, f32x4{0.f, 0.f, 0.f, 0.f});
       z = mma32x3(Bt1, Sx1, z);
@@ -516,10 +526,7 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
       dv = mma_s3(f_akt, dsas, dv);
       // carried gradient dS0^T = dS'^T + R^^T dY + A^^T dSA
 #pragma unroll
-      for (int ib = 0; ib < 4; ++ib) {
-        f32x4 acc = mma_s2(rT[ib], dycf, dSp[ib]);
-        dS[ib] = mma_s3(aT[ib], dsas, acc);
-      }
+      for (int ib = 0; ib < 4; ++ib) dS[ib] = mma_s3(aT[ib], dsas, acc[ib]);
       // exchange for the key stage: dS' as [value j][key i], dSA as [j][step]
 #pragma unroll
       for (int m = 0; m < 2; ++m)
@@ -627,7 +634,7 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
         __builtin_amdgcn_sched_barrier(0);
         stage_dec(pre);             // decay rows of chunk c - 2 (the decays of phase A are done)
         stage_grad(pre, sb ^ 1);    // gradient rows of chunk c - 1 (free buffer)
-        setup_products(Pn, gi, wq, t, qd, lane);
+        setup_products(Pn, gi, wq, t, qd, lane, L.abt);
       }
     }
     // Phase C's operands that phase B does not write, read before the
