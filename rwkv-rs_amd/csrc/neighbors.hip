@@ -129,10 +129,127 @@ __device__ __forceinline__ bool valid(const ShiftMixArgs& a, int64_t r) {
   return !a.mask || load1<XB>(a.mask, r) != 0.f;
 }
 
+// Raw 4-element loads, widened later, so that a group of rows can have all
+// its loads in flight before any is used
+template <bool BF> struct Raw4;
+template <> struct Raw4<true> {
+  typedef uint2 type;
+  static __device__ __forceinline__ type load(const void* base, int64_t i) {
+    return *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + i);
+  }
+  static __device__ __forceinline__ F4 widen(type r) {
+    return F4{{bf16_to_f32(r.x & 0xffffu), bf16_to_f32(r.x >> 16), bf16_to_f32(r.y & 0xffffu),
+               bf16_to_f32(r.y >> 16)}};
+  }
+};
+template <> struct Raw4<false> {
+  typedef float4 type;
+  static __device__ __forceinline__ type load(const void* base, int64_t i) {
+    return *reinterpret_cast<const float4*>(static_cast<const float*>(base) + i);
+  }
+  static __device__ __forceinline__ F4 widen(type r) { return F4{{r.x, r.y, r.z, r.w}}; }
+};
+
 // KM: the largest mix count an instantiation serves (1, 6 or 8), so that
-// its per-thread arrays hold only as many mixes as the call can have
+// its per-thread arrays hold only as many mixes as the call can have.
+//
+// A wave's rows, in three phases: every x and mask load of its rows (and of
+// the row before them) is issued first, row indices clamped to the tensor so
+// that the loads need no branch; then the external shifts, loaded only for
+// rows that start a sequence or follow a masked step; then each row's mixes
+// are computed and stored. The store phase has no loads, so nothing waits
+// for a store: on this hardware a wait for a load also waits for every store
+// issued before it. (One row's loads in flight per wave, each behind the
+// previous row's stores, left the kernel bound by memory latency.)
 template <bool XB, bool OB, int KM>
 __global__ __launch_bounds__(256) void shift_mix_forward_kernel(ShiftMixArgs a) {
+  constexpr int R = kMixRowsPerWave;
+  typedef Raw4<XB> RX;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t C = a.C;
+  const int64_t c = (static_cast<int64_t>(blockIdx.y) * 64 + lane) * 4;
+  const int64_t rows = a.batch * a.T;
+  const int64_t r0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * R;
+  const int64_t r1 = r0 + R < rows ? r0 + R : rows;
+  if (c >= C || r0 >= r1) return;
+  const int n = static_cast<int>(r1 - r0);
+  // the scales first: their loads sit under a branch (there may be none), and
+  // a wait for them then waits for no row load
+  F4 mu[KM];
+#pragma unroll
+  for (int k = 0; k < KM; ++k)
+    mu[k] = k < a.num_mixes ? load4<false>(a.scales, k * C + c) : zero4();
+  // the mask, or x standing in for it when there is none (in bounds at every
+  // row index, value ignored), so that its loads need no branch either
+  const void* const mp = a.mask ? a.mask : a.x;
+  // slot 0 is the row before the first (read as row r0 when r0 = 0: unused)
+  typename RX::type xr[R + 1];
+  float mr[R + 1];
+#pragma unroll
+  for (int i = 0; i <= R; ++i) {
+    const int64_t r = r0 - 1 + (i == 0 ? (r0 > 0 ? 0 : 1) : (i <= n ? i : n));
+    xr[i] = RX::load(a.x, r * C + c);
+    mr[i] = load1<XB>(mp, r);
+  }
+  // which rows take the external shift (row-uniform, so wave-uniform)
+  const int64_t b0 = r0 / a.T, t0 = r0 - b0 * a.T;
+  bool ext[R];
+  {
+    int64_t t = t0;
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      ext[i] = t == 0 || (a.mask && mr[i] == 0.f);   // mr[i] is the previous row's mask
+      if (++t == a.T) t = 0;
+    }
+  }
+  F4 es[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) es[i] = zero4();
+  if (a.shift) {
+    int64_t b = b0, t = t0;
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      if (i < n && ext[i]) es[i] = external_shift<XB>(a, b, c);
+      if (++t == a.T) {
+        t = 0;
+        ++b;
+      }
+    }
+    // settle these loads here (no store is outstanding yet), so that the
+    // store phase never waits on them: vmcnt(0), other counters untouched
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+  }
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    if (i < n) {
+      const int64_t r = r0 + i;
+      const F4 xt = RX::widen(xr[i + 1]);
+      const bool cur_valid = !a.mask || mr[i + 1] != 0.f;
+      const F4 prev = ext[i] ? es[i] : RX::widen(xr[i]);
+      F4 d;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) d.v[j] = cur_valid ? prev.v[j] - xt.v[j] : 0.f;
+#pragma unroll
+      for (int k = 0; k < KM; ++k) {
+        if (k < a.num_mixes) {
+          F4 o;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) o.v[j] = xt.v[j] + d.v[j] * mu[k].v[j];
+          store4<OB>(a.mixes[k], r * C + c, o);
+        }
+      }
+      if (a.diff) store4<OB>(a.diff, r * C + c, d);
+    }
+  }
+}
+
+// The one-mix instance walks its rows one at a time instead: there a row is
+// mostly its x load (16 bytes per lane against one 8-byte store), and the
+// phased walk above measured slower for it (9.4 against 8.7 us per launch in
+// the config[4] step, same box), while with six mixes it measured faster
+// (17.2 against 22.1 us at config[4]'s shape, same box).
+template <bool XB, bool OB, int KM>
+__global__ __launch_bounds__(256) void shift_mix_forward_serial_kernel(ShiftMixArgs a) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t C = a.C;
   const int64_t c = (static_cast<int64_t>(blockIdx.y) * 64 + lane) * 4;
@@ -208,27 +325,6 @@ __device__ __forceinline__ F4 diff_grad_at(const ShiftMixArgs& a, const F4 (&mu)
   }
   return dd;
 }
-
-// Raw 4-element loads, widened later, so that a group of rows can have all
-// its loads in flight before any is used
-template <bool BF> struct Raw4;
-template <> struct Raw4<true> {
-  typedef uint2 type;
-  static __device__ __forceinline__ type load(const void* base, int64_t i) {
-    return *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + i);
-  }
-  static __device__ __forceinline__ F4 widen(type r) {
-    return F4{{bf16_to_f32(r.x & 0xffffu), bf16_to_f32(r.x >> 16), bf16_to_f32(r.y & 0xffffu),
-               bf16_to_f32(r.y >> 16)}};
-  }
-};
-template <> struct Raw4<false> {
-  typedef float4 type;
-  static __device__ __forceinline__ type load(const void* base, int64_t i) {
-    return *reinterpret_cast<const float4*>(static_cast<const float*>(base) + i);
-  }
-  static __device__ __forceinline__ F4 widen(type r) { return F4{{r.x, r.y, r.z, r.w}}; }
-};
 
 // The backward of a wave's rows: dx_t = sum_i g_i - m_t dd_t + m_t m_(t+1)
 // dd_(t+1), with dd_t = sum_i g_i scale_i (+ the diff gradient), the last
@@ -424,10 +520,22 @@ __global__ __launch_bounds__(64 * kSumWaves) void column_sum_kernel(ColumnSumArg
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t c = static_cast<int64_t>(blockIdx.x) * 64 + lane;
   const int q = blockIdx.y;
+  // kBatch partials in flight per wave (indices clamped, so the loads need no
+  // branch), added in the same order as one at a time
+  constexpr int kBatch = 8;
   float s = 0.f;
   if (c < a.C)
-    for (int64_t rb = wave; rb < a.row_blocks; rb += kSumWaves)
-      s += a.ws[(rb * a.Q + q) * a.C + c];
+    for (int64_t rb0 = wave; rb0 < a.row_blocks; rb0 += kSumWaves * kBatch) {
+      float x[kBatch];
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const int64_t rb = rb0 + i * kSumWaves;
+        x[i] = a.ws[((rb < a.row_blocks ? rb : a.row_blocks - 1) * a.Q + q) * a.C + c];
+      }
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i)
+        if (rb0 + i * kSumWaves < a.row_blocks) s += x[i];
+    }
   red[wave][lane] = s;
   __syncthreads();
   if (wave == 0 && c < a.C) {
@@ -441,14 +549,10 @@ __global__ __launch_bounds__(64 * kSumWaves) void column_sum_kernel(ColumnSumArg
 }
 
 // -------------------------------------------------------------- gated readout
-template <bool OPB>
-__device__ __forceinline__ void readout_row(const ReadoutArgs& a, int64_t idx, const F4& rk,
-                                            F4& y, F4& r, F4& k, F4& v, float& rstd, F4& yh,
-                                            float& s) {
-  y = load4<OPB>(a.y, idx);
-  r = load4<OPB>(a.r, idx);
-  k = load4<OPB>(a.k, idx);
-  v = load4<OPB>(a.v, idx);
+// A row's group-norm statistics and bonus term: yh = (y - mean) rstd over the
+// head's 64 channels, s = sum_n r k bonus (16 lanes of 4 channels).
+__device__ __forceinline__ void readout_stats(float eps, const F4& rk, const F4& y, const F4& r,
+                                              const F4& k, F4& yh, float& rstd, float& s) {
   const float mean = sum16(y.v[0] + y.v[1] + y.v[2] + y.v[3]) * (1.f / 64.f);
   float d2 = 0.f, bon = 0.f;
 #pragma unroll
@@ -457,85 +561,124 @@ __device__ __forceinline__ void readout_row(const ReadoutArgs& a, int64_t idx, c
     d2 += yh.v[j] * yh.v[j];
     bon += r.v[j] * k.v[j] * rk.v[j];
   }
-  rstd = rsqrtf(sum16(d2) * (1.f / 64.f) + a.eps);
+  rstd = rsqrtf(sum16(d2) * (1.f / 64.f) + eps);
 #pragma unroll
   for (int j = 0; j < 4; ++j) yh.v[j] *= rstd;
   s = sum16(bon);
 }
 
+// Both readout kernels: a 16-lane group walks kReadoutRowsPerGroup rows of
+// one head. All of the group's loads are issued before any row is used (row
+// indices clamped to the tensor, so the loads need no branch); rows past the
+// end are computed on the clamped data and not stored. (One row's loads in
+// flight per group left these kernels bound by HBM latency.)
 template <bool OPB, bool ACTB>
 __global__ __launch_bounds__(256) void readout_forward_kernel(ReadoutArgs a) {
+  constexpr int R = kReadoutRowsPerGroup;
+  typedef Raw4<OPB> RO;
+  typedef Raw4<ACTB> RA;
   const int grp = threadIdx.x >> 4, l = threadIdx.x & 15;
   const int64_t C = a.H * 64;
   const int64_t cc = static_cast<int64_t>(blockIdx.y) * 64 + l * 4;
+  const int64_t r0 = (static_cast<int64_t>(blockIdx.x) * 16 + grp) * R;
+  if (r0 >= a.rows) return;  // uniform over the group; no block-wide sync follows
+  const int n = a.rows - r0 < R ? static_cast<int>(a.rows - r0) : R;
+  typename RO::type yr[R], rr[R], kr[R], vr[R];
+  typename RA::type gr[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int64_t idx = (r0 + (i < n ? i : n - 1)) * C + cc;
+    yr[i] = RO::load(a.y, idx);
+    rr[i] = RO::load(a.r, idx);
+    kr[i] = RO::load(a.k, idx);
+    vr[i] = RO::load(a.v, idx);
+    gr[i] = RA::load(a.gate, idx);
+  }
   const F4 gw = load4<false>(a.weight, cc), gb = load4<false>(a.bias, cc);
   const F4 rk = load4<false>(a.bonus, cc);
-  const int64_t r0 = (static_cast<int64_t>(blockIdx.x) * 16 + grp) * kReadoutRowsPerGroup;
-  for (int i = 0; i < kReadoutRowsPerGroup; ++i) {
-    const int64_t row = r0 + i;
-    if (row >= a.rows) break;  // uniform over the 16 lanes of the group
-    const int64_t idx = row * C + cc;
-    F4 y, r, k, v, yh;
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const F4 v = RO::widen(vr[i]), g = RA::widen(gr[i]);
+    F4 yh;
     float rstd, s;
-    readout_row<OPB>(a, idx, rk, y, r, k, v, rstd, yh, s);
-    const F4 g = load4<ACTB>(a.gate, idx);
+    readout_stats(a.eps, rk, RO::widen(yr[i]), RO::widen(rr[i]), RO::widen(kr[i]), yh, rstd, s);
     F4 o;
 #pragma unroll
     for (int j = 0; j < 4; ++j) o.v[j] = (yh.v[j] * gw.v[j] + gb.v[j] + s * v.v[j]) * g.v[j];
-    store4<ACTB>(a.out, idx, o);
+    if (i < n) store4<ACTB>(a.out, (r0 + i) * C + cc, o);
   }
 }
 
 template <bool OPB, bool ACTB>
 __global__ __launch_bounds__(256) void readout_backward_kernel(ReadoutArgs a) {
+  constexpr int R = kReadoutRowsPerGroup;
+  typedef Raw4<OPB> RO;
+  typedef Raw4<ACTB> RA;
   __shared__ float red[16][kReadoutSums][64];
   const int grp = threadIdx.x >> 4, l = threadIdx.x & 15;
   const int64_t C = a.H * 64;
   const int64_t cc = static_cast<int64_t>(blockIdx.y) * 64 + l * 4;
-  const F4 gw = load4<false>(a.weight, cc), gb = load4<false>(a.bias, cc);
-  const F4 rk = load4<false>(a.bonus, cc);
   F4 aw = zero4(), ab = zero4(), ak = zero4();
-  const int64_t r0 = (static_cast<int64_t>(blockIdx.x) * 16 + grp) * kReadoutRowsPerGroup;
-  for (int i = 0; i < kReadoutRowsPerGroup; ++i) {
-    const int64_t row = r0 + i;
-    if (row >= a.rows) break;  // uniform over the 16 lanes of the group
-    const int64_t idx = row * C + cc;
-    F4 y, r, k, v, yh;
-    float rstd, s;
-    readout_row<OPB>(a, idx, rk, y, r, k, v, rstd, yh, s);
-    const F4 g = load4<ACTB>(a.gate, idx);
-    const F4 dout = load4<ACTB>(a.out_grad, idx);
-    F4 dz, dg, dv, dyh;
-    float ds = 0.f, m1 = 0.f, m2 = 0.f;
+  const int64_t r0 = (static_cast<int64_t>(blockIdx.x) * 16 + grp) * R;
+  if (r0 < a.rows) {  // uniform over the group
+    const int n = a.rows - r0 < R ? static_cast<int>(a.rows - r0) : R;
+    typename RO::type yr[R], rr[R], kr[R], vr[R];
+    typename RA::type gr[R], dr[R];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float z = yh.v[j] * gw.v[j] + gb.v[j] + s * v.v[j];
-      dz.v[j] = dout.v[j] * g.v[j];
-      dg.v[j] = dout.v[j] * z;
-      aw.v[j] += dz.v[j] * yh.v[j];
-      ab.v[j] += dz.v[j];
-      dv.v[j] = dz.v[j] * s;
-      ds += dz.v[j] * v.v[j];
-      dyh.v[j] = dz.v[j] * gw.v[j];
-      m1 += dyh.v[j];
-      m2 += dyh.v[j] * yh.v[j];
+    for (int i = 0; i < R; ++i) {
+      const int64_t idx = (r0 + (i < n ? i : n - 1)) * C + cc;
+      yr[i] = RO::load(a.y, idx);
+      rr[i] = RO::load(a.r, idx);
+      kr[i] = RO::load(a.k, idx);
+      vr[i] = RO::load(a.v, idx);
+      gr[i] = RA::load(a.gate, idx);
+      dr[i] = RA::load(a.out_grad, idx);
     }
-    ds = sum16(ds);
-    m1 = sum16(m1) * (1.f / 64.f);
-    m2 = sum16(m2) * (1.f / 64.f);
-    F4 dr, dk, dy;
+    const F4 gw = load4<false>(a.weight, cc), gb = load4<false>(a.bias, cc);
+    const F4 rk = load4<false>(a.bonus, cc);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      dr.v[j] = ds * k.v[j] * rk.v[j];
-      dk.v[j] = ds * r.v[j] * rk.v[j];
-      ak.v[j] += ds * r.v[j] * k.v[j];
-      dy.v[j] = rstd * (dyh.v[j] - m1 - yh.v[j] * m2);
+    for (int i = 0; i < R; ++i) {
+      const F4 r = RO::widen(rr[i]), k = RO::widen(kr[i]), v = RO::widen(vr[i]);
+      const F4 g = RA::widen(gr[i]), dout = RA::widen(dr[i]);
+      F4 yh;
+      float rstd, s;
+      readout_stats(a.eps, rk, RO::widen(yr[i]), r, k, yh, rstd, s);
+      const bool live = i < n;  // a row past the end adds nothing to the column sums
+      F4 dz, dg, dv, dyh;
+      float ds = 0.f, m1 = 0.f, m2 = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float z = yh.v[j] * gw.v[j] + gb.v[j] + s * v.v[j];
+        dz.v[j] = dout.v[j] * g.v[j];
+        dg.v[j] = dout.v[j] * z;
+        aw.v[j] = live ? aw.v[j] + dz.v[j] * yh.v[j] : aw.v[j];
+        ab.v[j] = live ? ab.v[j] + dz.v[j] : ab.v[j];
+        dv.v[j] = dz.v[j] * s;
+        ds += dz.v[j] * v.v[j];
+        dyh.v[j] = dz.v[j] * gw.v[j];
+        m1 += dyh.v[j];
+        m2 += dyh.v[j] * yh.v[j];
+      }
+      ds = sum16(ds);
+      m1 = sum16(m1) * (1.f / 64.f);
+      m2 = sum16(m2) * (1.f / 64.f);
+      F4 drr, dk, dy;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        drr.v[j] = ds * k.v[j] * rk.v[j];
+        dk.v[j] = ds * r.v[j] * rk.v[j];
+        ak.v[j] = live ? ak.v[j] + ds * r.v[j] * k.v[j] : ak.v[j];
+        dy.v[j] = rstd * (dyh.v[j] - m1 - yh.v[j] * m2);
+      }
+      if (live) {
+        const int64_t idx = (r0 + i) * C + cc;
+        store4<ACTB>(a.gate_grad, idx, dg);
+        store4<OPB>(a.v_grad, idx, dv);
+        store4<OPB>(a.r_grad, idx, drr);
+        store4<OPB>(a.k_grad, idx, dk);
+        store4<OPB>(a.y_grad, idx, dy);
+      }
     }
-    store4<ACTB>(a.gate_grad, idx, dg);
-    store4<OPB>(a.v_grad, idx, dv);
-    store4<OPB>(a.r_grad, idx, dr);
-    store4<OPB>(a.k_grad, idx, dk);
-    store4<OPB>(a.y_grad, idx, dy);
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -791,6 +934,10 @@ hipError_t dispatch(const ShiftMixArgs& a, dim3 grid, dim3 block, hipStream_t s)
 template <bool XB, bool OB, int KM>
 struct MixForward {
   static constexpr auto fn = shift_mix_forward_kernel<XB, OB, KM>;
+};
+template <bool XB, bool OB>
+struct MixForward<XB, OB, 1> {
+  static constexpr auto fn = shift_mix_forward_serial_kernel<XB, OB, 1>;
 };
 template <bool XB, bool OB, int KM>
 struct MixBackward {

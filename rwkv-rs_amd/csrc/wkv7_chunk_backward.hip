@@ -602,31 +602,43 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_chunk_kernel(const BwdChun
       if (c < last) flush(c + 1);
 #pragma unroll
       for (int r = 0; r < 4; ++r) out_at(outs[O_DV], 4 * qd + r, jcol) = __builtin_bit_cast(bf16_t, (__bf16)dv[r]);
-      // step products with dSA (one per wave): B_sav^T = dsa v^T (s > t),
-      // C_dsav^T = v dsa^T (s < t), B_sasa^T = dsa sa^T (s > t),
-      // C_dsasa^T = sa dsa^T (s < t)
-      const Split8 q[2] = {{dsa_frag(0, 0), dsa_frag(1, 0)}, {dsa_frag(0, 1), dsa_frag(1, 1)}};
-      Split8 g[2];
-      {
-        const bf16_t (*const ylo)[64] = wq >= 2 ? stg[S_SAL].r : L.zero;
-        const int yhi = wq >= 2 ? S_SAH : S_V;
+      // step products with dSA: B_sav^T = dsa v^T (s > t), C_dsav^T = v dsa^T
+      // (s < t), B_sasa^T = dsa sa^T (s > t), C_dsasa^T = sa dsa^T (s < t).
+      // Wave 0 forms none: its SIMD also runs set-up wave 4, which forms the
+      // inverse in this phase. Wave 1 forms both products with v (the two
+      // orientations of the same operands), waves 2 and 3 one each with sa.
+      if (wq != 0) {
+        const Split8 q[2] = {{dsa_frag(0, 0), dsa_frag(1, 0)}, {dsa_frag(0, 1), dsa_frag(1, 1)}};
+        Split8 g[2];
+        {
+          const bf16_t (*const ylo)[64] = wq >= 2 ? stg[S_SAL].r : L.zero;
+          const int yhi = wq >= 2 ? S_SAH : S_V;
 #pragma unroll
-        for (int m = 0; m < 2; ++m) g[m] = Split8{row_frag(stg[yhi].r, t, m, qd), row_frag(ylo, t, m, qd)};
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      const int sgn = (wq & 1) ? -1 : 1;   // keep s > t (B_), s < t (C_)
-      // the wave's orientation (wq is wave-uniform: a scalar branch)
-      f32x4 e = {0.f, 0.f, 0.f, 0.f};
-      if (wq & 1) {
-        e = mma32x3(g[0], q[0], e);
-        e = mma32x3(g[1], q[1], e);
-      } else {
-        e = mma32x3(q[0], g[0], e);
-        e = mma32x3(q[1], g[1], e);
-      }
+          for (int m = 0; m < 2; ++m) g[m] = Split8{row_frag(stg[yhi].r, t, m, qd), row_frag(ylo, t, m, qd)};
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        const int sgn = (wq & 1) ? -1 : 1;   // keep s > t (B_), s < t (C_)
+        // the wave's orientation (wq is wave-uniform: a scalar branch)
+        f32x4 e = {0.f, 0.f, 0.f, 0.f};
+        if (wq & 1) {
+          e = mma32x3(g[0], q[0], e);
+          e = mma32x3(g[1], q[1], e);
+        } else {
+          e = mma32x3(q[0], g[0], e);
+          e = mma32x3(q[1], g[1], e);
+        }
 #pragma unroll
-      for (int r = 0; r < 4; ++r) e[r] = sgn * (4 * qd + r - t) > 0 ? e[r] : 0.f;
-      L.frag[G_BSAV + wq][lane] = stack_f(e);
+        for (int r = 0; r < 4; ++r) e[r] = sgn * (4 * qd + r - t) > 0 ? e[r] : 0.f;
+        L.frag[G_BSAV + wq][lane] = stack_f(e);
+        if (wq == 1) {   // B_sav for wave 0
+          f32x4 e0 = {0.f, 0.f, 0.f, 0.f};
+          e0 = mma32x3(q[0], g[0], e0);
+          e0 = mma32x3(q[1], g[1], e0);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) e0[r] = (4 * qd + r - t) > 0 ? e0[r] : 0.f;
+          L.frag[G_BSAV][lane] = stack_f(e0);
+        }
+      }
     } else {
       if constexpr (kFull) {
         // the decayed rows first: the staging waits for phase A's global loads

@@ -187,6 +187,9 @@ READOUT_CASES = [
     dict(B=2, T=24, H=3, op="f32", act="f32"),
     dict(B=2, T=16, H=12, op="bf16", act="bf16"),
     dict(B=1, T=70, H=4, op="bf16", act="f32"),
+    # the last 16-lane group of rows holds 1 and 3 rows (groups walk 4)
+    dict(B=3, T=11, H=2, op="f32", act="bf16"),
+    dict(B=1, T=67, H=5, op="bf16", act="bf16"),
     dict(B=16, T=512, H=12, op="bf16", act="bf16"),
 ]
 
