@@ -264,7 +264,7 @@ def neighbor_bytes(cfg):
         "shift_mix_forward_kernel<false, true, 6>": (rc * 4 + 6 * rc * 2, "x fp32 in, 6 bf16 mixes out"),
         "shift_mix_forward_serial_kernel<false, true, 1>": (rc * 4 + rc * 2, "x fp32 in, 1 bf16 mix out"),
         "shift_mix_backward_kernel<false, true, 6>": (6 * rc * 2 + 2 * rc * 4, "6 bf16 mix grads + x in, dx fp32 out"),
-        "shift_mix_backward_kernel<false, true, 1>": (rc * 2 + 2 * rc * 4, "1 bf16 mix grad + x in, dx fp32 out"),
+        "shift_mix_backward_phased_kernel<false, true, 1>": (rc * 2 + 2 * rc * 4, "1 bf16 mix grad + x in, dx fp32 out"),
         "readout_forward_kernel<true, true>": (6 * rc * 2, "y, r, k~, v, gate bf16 in, out bf16"),
         "readout_backward_kernel<true, true>": (11 * rc * 2, "+ dout in; dy, dr, dk~, dv, dgate out"),
         "prepare_forward_kernel<true, true, true>": (11 * rc * 2, "6 bf16 products in, 5 bf16 operands out"),
