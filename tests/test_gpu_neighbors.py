@@ -47,6 +47,13 @@ SHIFT_CASES = [
     dict(B=4, T=1, C=128, K=1, mask=False, shift=True, ids=True, xdt="f32", odt="f32"),
     dict(B=2, T=16, C=128, K=6, mask=True, shift=True, ids=False, xdt="bf16", odt="bf16"),
     dict(B=16, T=512, C=768, K=6, mask=False, shift=False, ids=False, xdt="f32", odt="bf16"),
+    # one mix (its own forward and backward walks) over runs of rows within a
+    # sequence, ragged (T not a multiple of a wave's 8 rows), with masks
+    dict(B=3, T=37, C=192, K=1, mask=True, shift=True, ids=True, xdt="f32", odt="bf16"),
+    dict(B=2, T=29, C=256, K=1, mask=False, shift=False, ids=False, xdt="bf16", odt="bf16"),
+    # seven and eight mixes (the eight-mix instance)
+    dict(B=3, T=21, C=128, K=8, mask=True, shift=False, ids=False, xdt="bf16", odt="f32"),
+    dict(B=2, T=13, C=64, K=7, mask=False, shift=True, ids=False, xdt="f32", odt="f32"),
 ]
 DT = {"f32": torch.float32, "bf16": torch.bfloat16}
 
