@@ -284,6 +284,48 @@ def test_empty_sequence(wk):
     assert torch.equal(g.initial_state_grad, dsT)
 
 
+def test_two_streams_match_one(wk):
+    # The C ABI enqueues on the caller's stream and keeps no state between
+    # calls (include/wkv7.h): two workloads launched alternately on two
+    # streams -- bf16 on the chunked kernels, fp32 on the step kernels --
+    # give each workload's one-stream results bit for bit.
+    announce("two streams")
+    syn = load_pkg().synthetic
+    work = []
+    for seed, dtype in ((31, torch.bfloat16), (32, torch.float32)):
+        d = syn.make_inputs(2, 128, 4, 64, seed=seed, s0_std=0.1)
+        ins = [to_dev(d[n], dtype) for n in NAMES]
+        work.append((ins, to_dev(d["s0"]), to_dev(d["dy"], dtype)))
+
+    def run(ins, s0, dy):
+        f = wk.wkv7_statepass_forward(*ins, s0, 16)
+        g = wk.wkv7_statepass_backward(*ins, f.state, f.removal_state, dy,
+                                       torch.zeros_like(s0), 16)
+        return f, g
+
+    one = [run(*w) for w in work]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    fwd = [None, None]
+    for i, (s, (ins, s0, dy)) in enumerate(zip(streams, work)):
+        with torch.cuda.stream(s):
+            fwd[i] = wk.wkv7_statepass_forward(*ins, s0, 16)
+    two = []
+    for i, (s, (ins, s0, dy)) in enumerate(zip(streams, work)):
+        with torch.cuda.stream(s):
+            f = fwd[i]
+            two.append((f, wk.wkv7_statepass_backward(*ins, f.state, f.removal_state, dy,
+                                                      torch.zeros_like(s0), 16)))
+    torch.cuda.synchronize()
+    for (f1, g1), (f2, g2) in zip(one, two):
+        for name in ("output", "state", "removal_state", "final_state"):
+            assert torch.equal(getattr(f1, name), getattr(f2, name)), name
+        for gn in GRAD_NAMES + ("initial_state_grad",):
+            assert torch.equal(getattr(g1, gn), getattr(g2, gn)), gn
+
+
 def test_autograd_matches_direct_backward(wk):
     announce("autograd")
     d = load_pkg().synthetic.make_inputs(1, 32, 2, 64, seed=23, s0_std=0.1)
