@@ -296,3 +296,36 @@ def test_decode_step_replays_from_a_captured_graph(wk):
         assert torch.equal(y_graph, y_eager), rep
         assert torch.equal(st_graph, st_eager), rep
         assert torch.equal(el_graph, el_eager), rep
+
+
+def test_decode_slots_past_2g_elements(wk, oracle):
+    """A slot buffer past 2^31 elements ([8200, 64, 64, 64] fp32: 2.15e9
+    elements, 8.6 GB): four rows mapped to the first and the last slots, one
+    decode step, against the oracle on those slots; the slots between are
+    untouched."""
+    announce("decode slots past 2^31 elements")
+    pkg = load_pkg()
+    Ba, H, full = 4, 64, 8200
+    assert full * H * 64 * 64 > 2 ** 31
+    d = pkg.synthetic.make_inputs(Ba, 1, H, 64, seed=0x5EED00B2, bf16=True, with_grad=False)
+    ids = np.array([full - 1, 0, full - 2, 1], np.int32)
+    rng = np.random.default_rng(0x5EED00B2)
+    picked = (rng.standard_normal((Ba, H, 64, 64), dtype=np.float32) * np.float32(0.1))
+    st_gpu = torch.zeros(full, H, 64, 64, device="cuda")
+    st_gpu[torch.from_numpy(ids.astype(np.int64)).cuda()] = to_dev(picked)
+    probe = st_gpu[full // 2].clone()
+    elapsed = np.zeros(full, np.int32)
+    out = wk.wkv7_infer_forward(*(to_dev(d[n], torch.bfloat16) for n in NAMES),
+                                torch.from_numpy(ids).cuda(), st_gpu, None,
+                                torch.from_numpy(elapsed).cuda())
+    torch.cuda.synchronize()
+    # the oracle on a buffer of just the four slots, rows mapped in order
+    st_ref = picked.copy()
+    y_ref = oracle.infer_f32(*(d[n] for n in NAMES), np.arange(Ba, dtype=np.int32), st_ref, None,
+                             np.zeros(Ba, np.uint32))
+    err_y = rel_l2(to_np(out.output), pkg.synthetic.bf16_round(y_ref))
+    got = to_np(st_gpu[torch.from_numpy(ids.astype(np.int64)).cuda()])
+    err_s = rel_l2(got, st_ref)
+    print("slots past 2^31", f"y {err_y:.2e} state {err_s:.2e}", flush=True)
+    assert err_y < 1e-2 and err_s < 1e-5
+    assert torch.equal(st_gpu[full // 2], probe)

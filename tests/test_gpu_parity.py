@@ -530,3 +530,50 @@ def test_handover_fault_poisons_outputs_and_is_reported(wk):
     rc = native.lib().wkv7_take_faults(torch.cuda.current_stream().cuda_stream, ctypes.byref(n))
     assert rc == native.WKV7_ERR_HANDOVER and n.value > 0, (rc, n.value)
     assert wk.take_faults() == 0
+
+
+def test_tensors_past_2g_elements(wk, oracle):
+    # Inputs past 2^31 elements each ([136, 4096, 64, 64] bf16: 2.28e9
+    # elements, 4.6 GB; about 110 GB on the device with the checkpoints and
+    # gradients): the first and the last (b, h) pairs -- the last one's
+    # elements lie past 2^31 elements and 2^32 bytes from every tensor's
+    # start -- against the oracle run on that pair alone, at the bf16 bars.
+    announce("tensors past 2^31 elements")
+    pkg = load_pkg()
+    B, T, H = 136, 4096, 64
+    assert B * T * H * 64 > 2 ** 31
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0x5EED00B1)
+
+    def randn(*shape):
+        return torch.randn(*shape, generator=gen, device="cuda")
+
+    x = {n: randn(B, T, H, 64).to(torch.bfloat16) for n in ("w", "r", "k", "v")}
+    kk = torch.nn.functional.normalize(randn(B, T, H, 64), dim=-1)
+    x["a"] = (-kk).to(torch.bfloat16)
+    x["b"] = (kk * torch.sigmoid(randn(B, T, H, 64))).to(torch.bfloat16)
+    del kk
+    dy = randn(B, T, H, 64).to(torch.bfloat16)
+    s0 = randn(B, H, 64, 64) * 0.1
+    ins = [x[n] for n in NAMES]
+    fwd = wk.wkv7_statepass_forward(*ins, s0, 16)
+    bwd = wk.wkv7_statepass_backward(*ins, fwd.state, fwd.removal_state, dy,
+                                     torch.zeros_like(s0), 16)
+    torch.cuda.synchronize()
+    for bi, h in ((0, 0), (B - 1, H - 1)):
+        tok = lambda t: to_np(t[bi:bi + 1, :, h:h + 1])      # [1, T, 1, 64]
+        st = lambda t: to_np(t[bi:bi + 1, h:h + 1])          # [1, 1, ...]
+        pin = [tok(t) for t in ins]
+        of = oracle.forward_f32(*pin, s0=st(s0), chunk_len=16)
+        ob = oracle.backward_f32(*pin, of["state"], of["removal_state"], tok(dy), chunk_len=16)
+        errs = {"output": (rel_l2(tok(fwd.output), pkg.synthetic.bf16_round(of["output"])), BF16_TOL),
+                "removal_state": (rel_l2(tok(fwd.removal_state), of["removal_state"]), BF16_STATE_TOL),
+                "state": (rel_l2(st(fwd.state), of["state"]), BF16_STATE_TOL),
+                "final_state": (rel_l2(st(fwd.final_state), of["final_state"]), BF16_STATE_TOL),
+                "initial_state_grad": (rel_l2(st(bwd.initial_state_grad), ob["initial_state_grad"]),
+                                       BF16_STATE_TOL)}
+        for gn in GRAD_NAMES:
+            errs[gn] = (rel_l2(tok(getattr(bwd, gn)), pkg.synthetic.bf16_round(ob[gn])), BF16_TOL)
+        print("pair", (bi, h), {k: f"{e:.2e}" for k, (e, _) in errs.items()}, flush=True)
+        for k, (e, tol) in errs.items():
+            assert e <= tol, ((bi, h), k, e)
