@@ -532,15 +532,22 @@ def test_handover_fault_poisons_outputs_and_is_reported(wk):
     assert wk.take_faults() == 0
 
 
-def test_tensors_past_2g_elements(wk, oracle):
-    # Inputs past 2^31 elements each ([136, 4096, 64, 64] bf16: 2.28e9
-    # elements, 4.6 GB; about 110 GB on the device with the checkpoints and
-    # gradients): the first and the last (b, h) pairs -- the last one's
-    # elements lie past 2^31 elements and 2^32 bytes from every tensor's
-    # start -- against the oracle run on that pair alone, at the bf16 bars.
-    announce("tensors past 2^31 elements")
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_tensors_past_2g_elements(wk, oracle, dtype):
+    # Inputs past 2^31 elements each: bf16 [136, 4096, 64, 64] on the chunked
+    # kernels (2.28e9 elements, 4.6 GB each; about 110 GB on the device with
+    # the checkpoints and gradients), fp32 [129, 4096, 64, 64] on the step
+    # kernels (2.16e9 elements, 8.7 GB each; about 165 GB). The first and the
+    # last (b, h) pairs -- the last one's elements lie past 2^31 elements and
+    # 2^32 bytes from every tensor's start -- against the oracle run on that
+    # pair alone, at the dtype's bars.
+    announce("tensors past 2^31 elements", dtype)
     pkg = load_pkg()
-    B, T, H = 136, 4096, 64
+    bf16 = dtype == "bf16"
+    B, T, H = (136 if bf16 else 129), 4096, 64
+    dt = torch.bfloat16 if bf16 else torch.float32
+    tok_tol, st_tol = (BF16_TOL, BF16_STATE_TOL) if bf16 else (FP32_TOL, FP32_TOL)
+    rnd_out = pkg.synthetic.bf16_round if bf16 else (lambda a: a)
     assert B * T * H * 64 > 2 ** 31
     gen = torch.Generator(device="cuda")
     gen.manual_seed(0x5EED00B1)
@@ -548,12 +555,12 @@ def test_tensors_past_2g_elements(wk, oracle):
     def randn(*shape):
         return torch.randn(*shape, generator=gen, device="cuda")
 
-    x = {n: randn(B, T, H, 64).to(torch.bfloat16) for n in ("w", "r", "k", "v")}
+    x = {n: randn(B, T, H, 64).to(dt) for n in ("w", "r", "k", "v")}
     kk = torch.nn.functional.normalize(randn(B, T, H, 64), dim=-1)
-    x["a"] = (-kk).to(torch.bfloat16)
-    x["b"] = (kk * torch.sigmoid(randn(B, T, H, 64))).to(torch.bfloat16)
+    x["a"] = (-kk).to(dt)
+    x["b"] = (kk * torch.sigmoid(randn(B, T, H, 64))).to(dt)
     del kk
-    dy = randn(B, T, H, 64).to(torch.bfloat16)
+    dy = randn(B, T, H, 64).to(dt)
     s0 = randn(B, H, 64, 64) * 0.1
     ins = [x[n] for n in NAMES]
     fwd = wk.wkv7_statepass_forward(*ins, s0, 16)
@@ -566,14 +573,14 @@ def test_tensors_past_2g_elements(wk, oracle):
         pin = [tok(t) for t in ins]
         of = oracle.forward_f32(*pin, s0=st(s0), chunk_len=16)
         ob = oracle.backward_f32(*pin, of["state"], of["removal_state"], tok(dy), chunk_len=16)
-        errs = {"output": (rel_l2(tok(fwd.output), pkg.synthetic.bf16_round(of["output"])), BF16_TOL),
-                "removal_state": (rel_l2(tok(fwd.removal_state), of["removal_state"]), BF16_STATE_TOL),
-                "state": (rel_l2(st(fwd.state), of["state"]), BF16_STATE_TOL),
-                "final_state": (rel_l2(st(fwd.final_state), of["final_state"]), BF16_STATE_TOL),
+        errs = {"output": (rel_l2(tok(fwd.output), rnd_out(of["output"])), tok_tol),
+                "removal_state": (rel_l2(tok(fwd.removal_state), of["removal_state"]), st_tol),
+                "state": (rel_l2(st(fwd.state), of["state"]), st_tol),
+                "final_state": (rel_l2(st(fwd.final_state), of["final_state"]), st_tol),
                 "initial_state_grad": (rel_l2(st(bwd.initial_state_grad), ob["initial_state_grad"]),
-                                       BF16_STATE_TOL)}
+                                       st_tol)}
         for gn in GRAD_NAMES:
-            errs[gn] = (rel_l2(tok(getattr(bwd, gn)), pkg.synthetic.bf16_round(ob[gn])), BF16_TOL)
-        print("pair", (bi, h), {k: f"{e:.2e}" for k, (e, _) in errs.items()}, flush=True)
+            errs[gn] = (rel_l2(tok(getattr(bwd, gn)), rnd_out(ob[gn])), tok_tol)
+        print(dtype, "pair", (bi, h), {k: f"{e:.2e}" for k, (e, _) in errs.items()}, flush=True)
         for k, (e, tol) in errs.items():
             assert e <= tol, ((bi, h), k, e)
