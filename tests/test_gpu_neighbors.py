@@ -392,3 +392,75 @@ def test_parameter_gradients_are_bitwise_repeatable():
     first, second = run(), run()
     for i, (a, b) in enumerate(zip(first, second)):
         assert torch.equal(a, b), i
+
+
+def test_token_shift_past_2g_elements():
+    # x [2048, 2048, 768] fp32 (3.2e9 elements, 12.9 GB), one mix in bf16:
+    # mixes and dx of the first and last rows against float64 on the CPU
+    # (mix_t = x_t + (x_{t-1} - x_t) s, dx_t = g_t (1 - s) + g_{t+1} s), and
+    # the scale gradient sum_t g_t (x_{t-1} - x_t) against float64 sums.
+    nb = _nb()
+    B, T, C = 2048, 2048, 768
+    assert B * T * C > 2 ** 31
+    announce("token_shift past 2^31 elements", (B, T, C))
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0x5EED00B3)
+    x = torch.randn(B, T, C, generator=gen, device="cuda").requires_grad_(True)
+    s = (0.5 * torch.rand(C, generator=gen, device="cuda")).requires_grad_(True)
+    g = torch.randn(B, T, C, generator=gen, device="cuda").to(torch.bfloat16)
+    (mix,) = nb.token_shift_mix(x, [s], out_dtype=torch.bfloat16)
+    mix.backward(g)
+    torch.cuda.synchronize()
+    s64 = s.detach().double().cpu()
+    for b in (0, B - 1):
+        xs = x.detach()[b].double().cpu()          # one sequence: [T, C]
+        gs = g[b].double().cpu()
+        prev = torch.cat([torch.zeros(1, C, dtype=torch.float64), xs[:-1]])
+        want_mix = xs + (prev - xs) * s64
+        nxt = torch.cat([gs[1:], torch.zeros(1, C, dtype=torch.float64)])
+        want_dx = gs * (1 - s64) + nxt * s64
+        assert _err(mix[b], want_mix) <= BF16_TOL, ("mix", b)
+        assert _err(x.grad[b], want_dx) <= F32_TOL, ("dx", b)
+    # the scale gradient over all rows, summed in float64 a batch slice at a time
+    want_ds = torch.zeros(C, dtype=torch.float64, device="cuda")
+    for b0 in range(0, B, 256):
+        xb = x.detach()[b0:b0 + 256].double()
+        prev = torch.cat([torch.zeros_like(xb[:, :1]), xb[:, :-1]], 1)
+        want_ds += (g[b0:b0 + 256].double() * (prev - xb)).sum(dim=(0, 1))
+    assert _err(s.grad, want_ds) <= F32_TOL
+
+
+def test_gated_readout_past_2g_elements():
+    # y, r, k, v [2048, 2048, 12, 64] bf16 (3.2e9 elements each, 6.4 GB): the
+    # output and the operand gradients of the first and last rows against
+    # float64 GroupNorm + bonus + gate on the CPU.
+    nb = _nb()
+    B, T, H = 2048, 2048, 12
+    C = H * 64
+    assert B * T * C > 2 ** 31
+    announce("gated_readout past 2^31 elements", (B, T, H))
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0x5EED00B4)
+    bf = torch.bfloat16
+    y, r, k, v = (torch.randn(B, T, H, 64, generator=gen, device="cuda").to(bf).requires_grad_(True)
+                  for _ in range(4))
+    gate = torch.rand(B, T, C, generator=gen, device="cuda").to(bf).requires_grad_(True)
+    bonus = (0.1 * torch.randn(H, 64, generator=gen, device="cuda")).requires_grad_(True)
+    w = (1.0 + 0.1 * torch.randn(C, generator=gen, device="cuda")).requires_grad_(True)
+    bias = (0.1 * torch.randn(C, generator=gen, device="cuda")).requires_grad_(True)
+    dout = torch.randn(B, T, C, generator=gen, device="cuda").to(bf)
+    out = nb.gated_readout(y, r, k, v, gate, bonus, w, bias, eps=64e-5)
+    out.backward(dout)
+    torch.cuda.synchronize()
+    for b, t0 in ((0, 0), (B - 1, T - 4)):
+        sl = lambda z: z.detach()[b, t0:t0 + 4].double().cpu().requires_grad_(True)
+        y4, r4, k4, v4, g4 = sl(y), sl(r), sl(k), sl(v), sl(gate)
+        bo, w64, b64 = (z.detach().double().cpu() for z in (bonus, w, bias))
+        yn = F.group_norm(y4.reshape(4, C), H, w64, b64, 64e-5).reshape(4, C)
+        bon = ((r4 * k4 * bo).sum(-1, keepdim=True) * v4).reshape(4, C)
+        want = (yn + bon) * g4
+        (want * dout[b, t0:t0 + 4].double().cpu()).sum().backward()
+        assert _err(out[b, t0:t0 + 4], want) <= BF16_TOL, ("out", b)
+        for name, got, ref in (("y", y, y4), ("r", r, r4), ("k", k, k4), ("v", v, v4),
+                               ("gate", gate, g4)):
+            assert _err(got.grad[b, t0:t0 + 4], ref.grad) <= BF16_TOL, (name, b)
