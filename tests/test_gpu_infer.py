@@ -329,3 +329,5 @@ def test_decode_slots_past_2g_elements(wk, oracle):
     print("slots past 2^31", f"y {err_y:.2e} state {err_s:.2e}", flush=True)
     assert err_y < 1e-2 and err_s < 1e-5
     assert torch.equal(st_gpu[full // 2], probe)
+    del st_gpu, out
+    torch.cuda.empty_cache()

@@ -428,6 +428,8 @@ def test_token_shift_past_2g_elements():
         prev = torch.cat([torch.zeros_like(xb[:, :1]), xb[:, :-1]], 1)
         want_ds += (g[b0:b0 + 256].double() * (prev - xb)).sum(dim=(0, 1))
     assert _err(s.grad, want_ds) <= F32_TOL
+    del x, g, mix, xb, prev
+    torch.cuda.empty_cache()
 
 
 def test_gated_readout_past_2g_elements():
@@ -464,3 +466,5 @@ def test_gated_readout_past_2g_elements():
         for name, got, ref in (("y", y, y4), ("r", r, r4), ("k", k, k4), ("v", v, v4),
                                ("gate", gate, g4)):
             assert _err(got.grad[b, t0:t0 + 4], ref.grad) <= BF16_TOL, (name, b)
+    del y, r, k, v, gate, dout, out
+    torch.cuda.empty_cache()

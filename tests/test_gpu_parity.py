@@ -584,3 +584,6 @@ def test_tensors_past_2g_elements(wk, oracle, dtype):
         print(dtype, "pair", (bi, h), {k: f"{e:.2e}" for k, (e, _) in errs.items()}, flush=True)
         for k, (e, tol) in errs.items():
             assert e <= tol, ((bi, h), k, e)
+    # give the device memory back to the tests that follow in this process
+    del x, ins, dy, s0, fwd, bwd
+    torch.cuda.empty_cache()
