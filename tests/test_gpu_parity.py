@@ -326,6 +326,43 @@ def test_two_streams_match_one(wk):
             assert torch.equal(getattr(g1, gn), getattr(g2, gn)), gn
 
 
+def test_graph_replays_match_eager(wk):
+    # The forward and backward launch kernels only (no memsets, copies or
+    # allocations inside the library), so a caller can capture them in a HIP
+    # graph: each of several replays, with eager work between them, gives
+    # the eager results bit for bit (bf16 operands: the chunked kernels).
+    announce("graph replay")
+    d = load_pkg().synthetic.make_inputs(2, 128, 4, 64, seed=41, s0_std=0.1, bf16=True)
+    ins = [to_dev(d[n], torch.bfloat16) for n in NAMES]
+    s0, dy = to_dev(d["s0"]), to_dev(d["dy"], torch.bfloat16)
+    zero = torch.zeros_like(s0)
+
+    def run():
+        f = wk.wkv7_statepass_forward(*ins, s0, 16)
+        return f, wk.wkv7_statepass_backward(*ins, f.state, f.removal_state, dy, zero, 16)
+
+    ef, eg = run()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run()                                  # warm-up off the capture
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        gf, gg = run()
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        for name in ("output", "state", "removal_state", "final_state"):
+            assert torch.equal(getattr(gf, name), getattr(ef, name)), name
+        for gn in GRAD_NAMES + ("initial_state_grad",):
+            assert torch.equal(getattr(gg, gn), getattr(eg, gn)), gn
+        run()                                  # eager work between replays
+        torch.cuda.synchronize()
+
+
 def test_autograd_matches_direct_backward(wk):
     announce("autograd")
     d = load_pkg().synthetic.make_inputs(1, 32, 2, 64, seed=23, s0_std=0.1)
