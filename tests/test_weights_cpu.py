@@ -2,17 +2,22 @@
 mirror of examples/rwkv-lm/src/pth2bpk.rs.
 
 No release checkpoint ships with the reference and there is no network, so
-the checkpoint here is synthetic: the release format's key names and shapes
-(written out literally below, not taken from the loader's table), filled
-with distinct random values, so that every tensor can be traced to the
-parameter it lands in."""
+the checkpoint here is synthetic (``model_helpers.release_checkpoint``): the
+release format's key names and shapes, written out there and not taken from
+the loader's table, filled with distinct random values, so that every tensor
+can be traced to the parameter it lands in. Where tensors are traced only by
+identity, a key mapped to the wrong one of two same-shaped parameters would
+still pass; ``test_loaded_model_computes_the_release_forward`` closes that by
+comparing the loaded model's logits with a float64 forward that reads the
+checkpoint by its release key names (``model_helpers.release_forward_f64``)."""
 
 import importlib
 
 import pytest
 import torch
 
-from model_helpers import _model_mod
+from model_helpers import TorchKernel, _model_mod, model_logits, release_checkpoint as _release
+from model_helpers import release_forward_f64
 
 
 def _w():
@@ -24,36 +29,13 @@ L, C, H, V = 2, 128, 2, 97
 RW, RA, RV, RG = 32, 32, 32, 64
 
 
-def release_checkpoint(seed=0, dtype=torch.bfloat16):
-    g = torch.Generator().manual_seed(seed)
-
-    def t(*shape):
-        return torch.randn(*shape, generator=g).to(dtype)
-
-    sd = {"emb.weight": t(V, C), "blocks.0.ln0.weight": t(C), "blocks.0.ln0.bias": t(C),
-          "ln_out.weight": t(C), "ln_out.bias": t(C), "head.weight": t(V, C)}
-    for i in range(L):
-        b = f"blocks.{i}."
-        for n in ("ln1", "ln2", "att.ln_x"):
-            sd[b + n + ".weight"] = t(C)
-            sd[b + n + ".bias"] = t(C)
-        for n in ("x_r", "x_w", "x_k", "x_v", "x_a", "x_g", "k_k", "k_a", "w0", "a0", "v0"):
-            sd[b + "att." + n] = t(1, 1, C)
-        sd[b + "att.r_k"] = t(H, 64)
-        sd[b + "att.w1"], sd[b + "att.w2"] = t(C, RW), t(RW, C)
-        sd[b + "att.a1"], sd[b + "att.a2"] = t(C, RA), t(RA, C)
-        sd[b + "att.v1"], sd[b + "att.v2"] = t(C, RV), t(RV, C)
-        sd[b + "att.g1"], sd[b + "att.g2"] = t(C, RG), t(RG, C)
-        for n in ("receptance", "key", "value", "output"):
-            sd[b + f"att.{n}.weight"] = t(C, C)
-        sd[b + "ffn.x_k"] = t(1, 1, C)
-        sd[b + "ffn.key.weight"] = t(4 * C, C)
-        sd[b + "ffn.value.weight"] = t(C, 4 * C)
-    return sd
+def release_checkpoint(seed=0, dtype=torch.bfloat16, scaled=False):
+    return _release(L, C, H, V, (RW, RA, RV, RG), seed, dtype, scaled)
 
 
-def tiny():
-    return _model_mod().AutoRegressiveModel(V, L, C, H, 64, neighbor_ops="torch")
+def tiny(wkv7_dtype=torch.bfloat16):
+    return _model_mod().AutoRegressiveModel(V, L, C, H, 64, wkv7_dtype=wkv7_dtype,
+                                            neighbor_ops="torch")
 
 
 CELL0_VALUE_RESIDUAL = {"blocks.0.att.v0", "blocks.0.att.v1", "blocks.0.att.v2"}
@@ -166,3 +148,41 @@ def test_release_lora_shapes_of_the_0_1b_model():
     assert tuple(tm.weight_prepare.param_value_residual_lora.w_a.shape) == (768, 32)
     assert tuple(tm.gated_readout.param_output_gate_lora.w_a.shape) == (768, 128)
     assert tuple(model.unembed.weight.shape) == (65536, 768)
+
+
+def _logits_cpu(model, tokens):
+    with torch.no_grad():
+        return model_logits(model, tokens, TorchKernel).double()
+
+
+def _rel(a, b):
+    return float((a - b).norm() / b.norm())
+
+
+def test_loaded_model_computes_the_release_forward():
+    """The loaded model (torch neighbour ops, the float64 recurrence as the
+    operator, fp32 weights) gives the logits of the release-key forward; the
+    same model loaded from a checkpoint with two same-shaped LoRA factors
+    swapped, or a square projection transposed, does not (a planted mapping
+    mistake moves the logits by far more than the bar)."""
+    w = _w()
+    sd = release_checkpoint(seed=5, dtype=torch.float32, scaled=True)
+    g = torch.Generator().manual_seed(9)
+    toks = torch.randint(0, V, (2, 24), generator=g)
+    want = release_forward_f64(sd, toks, H)
+    model = tiny(torch.float32)
+    w.load_pth(model, sd)
+    err = _rel(_logits_cpu(model, toks), want)
+    assert err <= 1e-5, err
+    planted = {
+        "lora factors swapped": dict(sd, **{"blocks.1.att.w1": sd["blocks.1.att.a1"],
+                                            "blocks.1.att.a1": sd["blocks.1.att.w1"]}),
+        "projection transposed": dict(sd, **{"blocks.0.att.key.weight":
+                                             sd["blocks.0.att.key.weight"].T.contiguous()}),
+        "mixes swapped": dict(sd, **{"blocks.0.att.x_r": sd["blocks.0.att.x_g"],
+                                     "blocks.0.att.x_g": sd["blocks.0.att.x_r"]}),
+    }
+    for label, bad in planted.items():
+        m = tiny(torch.float32)
+        w.load_pth(m, bad)
+        assert _rel(_logits_cpu(m, toks), want) > 1e-2, label
