@@ -410,6 +410,8 @@ def bench_train(cfg, steps, warmup, with_cpu, probe=False, kernels="auto"):
         e2.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    # outside the timed region: no chunked forward gave up a hand-over wait
+    importlib.import_module("rwkv-rs_amd.wkv7").check_faults(dev)
     fwd_each = sorted(a.elapsed_time(b) for a, b, _ in ev)
     bwd_each = sorted(b.elapsed_time(c) for _, b, c in ev)
     fwd_ms = sum(fwd_each) / steps          # mean launch time, as rocprofv3's average
@@ -714,6 +716,7 @@ def bench_lm(cfg, steps, warmup, neighbor_ops="hip"):
     e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    wkv7.check_faults(dev)
     step_ms = e0.elapsed_time(e1) / steps
     fwd_ms = sum(a.elapsed_time(b) for n, a, b in log if n == "forward") / steps
     bwd_ms = sum(a.elapsed_time(b) for n, a, b in log if n == "backward") / steps

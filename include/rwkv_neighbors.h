@@ -147,8 +147,11 @@ int rwkv_gated_readout_backward(const void *wkv7_output, const void *receptance,
  * call on one GPU shares that GPU's array: calls that overlap in time on one
  * GPU (different streams without ordering between them) race and give wrong
  * parameter gradients; order them. The array's device address is looked up
- * on the first call per device, with that device current. Outputs equal
- * rwkv_gated_readout_backward's bit for bit. */
+ * on the first call per device, with that device current (that call may be
+ * under graph capture), and kept for the life of the process: after a
+ * hipDeviceReset of a device this entry point must not be called on it
+ * again in the same process. Outputs equal rwkv_gated_readout_backward's
+ * bit for bit. */
 int rwkv_gated_readout_backward_noalloc(const void *wkv7_output, const void *receptance,
                                         const void *replacement_key, const void *value,
                                         const void *gate, const float *receptance_key_bonus,

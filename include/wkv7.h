@@ -29,9 +29,23 @@
  *
  * dtype (WKV7_DTYPE_*) is the element type of the per-token tensors and of
  * output / the six input gradients. State-family tensors (initial and final
- * state, checkpoints, removal_state, their gradients) are always fp32 and all
- * arithmetic is fp32, as in the reference, which casts non-fp32 inputs to fp32
- * and the outputs back (wkv7_common/host.rs:45-64, 204-229).
+ * state, checkpoints, removal_state, their gradients) are always fp32.
+ *
+ * Arithmetic. The reference casts non-fp32 inputs to fp32, computes in fp32
+ * and casts the outputs back (wkv7_common/host.rs:45-64, 204-229). Here the
+ * arithmetic depends on the kernel family a call runs on (WKV7_KERNELS_AUTO):
+ *   - bf16 operands, forward at chunk_len 16, backward at chunk_len a multiple
+ *     of 16 (the chunked matrix-core kernels): state, checkpoints,
+ *     removal_state and every sum are fp32, but each product of two fp32
+ *     quantities is formed from their bf16 halves as hi*hi + hi*lo + lo*hi,
+ *     about 16 significant bits where fp32 has 24. Measured against the
+ *     reference-order fp32 result: the state family about 3e-6 relative L2,
+ *     the bf16 outputs and gradients at their own bf16 rounding (1e-4 to 7e-4);
+ *   - fp32 operands, and bf16 operands at every other chunk_len (the forward
+ *     at chunk_len > 16 included): the step kernels, fp32 products and sums,
+ *     about 1e-7 from the reference-order fp32 result.
+ * wkv7_forward_ex / wkv7_backward_ex with WKV7_KERNELS_STEP run the step
+ * kernels, i.e. fp32 products, for bf16 operands too.
  *
  * Ownership and threading: the caller allocates every buffer on the device
  * (use wkv7_checkpoint_numel for the checkpoint tensor); the library
@@ -142,8 +156,10 @@ int wkv7_backward(const void *weight_decay, const void *receptance,
  * Explicit kernel choice. No counterpart in the reference (whose backend picks
  * one kernel per element type). wkv7_forward / wkv7_backward and the trait
  * entry points use WKV7_KERNELS_AUTO: the chunked matrix-core kernels for
- * bf16 operands with chunk_len 16 (T a multiple of 16), the step-by-step fp32
- * kernels otherwise. WKV7_KERNELS_STEP runs the step kernels for every case
+ * bf16 operands (forward at chunk_len 16, backward at chunk_len a multiple of
+ * 16), the step-by-step fp32 kernels otherwise; the arithmetic of each family
+ * is described at the top of this file. WKV7_KERNELS_STEP runs the step
+ * kernels for every case
  * (to compare the two families on one input). handover_spin_limit bounds the
  * polls of each hand-over wait inside the chunked forward (0 = the default,
  * about 0.1 s); it exists so that tests can force the fault path below.
@@ -188,6 +204,22 @@ int wkv7_backward_ex(const void *weight_decay, const void *receptance,
  * resets the counter, and returns WKV7_ERR_HANDOVER if *count > 0 (WKV7_OK
  * otherwise). Calls on one device must not overlap. */
 int wkv7_take_faults(void *stream, uint32_t *count);
+
+/* Device self-test of two bf16 building blocks, run exactly as the kernels
+ * run them. No counterpart in the reference; it exists so that a toolchain
+ * change that alters their lowering fails a test instead of shifting results
+ * silently. For i < n, from the fp32 pairs (a[i], b[i]):
+ *   split[2i], split[2i+1]: the packed bf16 hi parts (RNE(a), RNE(b); a in
+ *     the low half) and lo parts (RNE(a - hi), RNE(b - hi)) with which the
+ *     chunked kernels form their products of two fp32 quantities;
+ *   sum[i]: RNE(a) + RNE(b) as an fp32 value, the sum the bf16-state decode
+ *     rounds to bf16 (its bf16 rounding is that of the fp32 addition; the
+ *     fp32 value can be one ulp off when one addend is below 2^-16 of the
+ *     other).
+ * Subnormal results are kept. Enqueued on `stream`; device pointers,
+ * 4-byte aligned. */
+int wkv7_selftest_bf16_ops(const float *a, const float *b, int64_t n,
+                           uint32_t *split, float *sum, void *stream);
 
 /* Wkv7PretrainBackend (wkv7_pretrain/mod.rs:18-41; CubeBackend impl
  * wkv7_pretrain/forward.rs:13-85): no initial state, no final state. */

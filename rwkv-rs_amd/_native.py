@@ -44,7 +44,7 @@ EXPORTS = (
     "wkv7_pretrain_forward", "wkv7_pretrain_backward",
     "wkv7_statepass_forward", "wkv7_statepass_backward",
     "wkv7_statetune_forward", "wkv7_statetune_backward",
-    "wkv7_infer_forward",
+    "wkv7_infer_forward", "wkv7_selftest_bf16_ops",
     "rwkv_token_shift_mix_workspace_bytes", "rwkv_token_shift_mix_forward",
     "rwkv_token_shift_mix_backward", "rwkv_gated_readout_workspace_bytes",
     "rwkv_gated_readout_forward", "rwkv_gated_readout_backward",
@@ -75,6 +75,7 @@ _SIGNATURES = {
     "wkv7_statetune_forward": ([_P] * 7 + [_I64] * 5 + [_INT] + [_P] * 4, _INT),
     "wkv7_statetune_backward": ([_P] * 9 + [_I64] * 5 + [_INT] + [_P] * 8, _INT),
     "wkv7_infer_forward": ([_P] * 10 + [_I64] * 5 + [_INT] * 3 + [_P] * 2, _INT),
+    "wkv7_selftest_bf16_ops": ([_P, _P, _I64, _P, _P, _P], _INT),
     "rwkv_token_shift_mix_workspace_bytes": ([_I64] * 4, _I64),
     "rwkv_token_shift_mix_forward": ([_P] * 5 + [_I64] * 5 + [_INT] * 2 + [_P] * 4, _INT),
     "rwkv_token_shift_mix_backward": ([_P] * 5 + [_I64] * 5 + [_INT] * 2 + [_P] * 6 + [_I64, _P],

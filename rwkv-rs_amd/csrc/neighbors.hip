@@ -1242,7 +1242,9 @@ hipError_t launch_prepare_backward(const PrepareArgs& a, hipStream_t s) {
 // of `scratch` at its own address for the life of the process. In host code
 // the name `scratch` is only a host-side stand-in, so it is never passed to a
 // kernel: the device address is looked up once per device with
-// hipGetSymbolAddress and kept in scratch_ptr[device].
+// hipGetSymbolAddress and kept in scratch_ptr[device] for the life of the
+// process. A hipDeviceReset would leave that address stale, so the noalloc
+// entry point is not for processes that reset a device they called it on.
 namespace {
 
 static __device__ __align__(256) float scratch[kReadoutScratchBytes / sizeof(float)];

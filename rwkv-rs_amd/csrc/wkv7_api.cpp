@@ -108,6 +108,20 @@ extern "C" {
 
 int wkv7_abi_version(void) { return WKV7_ABI_VERSION; }
 
+int wkv7_selftest_bf16_ops(const float* a, const float* b, int64_t n, uint32_t* split,
+                           float* sum, void* stream) {
+  if (n < 0 || n > (int64_t)INT32_MAX * 256) return WKV7_ERR_SHAPE;
+  if (n == 0) return WKV7_OK;
+  if (!a || !b || !split || !sum) return WKV7_ERR_NULL_POINTER;
+  if (!aligned(a, 4) || !aligned(b, 4) || !aligned(split, 4) || !aligned(sum, 4))
+    return WKV7_ERR_ALIGNMENT;
+  const std::vector<Range> ins = {{a, n * 4}, {b, n * 4}};
+  const std::vector<Range> outs = {{split, n * 8}, {sum, n * 4}};
+  if (any_overlap(outs, ins)) return WKV7_ERR_OVERLAP;
+  return hip_status(
+      wkv7::launch_bf16_ops_selftest(a, b, n, split, sum, static_cast<hipStream_t>(stream)));
+}
+
 int wkv7_last_hip_error(void) { return g_last_hip_error; }
 
 int wkv7_take_faults(void* stream, uint32_t* count) {

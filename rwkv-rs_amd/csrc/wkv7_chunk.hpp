@@ -77,9 +77,9 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 // two values to bf16 hi and lo parts, one packed conversion each. The
 // residual x - hi comes from one bf16 dot product per value, x + hi_pair .
 // (-1, -0), instead of widening hi and subtracting (two instructions). x - hi
-// is exact in fp32, so this matches the subtraction bit for bit (measured on
-// 2^24 random fp32 values) except where |x| rounds to infinity in bf16 or the
-// residual is below fp32's smallest normal (flushed: an error below 2^-126).
+// is exact in fp32, so any rounding of the dot product gives it, and the
+// split matches the subtraction bit for bit, subnormal residuals included,
+// except where |x| rounds to infinity in bf16 (tests/test_gpu_selftest.py).
 // The constants hold -0 rather than 0: this toolchain encodes (-1, 0) as the
 // inline constant -1.0, which the instruction reads as another 16-bit value
 // (measured: products of about hi / 128), while (-1, -0) stays a literal.

@@ -259,4 +259,33 @@ __device__ __forceinline__ void fwd_step(float* So, float* St, float4 w4, float4
   yp_t = yt;
 }
 
+// ------------------------------------------------------ bf16 arithmetic
+// one bf16 operation: an fp32 result of bf16 operands rounded to bf16 (ties
+// to even). Products of two bf16 values are exact in fp32, and a sum rounded
+// to fp32 and then to bf16 equals the sum rounded once (fp32 carries more
+// than twice bf16's significand bits plus two).
+__device__ __forceinline__ float rb(float x) { return (float)(__bf16)x; }
+
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+// rb(x) + rb(p) as an fp32 sum: both roundings in one packed conversion, the
+// sum of the two bf16 halves by a bf16 dot product with (1, 1). Three
+// instructions where rounding both operands and adding takes five (the
+// conversion, the zeroed accumulator and the dot product against two
+// conversions, two widenings and the addition). Every caller rounds the
+// result to bf16 (rb, or the next add_rb), and that rounding equals the
+// rounding of the IEEE fp32 addition of the two halves. The fp32 sum itself
+// is not always IEEE's: measured, when one addend is below 2^-16 of the
+// other it can be one fp32 ulp off. That cannot move the bf16 rounding:
+// with e the sum's exponent, a bf16 midpoint is then at least
+// 2^(e-8) - 2^(e-15) from the exact sum, and for every other pair the sum
+// and the midpoints lie on the 2^(e-23) grid. Subnormal results are kept;
+// (-0) + (-0) gives +0 (the +0 accumulator). tests/test_gpu_selftest.py
+// holds these facts on the device.
+__device__ __forceinline__ float add_rb(float x, float p) {
+  const bf16x2_t h = __builtin_convertvector(f32x2_t{x, p}, bf16x2_t);
+  return __builtin_amdgcn_fdot2_f32_bf16(h, bf16x2_t{(__bf16)1.0f, (__bf16)1.0f}, 0.0f, false);
+}
+
+
 }  // namespace wkv7

@@ -204,29 +204,6 @@ struct InferBf16Params {
   int T, H, full_batch, use_dither;
 };
 
-// one bf16 operation: an fp32 result of bf16 operands rounded to bf16 (ties
-// to even). Products of two bf16 values are exact in fp32, and a sum rounded
-// to fp32 and then to bf16 equals the sum rounded once (fp32 carries more
-// than twice bf16's significand bits plus two).
-__device__ __forceinline__ float rb(float x) { return (float)(__bf16)x; }
-
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-// rb(x) + rb(p) as an fp32 sum: both roundings in one packed conversion, the
-// sum of the two bf16 halves by a bf16 dot product with (1, 1). The two
-// halves are bf16 values, so the dot product's fp32 result is their sum
-// rounded once to fp32, as an fp32 addition of the two would give it, and
-// the bf16 rounding that follows (rb, or the next add_rb) sees the same
-// value. Three instructions where rounding both operands and adding takes
-// five (the conversion, the zeroed accumulator and the dot product against
-// two conversions, two widenings and the addition). The dot product flushes
-// fp32 results below 2^-126 (about 1.2e-38) to zero, where the addition
-// would keep them: the two differ only for sums of that size.
-__device__ __forceinline__ float add_rb(float x, float p) {
-  const bf16x2_t h = __builtin_convertvector(f32x2_t{x, p}, bf16x2_t);
-  return __builtin_amdgcn_fdot2_f32_bf16(h, bf16x2_t{(__bf16)1.0f, (__bf16)1.0f}, 0.0f, false);
-}
-
 __device__ __forceinline__ float bf_lo(uint32_t u) { return __uint_as_float(u << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
 

@@ -78,6 +78,11 @@ hipError_t launch_backward_chunked(const BackwardDesc& d, hipStream_t stream);
 hipError_t launch_backward(const BackwardDesc& d, hipStream_t stream);
 hipError_t launch_infer(const InferDesc& d, hipStream_t stream);
 
+// Device self-test of the bf16 split and rounded sum (wkv7_selftest.hip);
+// n <= 2^31 * 256 pairs, pointers checked by the ABI layer.
+hipError_t launch_bf16_ops_selftest(const float* a, const float* b, int64_t n, uint32_t* split,
+                                    float* sum, hipStream_t stream);
+
 // WKV7_OK for hipSuccess; otherwise records e for wkv7_last_hip_error() on
 // the calling thread and returns WKV7_ERR_HIP
 int hip_status(hipError_t e);

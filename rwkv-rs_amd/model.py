@@ -572,17 +572,30 @@ class AutoRegressiveModel(nn.Module):
                     p.normal_(0.0, std, generator=generator)
         return self
 
-    def new_infer_state(self, full_batch_size: int, device=None) -> "InferState":
-        """Zeroed per-slot buffers for ``full_batch_size`` slots."""
+    def new_infer_state(self, full_batch_size: int, device=None,
+                        state_dtype: Optional[torch.dtype] = None) -> "InferState":
+        """Zeroed per-slot buffers for ``full_batch_size`` slots.
+
+        By default the WKV7 state has the operator's element type, as the
+        reference keeps it in its backend's float type
+        (wkv7_infer/kernel.rs:35-42): a bfloat16 model decodes with the
+        reference's bf16 arithmetic and its dither. ``state_dtype=
+        torch.float32`` keeps a bfloat16 model's states in fp32 instead: the
+        decode then runs the reference's f32 kernel on the bf16 operands
+        (exact fp32 values), without the dither, as the training path's fp32
+        state does."""
         device = device if device is not None else self.embed.weight.device
         C = self.embed.weight.shape[1]
         H = self.cells.cells[0].time_mixer.num_heads
         N = self.cells.cells[0].time_mixer.head_size
         n = len(self.cells.cells)
-
-        # the WKV7 state has the operator's element type, as the reference
-        # keeps it in its backend's float type (wkv7_infer/kernel.rs:35-42)
-        state_dtype = self.cells.cells[0].time_mixer.wkv7_dtype
+        op_dtype = self.cells.cells[0].time_mixer.wkv7_dtype
+        if state_dtype is None:
+            state_dtype = op_dtype
+        if state_dtype not in (torch.float32, torch.bfloat16):
+            raise ValueError("state_dtype must be torch.float32 or torch.bfloat16")
+        if state_dtype == torch.bfloat16 and op_dtype != torch.bfloat16:
+            raise ValueError("a bfloat16 state needs the model's bfloat16 operator")
 
         def z(*shape, dtype=torch.float32):
             return torch.zeros(*shape, dtype=dtype, device=device)
@@ -688,13 +701,19 @@ def make_optimizer(model: nn.Module, lr: float = 6e-4, weight_decay: float = 0.1
 
 
 def train_step(model: AutoRegressiveModel, optimizer, inputs, targets, kernel=None,
-               autocast: bool = True) -> torch.Tensor:
+               autocast: bool = True, check_faults: bool = False) -> torch.Tensor:
     """One pretrain step: forward, loss, backward, optimizer update
-    (model.rs:316-324). Returns the detached loss."""
+    (model.rs:316-324). Returns the detached loss. With ``check_faults`` the
+    step ends by waiting for the device and raising ``Wkv7Error`` if a
+    chunked forward of the step gave up a hand-over wait (its outputs, and so
+    the loss, are then NaN); without it the step stays asynchronous and the
+    caller polls ``wkv7.check_faults`` where it synchronises anyway."""
     device_type = inputs.device.type
     with torch.autocast(device_type, dtype=torch.bfloat16, enabled=autocast):
         loss = model(inputs, targets, kernel)
     loss.backward()
     optimizer.step()
     optimizer.zero_grad(set_to_none=True)
+    if check_faults and inputs.is_cuda:
+        _wkv7.check_faults(inputs.device)
     return loss.detach()

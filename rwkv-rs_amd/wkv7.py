@@ -263,10 +263,10 @@ def wkv7_backward_ex(weight_decay, receptance, key, value, removal, replacement,
 
 
 def take_faults(device=None) -> int:
-    """wkv7_take_faults: waits for the current stream and returns the number of
-    chunked-forward launches on the device that gave up a hand-over wait since
-    the last call (their outputs are NaN); raises Wkv7Error
-    (WKV7_ERR_HANDOVER) when there were any."""
+    """wkv7_take_faults: waits for the current stream, resets the device's
+    counter and returns the number of chunked-forward launches on the device
+    that gave up a hand-over wait since the last call (their outputs are NaN).
+    Other failures of the call raise Wkv7Error."""
     import ctypes
     dev = torch.device("cuda", torch.cuda.current_device()) if device is None else device
     n = ctypes.c_uint32(0)
@@ -274,6 +274,19 @@ def take_faults(device=None) -> int:
     if status not in (_native.WKV7_OK, _native.WKV7_ERR_HANDOVER):
         _native.check(status)
     return int(n.value)
+
+
+def check_faults(device=None) -> None:
+    """Raises Wkv7Error (WKV7_ERR_HANDOVER) when a chunked forward on the
+    device gave up a hand-over wait since the last take_faults/check_faults,
+    i.e. when some of the outputs computed since then are NaN by that cause.
+    Waits for the current stream: call it where the caller synchronises
+    anyway (the end of a step, a logged loss), not inside a captured graph."""
+    n = take_faults(device)
+    if n:
+        raise _native.Wkv7Error(_native.WKV7_ERR_HANDOVER,
+                                f"{_native.lib().wkv7_strerror(_native.WKV7_ERR_HANDOVER).decode()}"
+                                f" ({n} (batch, head) pairs)")
 
 
 # ------------------------------------------------- Wkv7PretrainBackend (mirror)

@@ -33,7 +33,7 @@ def declared_functions(header=HEADER, prefix="wkv7_"):
 
 def test_header_declares_expected_entry_points():
     names = declared_functions()
-    assert len(names) == 16, names
+    assert len(names) == 17, names
     assert len(declared_functions(NEIGHBORS_HEADER, "rwkv_")) == 10
     assert len(declared_functions(LOSS_HEADER, "rwkv_")) == 2
 
@@ -187,3 +187,14 @@ def test_sizes_whose_byte_counts_overflow_are_refused(native):
     inf = lib.wkv7_infer_forward(*([FAKE] * 6), FAKE * 10, FAKE * 20, None, None, 65535, big_t,
                                  65535, 64, 65535, 1, 0, 0, FAKE * 30, None)
     assert inf == 2
+
+
+def test_selftest_argument_checks(native):
+    # refused on the host before any HIP call
+    lib = native.lib()
+    F = 0x10000
+    assert lib.wkv7_selftest_bf16_ops(F, F, -1, F, F, None) == 2          # shape
+    assert lib.wkv7_selftest_bf16_ops(F, F, 0, None, None, None) == 0      # nothing to do
+    assert lib.wkv7_selftest_bf16_ops(None, F, 4, 2 * F, 3 * F, None) == 1
+    assert lib.wkv7_selftest_bf16_ops(F + 2, 4 * F, 4, 2 * F, 3 * F, None) == 6
+    assert lib.wkv7_selftest_bf16_ops(F, 4 * F, 4, F + 8, 3 * F, None) == 7   # split over a

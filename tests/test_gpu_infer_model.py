@@ -146,3 +146,43 @@ def test_bf16_operator_serves_with_a_bf16_state_and_the_dither():
     model.infer(toks, ids, shifted)
     torch.cuda.synchronize()
     assert any(not torch.equal(a, b) for a, b in zip(shifted.state, one.state))
+
+
+@torch.no_grad()
+def test_bf16_operator_serves_with_an_fp32_state_on_request():
+    """new_infer_state(state_dtype=float32) keeps a bf16 model's WKV7 states in
+    fp32: the decode runs the f32 kernel on the bf16 operands with no dither.
+    A whole prompt through infer gives the training path's logits (the
+    chunked kernels, fp32 state) to the bf16 bar; the same prompt from
+    another elapsed_t leaves the same states bit for bit (no dither); prefill
+    plus decode matches one call to bf16 rounding (the per-token operands
+    are the same; only the row count of the matrix products differs)."""
+    model = tiny_model(seed=3, std=0.2, neighbor_ops="hip", wkv7_dtype=torch.bfloat16).to(DEV)
+    toks = _prompt(2, 32, 10)
+    ids = torch.tensor([0, 1], device=DEV)
+    one = model.new_infer_state(2, state_dtype=torch.float32)
+    assert all(s.dtype == torch.float32 for s in one.state)
+    announce("model infer bf16 operands, fp32 state", "one call")
+    got = model.infer(toks, ids, one, unembed_mode="full")
+    x = model.layer_norm_for_first_cell(model.embed(toks))
+    x, _, _, _ = model.cells(x, ids, _wkv7_mod().KernelPretrain)
+    want = model.unembed(model.layer_norm_for_unembed(x))
+    torch.cuda.synchronize()
+    assert _err(got, want) <= 1e-2
+    shifted = model.new_infer_state(2, state_dtype=torch.float32)
+    shifted.elapsed_t.fill_(1000)
+    announce("model infer bf16 operands, fp32 state", "other elapsed_t")
+    model.infer(toks, ids, shifted, unembed_mode="skip")
+    torch.cuda.synchronize()
+    assert all(torch.equal(a, b) for a, b in zip(shifted.state, one.state))
+    step = model.new_infer_state(2, state_dtype=torch.float32)
+    announce("model infer bf16 operands, fp32 state", "prefill 16 + 16 decode steps")
+    model.infer(toks[:, :16], ids, step, unembed_mode="skip")
+    for t in range(16, 32):
+        last = model.infer(toks[:, t:t + 1], ids, step)
+    torch.cuda.synchronize()
+    assert _err(last[:, 0], got[:, -1]) <= 1e-2
+    for a, b in zip(step.state, one.state):
+        assert _err(a, b) <= 1e-2
+    with pytest.raises(ValueError):
+        tiny_model(seed=3).new_infer_state(1, state_dtype=torch.bfloat16)

@@ -210,6 +210,64 @@ def test_bf16_long_chunks_on_the_chunked_kernels(wk, oracle, case):
             assert rel_l2(got, pkg.synthetic.bf16_round(obwd[gn])) <= BF16_TOL, gn
 
 
+@pytest.mark.parametrize("case", [
+    (1, 96, 3, 48, 0.1, 25),
+    (1, 192, 2, 64, 0.1, 26),
+    (2, 128, 2, 32, None, 27),
+])
+def test_bf16_long_chunks_well_conditioned(wk, oracle, case):
+    # The long-chunk test above can only hold dw, dr and da to the reference
+    # algorithm's own (large) error, because its decays amplify the reversal's
+    # rounding by 1/w~ ~ 1.35 per step. Here the decay logits are shifted by
+    # -6, so w~ = exp(-e^{-1/2} sigmoid(x - 6)) is within 0.2% of one and the
+    # reversal (kernel.rs:239-246) amplifies nothing: every tensor, the rebuilt-
+    # state gradients included, is held to the bf16 bars against the oracle.
+    # A wrong rebuild of the start states between checkpoints in the chunked
+    # backward (template instance kLong) moves dw, dr and da by O(1).
+    B, T, H, C, s0_std, seed = case
+    announce("bf16 long chunk, w~ near 1", case)
+    pkg = load_pkg()
+    d = pkg.synthetic.make_inputs(B, T, H, 64, seed=seed, s0_std=s0_std, bf16=True)
+    d["w"] = pkg.synthetic.bf16_round(d["w"] - 6.0)
+    if d["s0"] is None:
+        d["s0"] = np.zeros((B, H, 64, 64), np.float32)
+    fwd, bwd = run_gpu(wk, d, C, torch.bfloat16)
+    ofwd, obwd = run_oracle(oracle, d, C)
+    exact = oracle.grad_f64(*(d[n] for n in NAMES), d["s0"], d["dy"])
+    for gn in ("weight_decay_grad", "receptance_grad", "removal_grad"):
+        print(case, gn, f"reference algorithm vs exact {rel_l2(obwd[gn], exact[gn]):.2e}",
+              flush=True)
+        assert rel_l2(obwd[gn], exact[gn]) <= 1e-4, gn   # the case is well conditioned
+    ofwd["output"] = pkg.synthetic.bf16_round(ofwd["output"])
+    for gn in GRAD_NAMES:
+        obwd[gn] = pkg.synthetic.bf16_round(obwd[gn])
+    compare(fwd, bwd, ofwd, obwd, BF16_TOL, f"bf16 long chunk w~1 {case}", BF16_STATE_TOL)
+
+
+def test_bf16_statetune_on_the_chunked_kernels(wk, oracle):
+    # the statetune flags (s0 in, no s_T; no ds_T, ds0 out:
+    # wkv7_statetune/forward.rs:19-76) with bf16 operands, i.e. on the chunked
+    # kernels, against the oracle with the same flags
+    announce("bf16 statetune", (2, 64, 3, 16))
+    pkg = load_pkg()
+    d = pkg.synthetic.make_inputs(2, 64, 3, 64, seed=28, s0_std=0.1, bf16=True)
+    ins = [to_dev(d[n], torch.bfloat16) for n in NAMES]
+    s0 = to_dev(d["s0"])
+    f = wk.wkv7_statetune_forward(*ins, s0, 16)
+    g = wk.wkv7_statetune_backward(*ins, f.state, f.removal_state,
+                                   to_dev(d["dy"], torch.bfloat16), 16)
+    torch.cuda.synchronize()
+    ofwd, obwd = run_oracle(oracle, d, 16)
+    assert rel_l2(to_np(f.output), pkg.synthetic.bf16_round(ofwd["output"])) <= BF16_TOL
+    for key in ("state", "removal_state"):
+        assert rel_l2(to_np(getattr(f, key)), ofwd[key]) <= BF16_STATE_TOL, key
+    for gn in GRAD_NAMES:
+        err = rel_l2(to_np(getattr(g, gn)), pkg.synthetic.bf16_round(obwd[gn]))
+        assert err <= BF16_TOL, (gn, err)
+    err = rel_l2(to_np(g.initial_state_grad), obwd["initial_state_grad"])
+    assert err <= BF16_STATE_TOL, err
+
+
 def test_long_chunk_bf16_backward_matches_step_backward(wk):
     # chunk_len 32 with bf16 operands: the forward runs the step kernels (their
     # fp32 checkpoints are what the rebuild between checkpoints needs) and the
@@ -270,11 +328,13 @@ def test_sequence_split_is_exact(wk):
     assert torch.equal(b.final_state, full.final_state)
 
 
-def test_empty_sequence(wk):
-    # T = 0: final state = initial state, initial-state grad = final-state grad
-    announce("T=0")
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+def test_empty_sequence(wk, dtype):
+    # T = 0: final state = initial state, initial-state grad = final-state grad.
+    # bf16 at chunk_len 16 runs the chunked forward with no chunks.
+    announce("T=0", str(dtype))
     B, H = 2, 3
-    e = torch.empty(B, 0, H, 64, device="cuda")
+    e = torch.empty(B, 0, H, 64, device="cuda", dtype=dtype)
     s0 = torch.randn(B, H, 64, 64, device="cuda")
     out = wk.wkv7_statepass_forward(e, e, e, e, e, e, s0, 16)
     assert out.output.shape == (B, 0, H, 64) and out.state.shape == (B, H, 0, 64, 64)
@@ -567,6 +627,11 @@ def test_handover_fault_poisons_outputs_and_is_reported(wk):
     rc = native.lib().wkv7_take_faults(torch.cuda.current_stream().cuda_stream, ctypes.byref(n))
     assert rc == native.WKV7_ERR_HANDOVER and n.value > 0, (rc, n.value)
     assert wk.take_faults() == 0
+    # and the Python side raises it where the caller polls
+    wk.wkv7_forward_ex(*ins, s0, 16, handover_spin_limit=1)
+    with pytest.raises(native.Wkv7Error, match="hand-over"):
+        wk.check_faults()
+    wk.check_faults()      # the counter was reset
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
