@@ -183,14 +183,15 @@ __global__ __launch_bounds__(kThreads) void wkv7_infer_kernel(InferParams<Tin> p
 // One wave per (active row, head); lane j owns value row j of the state, so
 // each row's sums over the key index run left to right inside one lane, as
 // the reference's thread j does (kernel.rs:81-96). The row is held as 32
-// registers of bf16 pairs, as stored, and widened where an operation reads a
-// value. The step's key-indexed operands (the rounded decay, a, b, k, r) go
-// through LDS as fp32 and are read back as broadcasts; lane j keeps its own
-// v_j. The step is bound by its instruction count (64 x 64 elements of one
-// (row, head) on one wave, a rounding after every operation): each "round
-// two values, add them" is one packed conversion and one bf16 dot product
-// (add_rb), and the two new state values of a key pair are rounded by one
-// packed conversion. The 8 KiB state moves between HBM and the lanes' rows
+// registers of bf16 pairs, as stored, and never widened. The step's
+// key-indexed operands (the rounded decay, a, b, k, r) go through LDS and are
+// read back as broadcasts; lane j keeps its own v_j. The step is mostly VALU
+// work (64 x 64 elements of one (row, head) on
+// one wave, a rounding after every operation): each product of two bf16
+// values is one bf16 dot product, each "round two values, add them" one
+// packed conversion and one bf16 dot product (see dot2x2 below), and the two
+// new state values of a key pair are rounded by one packed conversion. The
+// 8 KiB state moves between HBM and the lanes' rows
 // through LDS, with coalesced 16-byte accesses on the HBM side and each row's
 // 16-byte pieces rotated by row + row / 8 so that neither the row-per-lane
 // reads nor the contiguous writes conflict on LDS banks.
@@ -204,27 +205,80 @@ struct InferBf16Params {
   int T, H, full_batch, use_dither;
 };
 
-__device__ __forceinline__ float bf_lo(uint32_t u) { return __uint_as_float(u << 16); }
-__device__ __forceinline__ float bf_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
-
 __device__ __forceinline__ int rot_piece(int row, int q) { return row * 8 + ((q + row + (row >> 3)) & 7); }
 
+// The step's arithmetic is built on v_dot2_f32_bf16 in its VOP3P form,
+// a.b + 0 with a zero constant accumulator: the compiler emits only the VOP2
+// v_dot2c_f32_bf16, whose accumulator is its destination, and so needs a
+// move of zero before every use (256 per step here). The VOP3P form is
+// reachable through inline assembly only, where the compiler's hazard
+// recognizer cannot see it: a DOT result may be read by another VALU
+// instruction only two wait states after it is written, and overwritten by
+// a non-DOT VALU instruction only after three (what the compiler inserts
+// around v_dot2c on gfx950), so every block below ends with s_nop 2. The
+// kernel has no matrix-core instructions. Two uses:
+// - a product of two bf16 values, exact in fp32, is one dot product of the
+//   state pair with an operand word that holds the key's value in the half
+//   of the key's parity and zero in the other (no widening of the state);
+// - the reference's rounded sum rb(x + p) of two fp32 values is the dot
+//   product of their packed bf16 roundings with (1, 1), whose bf16 rounding
+//   is that of the fp32 addition (add_rb in wkv7_device.hpp, checked on the
+//   device by tests/test_gpu_selftest.py).
+__device__ __forceinline__ void dot2x2(uint32_t a0, uint32_t b0, uint32_t a1, uint32_t b1,
+                                       float& r0, float& r1) {
+  asm("v_dot2_f32_bf16 %0, %2, %3, 0\n\t"
+      "v_dot2_f32_bf16 %1, %4, %5, 0\n\t"
+      "s_nop 2"
+      : "=&v"(r0), "=v"(r1)
+      : "v"(a0), "v"(b0), "v"(a1), "v"(b1));
+}
+__device__ __forceinline__ float dot2x1(uint32_t a, uint32_t b) {
+  float r;
+  asm("v_dot2_f32_bf16 %0, %1, %2, 0\n\t"
+      "s_nop 2"
+      : "=v"(r)
+      : "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ uint32_t pack_rb(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
+}
+constexpr uint32_t kOnes = 0x3f803f80u;   // bf16 (1, 1)
+
 __global__ __launch_bounds__(64) void wkv7_infer_bf16_kernel(InferBf16Params p) {
-  __shared__ uint4 srow[kHead * 8];      // the state, 8 pieces of 16 bytes per row
-  __shared__ float4 ops[5][kHead / 4];   // rounded decay, a, b, k, r of the step
-  enum { O_W = 0, O_A, O_B, O_K, O_R };
+  __shared__ uint4 srow[kHead * 8];        // the state, 8 pieces of 16 bytes per row
+  // the step's key-indexed operands: a, the rounded decay and r as product
+  // words (key i's bf16 value in half i % 2), b and k as fp32
+  __shared__ uint4 opw[3][kHead / 4];
+  __shared__ float4 opf[2][kHead / 4];
+  enum { O_A = 0, O_W, O_R };
+  enum { O_B = 0, O_K };
 
   const int h = blockIdx.x, bi = blockIdx.y;
   const int lane = threadIdx.x;
   const int T = p.T;
   const int64_t tstride = (int64_t)p.H * kHead;
   const int64_t tok0 = ((int64_t)bi * T * p.H + h) * kHead + lane;
+  // operands of step t, loaded one step ahead; step 0's are requested first,
+  // before the slot and the state, so that their latency and the state's
+  // overlap
+  bool nlive = false;
+  bf16_t nw = 0, na = 0, nb = 0, nk = 0, nr = 0, nv = 0;
+  auto fetch = [&](int t) {
+    nlive = !p.mask || (p.mask[(int64_t)bi * T + t] & 0x7fffu) != 0u;
+    if (nlive) {
+      const int64_t off = tok0 + (int64_t)t * tstride;
+      nw = p.w[off]; na = p.a[off]; nb = p.b[off]; nk = p.k[off]; nr = p.r[off]; nv = p.v[off];
+    }
+  };
+  if (T > 0) fetch(0);
   const int64_t slot = p.batch_ids[bi];
   // an out-of-range slot is refused: zero output, no state touched
   if (slot < 0 || slot >= p.full_batch) {
     for (int t = 0; t < T; ++t) p.y[tok0 + (int64_t)t * tstride] = 0;
     return;
   }
+  const uint32_t elapsed = p.elapsed_t ? (uint32_t)p.elapsed_t[slot] : 0u;
   uint4* st = reinterpret_cast<uint4*>(p.state + (slot * p.H + h) * (kHead * kHead));
   // the state is read and written once, with the non-temporal hint as in the
   // fp32 kernel (measured at config[3] with the state read from HBM: 44.2 ->
@@ -238,7 +292,7 @@ __global__ __launch_bounds__(64) void wkv7_infer_bf16_kernel(InferBf16Params p) 
   }
   __syncthreads();
   // the row as it is stored: keys 2 m and 2 m + 1 in the low and high half of
-  // sp[m], widened to fp32 where an operation reads them
+  // sp[m]
   uint32_t sp[kHead / 2];
 #pragma unroll
   for (int q = 0; q < 8; ++q) {
@@ -249,20 +303,10 @@ __global__ __launch_bounds__(64) void wkv7_infer_bf16_kernel(InferBf16Params p) 
     sp[4 * q + 3] = x.w;
   }
 
-  const uint32_t elapsed = p.elapsed_t ? (uint32_t)p.elapsed_t[slot] : 0u;
   uint32_t valid_t = 0;
-  float* opf = reinterpret_cast<float*>(ops);
-  // operands of step t, loaded one step ahead
-  bool nlive = false;
-  bf16_t nw = 0, na = 0, nb = 0, nk = 0, nr = 0, nv = 0;
-  auto fetch = [&](int t) {
-    nlive = !p.mask || (p.mask[(int64_t)bi * T + t] & 0x7fffu) != 0u;
-    if (nlive) {
-      const int64_t off = tok0 + (int64_t)t * tstride;
-      nw = p.w[off]; na = p.a[off]; nb = p.b[off]; nk = p.k[off]; nr = p.r[off]; nv = p.v[off];
-    }
-  };
-  if (T > 0) fetch(0);
+  uint32_t* const opwu = reinterpret_cast<uint32_t*>(opw);
+  float* const opff = reinterpret_cast<float*>(opf);
+  const int half = 16 * (lane & 1);        // this lane's key in its word
   for (int t = 0; t < T; ++t) {
     const int64_t off = tok0 + (int64_t)t * tstride;
     const bool live = nlive;
@@ -274,12 +318,12 @@ __global__ __launch_bounds__(64) void wkv7_infer_bf16_kernel(InferBf16Params p) 
     }
     float wd = decay_f(sigmoid_f(bf16_to_f32(cw)));
     if (p.use_dither) wd += dither_f(elapsed + valid_t);
-    __syncthreads();   // the previous step's reads of ops are done
-    opf[O_W * kHead + lane] = rb(wd);
-    opf[O_A * kHead + lane] = bf16_to_f32(ca);
-    opf[O_B * kHead + lane] = bf16_to_f32(cb);
-    opf[O_K * kHead + lane] = bf16_to_f32(ck);
-    opf[O_R * kHead + lane] = bf16_to_f32(cr);
+    __syncthreads();   // the previous step's reads of the operands are done
+    opwu[O_A * kHead + lane] = (uint32_t)ca << half;
+    opwu[O_W * kHead + lane] = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)wd) << half;
+    opwu[O_R * kHead + lane] = (uint32_t)cr << half;
+    opff[O_B * kHead + lane] = bf16_to_f32(cb);
+    opff[O_K * kHead + lane] = bf16_to_f32(ck);
     const float vj = bf16_to_f32(cv);
     __syncthreads();
     // Running sums are kept unrounded (z): the reference's bf16 sum after key
@@ -288,29 +332,37 @@ __global__ __launch_bounds__(64) void wkv7_infer_bf16_kernel(InferBf16Params p) 
     float z = 0.0f;
 #pragma unroll
     for (int i4 = 0; i4 < kHead / 4; ++i4) {
-      const float4 a4 = ops[O_A][i4];
-      z = add_rb(z, a4.x * bf_lo(sp[2 * i4]));
-      z = add_rb(z, a4.y * bf_hi(sp[2 * i4]));
-      z = add_rb(z, a4.z * bf_lo(sp[2 * i4 + 1]));
-      z = add_rb(z, a4.w * bf_hi(sp[2 * i4 + 1]));
+      const uint4 a4 = opw[O_A][i4];
+      float p0, p1, p2, p3;
+      dot2x2(sp[2 * i4], a4.x, sp[2 * i4], a4.y, p0, p1);
+      dot2x2(sp[2 * i4 + 1], a4.z, sp[2 * i4 + 1], a4.w, p2, p3);
+      z = dot2x1(pack_rb(z, p0), kOnes);
+      z = dot2x1(pack_rb(z, p1), kOnes);
+      z = dot2x1(pack_rb(z, p2), kOnes);
+      z = dot2x1(pack_rb(z, p3), kOnes);
     }
     const float sa = rb(z);
     float zy = 0.0f;
 #pragma unroll
     for (int i4 = 0; i4 < kHead / 4; ++i4) {
-      const float4 w4 = ops[O_W][i4], b4 = ops[O_B][i4], k4 = ops[O_K][i4], r4 = ops[O_R][i4];
-      const float wv[4] = {w4.x, w4.y, w4.z, w4.w}, bv[4] = {b4.x, b4.y, b4.z, b4.w};
-      const float kv[4] = {k4.x, k4.y, k4.z, k4.w}, rv[4] = {r4.x, r4.y, r4.z, r4.w};
+      const uint4 w4 = opw[O_W][i4], r4 = opw[O_R][i4];
+      const float4 b4 = opf[O_B][i4], k4 = opf[O_K][i4];
+      const uint32_t wv[4] = {w4.x, w4.y, w4.z, w4.w}, rv[4] = {r4.x, r4.y, r4.z, r4.w};
+      const float bv[4] = {b4.x, b4.y, b4.z, b4.w}, kv[4] = {k4.x, k4.y, k4.z, k4.w};
 #pragma unroll
       for (int e = 0; e < 4; e += 2) {
         // S[j,i] = rb(rb(rb(S w) + rb(sa b)) + rb(k v)) for keys i, i + 1,
         // the two new values rounded by one packed conversion
         uint32_t& pair = sp[2 * i4 + e / 2];
-        const float u0 = add_rb(add_rb(bf_lo(pair) * wv[e], sa * bv[e]), kv[e] * vj);
-        const float u1 = add_rb(add_rb(bf_hi(pair) * wv[e + 1], sa * bv[e + 1]), kv[e + 1] * vj);
-        pair = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{u0, u1}, bf16x2_t));
-        zy = add_rb(zy, bf_lo(pair) * rv[e]);
-        zy = add_rb(zy, bf_hi(pair) * rv[e + 1]);
+        float u0, u1;
+        dot2x2(pair, wv[e], pair, wv[e + 1], u0, u1);                        // S w
+        dot2x2(pack_rb(u0, sa * bv[e]), kOnes, pack_rb(u1, sa * bv[e + 1]), kOnes, u0, u1);
+        dot2x2(pack_rb(u0, kv[e] * vj), kOnes, pack_rb(u1, kv[e + 1] * vj), kOnes, u0, u1);
+        pair = pack_rb(u0, u1);
+        float y0, y1;
+        dot2x2(pair, rv[e], pair, rv[e + 1], y0, y1);                        // S r
+        zy = dot2x1(pack_rb(zy, y0), kOnes);
+        zy = dot2x1(pack_rb(zy, y1), kOnes);
       }
     }
     const float y = rb(zy);
