@@ -14,7 +14,8 @@ ms per step, and:
 - "dtype"/"arithmetic": what the kernels compute in. With bf16 operands and
   chunk_len 16 the chunked matrix-core kernels run: fp32 state and
   accumulation, products of fp32 operands from bf16 hi/lo halves
-  (hi*hi + hi*lo + lo*hi);
+  (hi*hi + hi*lo + lo*hi); with fp32 operands the fp32 chunked kernels:
+  fp32 products on the fp32 matrix cores and fp32 sums;
 - "roofline": the dominant kernel (the backward): algorithmic FP32 FLOPs per
   launch / mean launch time (HIP events on the launch stream) against
   MI355X's 157.3 TFLOP/s FP32 peak, with "traffic" (HBM bytes per launch from
@@ -423,16 +424,24 @@ def bench_train(cfg, steps, warmup, with_cpu, probe=False, kernels="auto"):
     fwd_flops = FLOP_FWD * head_steps
     achieved = bwd_flops / (bwd_ms * 1e-3)
     e = 2 if io == torch.bfloat16 else 4
-    # which kernels ran (launch_forward / launch_backward dispatch)
-    chunked = io == torch.bfloat16 and C == 16 and T % 16 == 0 and kernels == "auto"
-    bwd_kernel = "wkv7_bwd_chunk_kernel" if chunked else "wkv7_bwd_kernel"
-    fwd_kernel = "wkv7_fwd_chunk_kernel" if chunked else "wkv7_fwd_kernel"
+    # which kernels ran (launch_forward / launch_backward dispatch; chunk_len
+    # is 16 here): the chunked kernels of the operand type, or the step kernels
+    chunked = C == 16 and T % 16 == 0 and kernels == "auto"
+    f32_chunked = chunked and io == torch.float32
+    tag = "f32_chunk" if f32_chunked else "chunk"
+    bwd_kernel = f"wkv7_bwd_{tag}_kernel" if chunked else "wkv7_bwd_kernel"
+    fwd_kernel = f"wkv7_fwd_{tag}_kernel" if chunked else "wkv7_fwd_kernel"
     # algorithmic HBM bytes per head-step: fwd 7 rows in/out (e bytes) + sa
     # out + 1/16 of a checkpoint; bwd 7 rows + sa in, 6 gradients out, 1/16
     # of a checkpoint in
     fwd_bytes = head_steps * (7 * N_HEAD * e + N_HEAD * 4 + N_HEAD * N_HEAD * 4 / C)
     bwd_bytes = head_steps * (13 * N_HEAD * e + N_HEAD * 4 + N_HEAD * N_HEAD * 4 / C)
-    if chunked:
+    if f32_chunked:
+        arithmetic = ("fp32 throughout: the chunked matrix form with fp32 products on the fp32 "
+                      "matrix cores (v_mfma_f32_16x16x4_f32) and fp32 sums; fp32 operands and "
+                      "outputs")
+        dtype = "f32"
+    elif chunked:
         arithmetic = ("fp32 state, checkpoints and accumulation; matrix products of two fp32 "
                       "operands formed from bf16 hi/lo halves as hi*hi + hi*lo + lo*hi on the "
                       "bf16 matrix cores (about 16 significant bits per product), products with "
@@ -484,7 +493,7 @@ def bench_train(cfg, steps, warmup, with_cpu, probe=False, kernels="auto"):
                      "peak_note": "FP32-equivalent: the metric's algorithmic fp32 FLOPs "
                                   "against MI355X's 157.3 TFLOP/s FP32 peak",
                      "units": units},
-        "kernels": "chunked-mfma" if chunked else "step-valu",
+        "kernels": ("chunked-mfma-f32" if f32_chunked else "chunked-mfma") if chunked else "step-valu",
         "fwd_ms": fwd_ms,
         "fwd_ms_median": fwd_each[steps // 2],
         "bwd_ms": bwd_ms,

@@ -41,11 +41,22 @@
  *     about 16 significant bits where fp32 has 24. Measured against the
  *     reference-order fp32 result: the state family about 3e-6 relative L2,
  *     the bf16 outputs and gradients at their own bf16 rounding (1e-4 to 7e-4);
- *   - fp32 operands, and bf16 operands at every other chunk_len (the forward
- *     at chunk_len > 16 included): the step kernels, fp32 products and sums,
- *     about 1e-7 from the reference-order fp32 result.
+ *   - fp32 operands at chunk_len a multiple of 16 (the fp32 chunked
+ *     kernels): fp32 products on the fp32 matrix cores and fp32 sums, in the
+ *     chunked matrix form (16-step blocks as matrix products rather than
+ *     step by step); the backward rebuilds start states between checkpoints
+ *     by the reference's reversal in its operation order, which amplifies
+ *     any fp32 difference by about 1.35 per step. Measured against the
+ *     reference-order fp32 result at config[0]: output 2.6e-7 relative L2,
+ *     checkpoints 1.7e-7, the gradients through the rebuilt start states
+ *     (dw, dr, da) 6.2e-6, 4.6e-6, 6.0e-6, the others 2.5e-7 to 4e-7 (the
+ *     step kernels on the same call: 1.8e-7, 7e-8, 3.7e-6, 3.0e-6, 4.3e-6);
+ *   - bf16 operands at every other chunk_len (the forward at chunk_len > 16
+ *     included) and fp32 operands at chunk lengths that are not multiples
+ *     of 16: the step kernels, fp32 products and sums in the reference's
+ *     operation order.
  * wkv7_forward_ex / wkv7_backward_ex with WKV7_KERNELS_STEP run the step
- * kernels, i.e. fp32 products, for bf16 operands too.
+ * kernels, i.e. the reference's operation order, for every case.
  *
  * Ownership and threading: the caller allocates every buffer on the device
  * (use wkv7_checkpoint_numel for the checkpoint tensor); the library
@@ -157,11 +168,11 @@ int wkv7_backward(const void *weight_decay, const void *receptance,
  * one kernel per element type). wkv7_forward / wkv7_backward and the trait
  * entry points use WKV7_KERNELS_AUTO: the chunked matrix-core kernels for
  * bf16 operands (forward at chunk_len 16, backward at chunk_len a multiple of
- * 16), the step-by-step fp32 kernels otherwise; the arithmetic of each family
- * is described at the top of this file. WKV7_KERNELS_STEP runs the step
- * kernels for every case
- * (to compare the two families on one input). handover_spin_limit bounds the
- * polls of each hand-over wait inside the chunked forward (0 = the default,
+ * 16) and for fp32 operands (chunk_len a multiple of 16), the step-by-step
+ * kernels otherwise; the arithmetic of each family is described at the top
+ * of this file. WKV7_KERNELS_STEP runs the step kernels for every case (to
+ * compare the families on one input). handover_spin_limit bounds the polls
+ * of each hand-over wait inside the chunked forwards (0 = the default,
  * about 0.1 s); it exists so that tests can force the fault path below.
  * options may be NULL (all defaults).
  * ------------------------------------------------------------------------- */
@@ -194,8 +205,9 @@ int wkv7_backward_ex(const void *weight_decay, const void *receptance,
                      float *initial_state_grad, const wkv7_options *options,
                      void *stream);
 
-/* Hand-over faults of the chunked forward. Its producer and consumer waves
- * pass chunks through LDS flags with bounded waits. A wait that gives up
+/* Hand-over faults of the chunked forwards (bf16 and fp32 operands). Their
+ * producer and consumer waves pass chunks through LDS flags with bounded
+ * waits. A wait that gives up
  * (which a correct kernel never does) makes the launch overwrite every output
  * of that (batch, head) -- output, removal_state, the checkpoints, the final
  * state -- with NaN, and adds one to a counter on the device. No counterpart

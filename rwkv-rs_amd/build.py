@@ -20,7 +20,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libwkv7_hip.so")
 SOURCES = ["wkv7_api.cpp", "wkv7_forward.hip", "wkv7_backward.hip", "wkv7_infer.hip",
-           "wkv7_chunk_forward.hip", "wkv7_chunk_backward.hip", "wkv7_selftest.hip",
+           "wkv7_chunk_forward.hip", "wkv7_chunk_backward.hip", "wkv7_f32_chunk.hip",
+           "wkv7_selftest.hip",
            "neighbors_api.cpp", "neighbors.hip", "lm_loss_api.cpp", "lm_loss.hip"]
 ARCH = "gfx950"
 

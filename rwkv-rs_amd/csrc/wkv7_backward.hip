@@ -504,7 +504,10 @@ hipError_t launch_bwd_t(const BackwardDesc& d, hipStream_t stream) {
 
 hipError_t launch_backward(const BackwardDesc& d, hipStream_t stream) {
   if (d.B == 0 || d.H == 0) return hipSuccess;
-  if (chunk_backward_supported(d) && !d.kc.step_only) return launch_backward_chunked(d, stream);
+  if (!d.kc.step_only) {
+    if (chunk_backward_supported(d)) return launch_backward_chunked(d, stream);
+    if (chunk_f32_backward_supported(d)) return launch_backward_chunked_f32(d, stream);
+  }
   return d.dtype == Dtype::BF16 ? launch_bwd_t<bf16_t>(d, stream) : launch_bwd_t<float>(d, stream);
 }
 

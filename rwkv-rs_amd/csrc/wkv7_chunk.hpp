@@ -271,5 +271,35 @@ __device__ __forceinline__ void wave_lds_sync() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
+// Hand-over between the waves of a workgroup through LDS flags, for the
+// chunked forwards whose preparing waves and chain waves run concurrently.
+// polls of a hand-over flag before a wave gives up (each poll sleeps ~64
+// cycles): about 0.1 s, far beyond any legitimate wait in a kernel that runs
+// for well under a millisecond. The caller may lower it (tests force the
+// fault path with a single poll).
+constexpr uint32_t kSpinLimit = 1u << 22;
+
+__device__ __forceinline__ int lds_load_flag(const int* f) {
+  return __atomic_load_n(f, __ATOMIC_RELAXED);
+}
+__device__ __forceinline__ void lds_store_flag(int* f, int v) {
+  __atomic_store_n(f, v, __ATOMIC_RELAXED);
+}
+// poll *f until it reaches v, at most `limit` times; false if it gave up
+__device__ __forceinline__ bool wait_flag(const int* f, int v, uint32_t limit) {
+  for (uint32_t n = 0; n < limit; ++n) {
+    if (lds_load_flag(f) >= v) return true;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  return lds_load_flag(f) >= v;
+}
+// the wave's earlier LDS writes are complete before its later LDS accesses
+__device__ __forceinline__ void lds_release() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+}
+__device__ __forceinline__ void lds_acquire() {
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 }  // namespace chunk
 }  // namespace wkv7

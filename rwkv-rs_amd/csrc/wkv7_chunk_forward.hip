@@ -46,14 +46,8 @@ constexpr int kBlock = 64 * kWaves;
 constexpr int kVecs = 6;                  // staged inputs: x, r, k, a, b, v
 enum { S_X, S_R, S_K, S_A, S_B, S_V };
 constexpr int kPieces = kVecs * kL * 8 / 64;   // 16-byte loads per prep lane and chunk
-// polls of a hand-over flag before a wave gives up (each poll sleeps ~64
-// cycles): about 0.1 s, far beyond any legitimate wait in a kernel that runs
-// for well under a millisecond. The caller may lower it (tests force the
-// fault path with a single poll).
-constexpr uint32_t kSpinLimit = 1u << 22;
-
-// hand-over faults on this device since the host last took them, and the
-// value the last take read
+// hand-over faults of the chunked forwards on this device since the host
+// last took them, and the value the last take read
 __device__ unsigned int handover_faults;
 __device__ unsigned int handover_faults_taken;
 
@@ -265,28 +259,6 @@ struct Flags {
   int taken[kSlots][kChainWaves];
   int fault;                 // a wave gave up a wait
 };
-
-__device__ __forceinline__ int lds_load_flag(const int* f) {
-  return __atomic_load_n(f, __ATOMIC_RELAXED);
-}
-__device__ __forceinline__ void lds_store_flag(int* f, int v) {
-  __atomic_store_n(f, v, __ATOMIC_RELAXED);
-}
-// poll *f until it reaches v, at most `limit` times; false if it gave up
-__device__ __forceinline__ bool wait_flag(const int* f, int v, uint32_t limit) {
-  for (uint32_t n = 0; n < limit; ++n) {
-    if (lds_load_flag(f) >= v) return true;
-    __builtin_amdgcn_s_sleep(1);
-  }
-  return lds_load_flag(f) >= v;
-}
-// the wave's earlier LDS writes are complete before its later LDS accesses
-__device__ __forceinline__ void lds_release() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-}
-__device__ __forceinline__ void lds_acquire() {
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
 
 // A prep lane's share of a chunk's raw rows: piece k is row 8 k + lane / 8
 // of the chunk's 6 x 16 rows (vec k / 2, step 8 (k % 2) + lane / 8); LDS slot
@@ -505,6 +477,10 @@ hipError_t launch_forward_chunked(const ForwardDesc& d, hipStream_t stream) {
   else
     hipLaunchKernelGGL(wkv7_fwd_chunk_kernel<false>, grid, block, 0, stream, p);
   return hipGetLastError();
+}
+
+hipError_t handover_fault_counter(unsigned int** counter) {
+  return hipGetSymbolAddress(reinterpret_cast<void**>(counter), HIP_SYMBOL(handover_faults));
 }
 
 hipError_t take_handover_faults(hipStream_t stream, uint32_t* count) {

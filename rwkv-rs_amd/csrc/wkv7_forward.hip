@@ -326,7 +326,10 @@ hipError_t launch_fwd_t(const ForwardDesc& d, hipStream_t stream) {
 
 hipError_t launch_forward(const ForwardDesc& d, hipStream_t stream) {
   if (d.B == 0 || d.H == 0) return hipSuccess;
-  if (chunk_forward_supported(d) && !d.kc.step_only) return launch_forward_chunked(d, stream);
+  if (!d.kc.step_only) {
+    if (chunk_forward_supported(d)) return launch_forward_chunked(d, stream);
+    if (chunk_f32_forward_supported(d)) return launch_forward_chunked_f32(d, stream);
+  }
   return d.dtype == Dtype::BF16 ? launch_fwd_t<bf16_t>(d, stream) : launch_fwd_t<float>(d, stream);
 }
 

@@ -66,15 +66,27 @@ hipError_t launch_forward(const ForwardDesc& d, hipStream_t stream);
 // asked for the step kernels (KernelChoice::step_only).
 bool chunk_forward_supported(const ForwardDesc& d);
 hipError_t launch_forward_chunked(const ForwardDesc& d, hipStream_t stream);
-// the chunked forward's hand-over fault counter on the current device: read
+// the chunked forwards' hand-over fault counter on the current device: read
 // and reset on `stream`, then wait for it
 hipError_t take_handover_faults(hipStream_t stream, uint32_t* count);
+// that counter's device address on the current device
+hipError_t handover_fault_counter(unsigned int** counter);
+
+// Chunked fp32 matrix-core forward (wkv7_f32_chunk.hip): fp32 operands,
+// chunk_len a multiple of 16; picked by launch_forward under the same choice.
+// Its hand-over faults count in the same counter.
+bool chunk_f32_forward_supported(const ForwardDesc& d);
+hipError_t launch_forward_chunked_f32(const ForwardDesc& d, hipStream_t stream);
 
 // Chunked matrix-core backward (wkv7_chunk_backward.hip): bf16 operands,
 // chunk_len a multiple of 16, T a positive multiple of chunk_len; picked by
 // launch_backward under the same choice.
 bool chunk_backward_supported(const BackwardDesc& d);
 hipError_t launch_backward_chunked(const BackwardDesc& d, hipStream_t stream);
+// Chunked fp32 matrix-core backward (wkv7_f32_chunk.hip): fp32 operands,
+// chunk_len a multiple of 16, T a positive multiple of chunk_len.
+bool chunk_f32_backward_supported(const BackwardDesc& d);
+hipError_t launch_backward_chunked_f32(const BackwardDesc& d, hipStream_t stream);
 hipError_t launch_backward(const BackwardDesc& d, hipStream_t stream);
 hipError_t launch_infer(const InferDesc& d, hipStream_t stream);
 

@@ -243,8 +243,9 @@ def wkv7_forward_ex(weight_decay, receptance, key, value, removal, replacement, 
                     kernels: str = "auto", handover_spin_limit: int = 0
                     ) -> Wkv7StatePassForwardOutput:
     """wkv7_forward_ex (include/wkv7.h): the generic forward with an explicit
-    kernel family ("auto", or "step" for the step-by-step fp32 kernels in
-    every case) and hand-over bound. No counterpart in the reference."""
+    kernel family ("auto", or "step" for the step-by-step kernels, the
+    reference's operation order, in every case) and hand-over bound. No
+    counterpart in the reference."""
     state, sa, y, sT = _forward(weight_decay, receptance, key, value, removal, replacement,
                                 initial_state, chunk_len, use_initial_state, return_final_state,
                                 _options(kernels, handover_spin_limit))

@@ -143,6 +143,58 @@ def test_fp32_long_chunks_as_accurate_as_reference(wk, oracle, case):
             assert rel_l2(got, obwd[gn]) <= FP32_TOL, gn
 
 
+CRITERION_SHAPES = [   # (B, T, H, chunk_len): crates/rwkv-nn/benches/kernels/mod.rs:108-113
+    (1, 128, 8, 32),
+    (2, 256, 8, 32),
+    (4, 512, 16, 64),
+]
+
+
+@pytest.mark.parametrize("shape", CRITERION_SHAPES)
+@pytest.mark.parametrize("conditioned", [True, False], ids=["w_near_1", "synthetic"])
+def test_fp32_chunked_kernels_at_the_criterion_shapes(wk, oracle, shape, conditioned):
+    # The reference's Criterion bench shapes with fp32 operands, which the
+    # library runs on its fp32 chunked matrix-core kernels (chunk lengths that
+    # are multiples of 16). The benches draw every input N(0, 1), under which
+    # the state grows without bound (timing inputs, not a parity case), so
+    # the inputs here are the synthetic distributions. With the decay logits
+    # shifted by -6 (w~ within 0.2% of one) the reversal between checkpoints
+    # (kernel.rs:239-246) amplifies nothing and every tensor, the rebuilt-
+    # state gradients dw, dr, da included, is held to 1e-5 against the
+    # oracle; a wrong rebuild of the start states, or a wrong hand-over of
+    # them between the kernel's wave groups, moves those by O(1). Unshifted,
+    # the reference algorithm itself is off the exact gradients by 4e-4 at
+    # chunk_len 32 and by more than the gradients' size at 64 (measured), so
+    # there dw, dr, da are held to five times its own error against fp64.
+    B, T, H, C = shape
+    announce("fp32 chunked, Criterion shape", shape, "w~ near 1" if conditioned else "synthetic")
+    pkg = load_pkg()
+    d = pkg.synthetic.make_inputs(B, T, H, 64, seed=40 + C + B, s0_std=0.1)
+    if conditioned:
+        d["w"] = (d["w"] - 6.0).astype(np.float32)
+    dsT = np.random.default_rng(B + T).standard_normal((B, H, 64, 64)).astype(np.float32)
+    fwd, bwd = run_gpu(wk, d, C, torch.float32, dsT=dsT)
+    ofwd, obwd = run_oracle(oracle, d, C, dsT=dsT)
+    exact = oracle.grad_f64(*(d[n] for n in NAMES), d["s0"], d["dy"], ds_T=dsT)
+    rebuilt = ("weight_decay_grad", "receptance_grad", "removal_grad")
+    if conditioned:
+        for gn in rebuilt:
+            assert rel_l2(obwd[gn], exact[gn]) <= 1e-5, gn   # the case is well conditioned
+        compare(fwd, bwd, ofwd, obwd, FP32_TOL, f"fp32 chunked {shape} w~1")
+        return
+    for key in ("output", "removal_state", "state", "final_state"):
+        assert rel_l2(to_np(getattr(fwd, key)), ofwd[key]) <= FP32_TOL, key
+    for gn in GRAD_NAMES + ("initial_state_grad",):
+        got = to_np(getattr(bwd, gn))
+        if gn in rebuilt:
+            ref_err = rel_l2(obwd[gn], exact[gn])
+            err = rel_l2(got, exact[gn])
+            print(shape, gn, f"gpu {err:.2e} reference-algorithm {ref_err:.2e}", flush=True)
+            assert err <= 5 * ref_err + 1e-6, (gn, err, ref_err)
+        else:
+            assert rel_l2(got, obwd[gn]) <= FP32_TOL, gn
+
+
 @pytest.mark.parametrize("case", [
     (2, 128, 4, 16, 0.1, 11),   # 16-step checkpoints, 32-step forward tiles (two per tile)
     (1, 64, 4, 16, None, 12),
@@ -347,7 +399,7 @@ def test_empty_sequence(wk, dtype):
 def test_two_streams_match_one(wk):
     # The C ABI enqueues on the caller's stream and keeps no state between
     # calls (include/wkv7.h): two workloads launched alternately on two
-    # streams -- bf16 on the chunked kernels, fp32 on the step kernels --
+    # streams -- bf16 and fp32 operands, each on its chunked kernels --
     # give each workload's one-stream results bit for bit.
     announce("two streams")
     syn = load_pkg().synthetic
@@ -583,20 +635,22 @@ def test_bf16_chunked_backward_matches_step_backward(wk, case):
     assert err < BF16_STATE_TOL, err
 
 
-def test_handover_fault_poisons_outputs_and_is_reported(wk):
-    """The chunked forward's waves hand chunks over through LDS flags with
-    bounded waits. With the bound forced down to a single poll (the
-    handover_spin_limit option) waves give up waits, which a correct run never
-    does: every (batch, head) whose launch saw that must come back entirely
-    NaN (output, removal_state, checkpoints, final state), the count of such
-    launches must be reported by wkv7_take_faults as WKV7_ERR_HANDOVER, and
-    every other (batch, head) must equal the normal run bit for bit. A
-    normal run afterwards reports no fault."""
-    announce("hand-over fault path (forced from the host)")
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_handover_fault_poisons_outputs_and_is_reported(wk, dtype):
+    """The chunked forwards' waves (bf16 and fp32 operands) hand chunks over
+    through LDS flags with bounded waits. With the bound forced down to a
+    single poll (the handover_spin_limit option) waves give up waits, which a
+    correct run never does: every (batch, head) whose launch saw that must
+    come back entirely NaN (output, removal_state, checkpoints, final state),
+    the count of such launches must be reported by wkv7_take_faults as
+    WKV7_ERR_HANDOVER, and every other (batch, head) must equal the normal run
+    bit for bit. A normal run afterwards reports no fault."""
+    announce("hand-over fault path (forced from the host)", dtype)
     pkg = load_pkg()
     B, T, H = 2, 256, 8
-    d = pkg.synthetic.make_inputs(B, T, H, 64, seed=51, s0_std=0.1, bf16=True)
-    ins = [to_dev(d[n], torch.bfloat16) for n in NAMES]
+    bf16 = dtype == "bf16"
+    d = pkg.synthetic.make_inputs(B, T, H, 64, seed=51, s0_std=0.1, bf16=bf16)
+    ins = [to_dev(d[n], torch.bfloat16 if bf16 else torch.float32) for n in NAMES]
     s0 = to_dev(d["s0"])
     assert wk.take_faults() == 0
     good = wk.wkv7_statepass_forward(*ins, s0, 16)
@@ -638,8 +692,8 @@ def test_handover_fault_poisons_outputs_and_is_reported(wk):
 def test_tensors_past_2g_elements(wk, oracle, dtype):
     # Inputs past 2^31 elements each: bf16 [136, 4096, 64, 64] on the chunked
     # kernels (2.28e9 elements, 4.6 GB each; about 110 GB on the device with
-    # the checkpoints and gradients), fp32 [129, 4096, 64, 64] on the step
-    # kernels (2.16e9 elements, 8.7 GB each; about 165 GB). The first and the
+    # the checkpoints and gradients), fp32 [129, 4096, 64, 64] on the fp32
+    # chunked kernels (2.16e9 elements, 8.7 GB each; about 165 GB). The first and the
     # last (b, h) pairs -- the last one's elements lie past 2^31 elements and
     # 2^32 bytes from every tensor's start -- against the oracle run on that
     # pair alone, at the dtype's bars.

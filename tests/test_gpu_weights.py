@@ -12,9 +12,9 @@ bfloat16 as the releases are, and read back by ``load_pth`` from disk.
 * The loaded model's logits equal a float64 forward that reads the checkpoint
   by its release key names with no key table (``release_forward_f64``), so a
   key mapped to the wrong one of two same-shaped parameters, or a transposed
-  projection, fails here even where the shapes agree: fp32 operands (the step
-  kernels) within 1e-5 relative L2; bf16 operands under autocast (the chunked
-  kernels) within 1e-2.
+  projection, fails here even where the shapes agree: fp32 operands (the fp32
+  chunked kernels) within 1e-5 relative L2; bf16 operands under autocast (the
+  bf16 chunked kernels) within 1e-2.
 * Loss and every parameter gradient through ``KernelPretrain`` equal those of
   the same loaded model with a plain PyTorch recurrence as the operator: fp32
   loss 1e-5 and gradients 1e-4, bf16 loss 1e-3 and gradients 1e-2.
