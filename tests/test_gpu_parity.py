@@ -438,15 +438,20 @@ def test_two_streams_match_one(wk):
             assert torch.equal(getattr(g1, gn), getattr(g2, gn)), gn
 
 
-def test_graph_replays_match_eager(wk):
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_graph_replays_match_eager(wk, dtype):
     # The forward and backward launch kernels only (no memsets, copies or
     # allocations inside the library), so a caller can capture them in a HIP
     # graph: each of several replays, with eager work between them, gives
-    # the eager results bit for bit (bf16 operands: the chunked kernels).
-    announce("graph replay")
-    d = load_pkg().synthetic.make_inputs(2, 128, 4, 64, seed=41, s0_std=0.1, bf16=True)
-    ins = [to_dev(d[n], torch.bfloat16) for n in NAMES]
-    s0, dy = to_dev(d["s0"]), to_dev(d["dy"], torch.bfloat16)
+    # the eager results bit for bit (bf16 and fp32 operands: the chunked
+    # kernels of each; the fp32 forward looks up its fault counter's address
+    # at every launch, captured ones included).
+    announce("graph replay", dtype)
+    bf16 = dtype == "bf16"
+    dt = torch.bfloat16 if bf16 else torch.float32
+    d = load_pkg().synthetic.make_inputs(2, 128, 4, 64, seed=41, s0_std=0.1, bf16=bf16)
+    ins = [to_dev(d[n], dt) for n in NAMES]
+    s0, dy = to_dev(d["s0"]), to_dev(d["dy"], dt)
     zero = torch.zeros_like(s0)
 
     def run():
