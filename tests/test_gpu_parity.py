@@ -196,6 +196,29 @@ def test_fp32_chunked_kernels_at_the_criterion_shapes(wk, oracle, shape, conditi
 
 
 @pytest.mark.parametrize("case", [
+    # (B, T, H, chunk_len, s0_std, seed)
+    (3, 32, 100, 16, 0.1, 60),   # 300 (batch, head) pairs: more workgroups than CUs
+    (1, 144, 2, 48, 0.1, 61),    # three 16-step chunks per checkpoint
+    (2, 64, 5, 32, None, 62),    # zero initial state, an odd head count
+    (1, 16, 3, 16, 0.1, 63),     # one chunk: the start state by the reversal alone
+])
+def test_fp32_chunked_kernels_more_shapes(wk, oracle, case):
+    # More shapes on the fp32 chunked kernels, with the decay logits shifted
+    # by -6 as above, so that every tensor, dw, dr and da included, is held
+    # to 1e-5 against the oracle at any chunk_len.
+    B, T, H, C, s0_std, seed = case
+    announce("fp32 chunked, w~ near 1", case)
+    d = load_pkg().synthetic.make_inputs(B, T, H, 64, seed=seed, s0_std=s0_std)
+    d["w"] = (d["w"] - 6.0).astype(np.float32)
+    if d["s0"] is None:
+        d["s0"] = np.zeros((B, H, 64, 64), np.float32)
+    dsT = np.random.default_rng(seed).standard_normal((B, H, 64, 64)).astype(np.float32)
+    fwd, bwd = run_gpu(wk, d, C, torch.float32, dsT=dsT)
+    ofwd, obwd = run_oracle(oracle, d, C, dsT=dsT)
+    compare(fwd, bwd, ofwd, obwd, FP32_TOL, f"fp32 chunked w~1 {case}")
+
+
+@pytest.mark.parametrize("case", [
     (2, 128, 4, 16, 0.1, 11),   # 16-step checkpoints, 32-step forward tiles (two per tile)
     (1, 64, 4, 16, None, 12),
     (1, 48, 3, 16, 0.1, 13),    # T not a multiple of 32: partial last forward tile
