@@ -758,7 +758,7 @@ def main():
     # the forward unchanged); the default warm-up covers that ramp
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--config", default="cfg1", choices=sorted(CONFIGS) + ["criterion"],
-                    help="cfg0-cfg4: BASELINE.json's configurations; criterion: the calls of the "
+                    help="cfg0-cfg4: the metric's configurations config[0]-config[4] (CONFIGS); criterion: the calls of the "
                          "reference's own Criterion benches on their three cases")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--state-dtype", default="f32", choices=("f32", "bf16"),
