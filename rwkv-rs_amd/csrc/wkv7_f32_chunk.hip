@@ -907,6 +907,9 @@ hipError_t launch_forward_chunked_f32(const ForwardDesc& d, hipStream_t stream) 
   p.H = d.H;
   p.C = d.C;
   p.spin_limit = d.kc.spin_limit ? d.kc.spin_limit : kSpinLimit;
+  // the counter lives in the bf16 forward's code object; its address is
+  // looked up on the current device at every launch (a host-side lookup, no
+  // stream work, so captured launches replay it as they are)
   hipError_t e = handover_fault_counter(&p.faults);
   if (e != hipSuccess) return e;
   const dim3 grid(d.H, d.B, 1), block(kBlock, 1, 1);
