@@ -765,6 +765,9 @@ def main():
                     help="cfg3: the decode state's element type")
     ap.add_argument("--kernels", default="auto", choices=("auto", "step"),
                     help="cfg0-cfg2: the library's choice, or the step-by-step kernels throughout")
+    ap.add_argument("--io", default=None, choices=("bf16", "f32"),
+                    help="cfg0-cfg2: the operands' element type instead of the configuration's "
+                         "own (e.g. config[1]'s shape with fp32 operands)")
     ap.add_argument("--neighbor-ops", default="hip", choices=("hip", "torch"),
                     help="cfg4: the ops beside the operator as fused kernels or torch ops")
     ap.add_argument("--copy-probe", action="store_true",
@@ -800,6 +803,8 @@ def main():
         out = bench_decode(cfg, args.steps, args.warmup, probe=args.copy_probe,
                            state_dtype=args.state_dtype)
     else:
+        if args.io:
+            cfg = dict(cfg, io=args.io)
         out = bench_train(cfg, args.steps, args.warmup,
                           with_cpu=(not args.no_cpu and args.config == "cfg1"),
                           probe=args.copy_probe, kernels=args.kernels)
