@@ -189,8 +189,8 @@ __global__ __launch_bounds__(kThreads) void wkv7_infer_kernel(InferParams<Tin> p
 // work (64 x 64 elements of one (row, head) on
 // one wave, a rounding after every operation): each product of two bf16
 // values is one bf16 dot product, each "round two values, add them" one
-// packed conversion and one bf16 dot product (see dot2x2 below), and the two
-// new state values of a key pair are rounded by one packed conversion. The
+// packed conversion and one bf16 dot product (see the blocks below), and the
+// two new state values of a key pair are rounded by one packed conversion. The
 // 8 KiB state moves between HBM and the lanes' rows
 // through LDS, with coalesced 16-byte accesses on the HBM side and each row's
 // 16-byte pieces rotated by row + row / 8 so that neither the row-per-lane
@@ -212,11 +212,8 @@ __device__ __forceinline__ int rot_piece(int row, int q) { return row * 8 + ((q 
 // v_dot2c_f32_bf16, whose accumulator is its destination, and so needs a
 // move of zero before every use (256 per step here). The VOP3P form is
 // reachable through inline assembly only, where the compiler's hazard
-// recognizer cannot see it: a DOT result may be read by another VALU
-// instruction only two wait states after it is written, and overwritten by
-// a non-DOT VALU instruction only after three (what the compiler inserts
-// around v_dot2c on gfx950), so every block below ends with s_nop 2. The
-// kernel has no matrix-core instructions. Two uses:
+// recognizer cannot see it. The kernel has no matrix-core instructions. Two
+// uses:
 // - a product of two bf16 values, exact in fp32, is one dot product of the
 //   state pair with an operand word that holds the key's value in the half
 //   of the key's parity and zero in the other (no widening of the state);
@@ -224,26 +221,183 @@ __device__ __forceinline__ int rot_piece(int row, int q) { return row * 8 + ((q 
 //   product of their packed bf16 roundings with (1, 1), whose bf16 rounding
 //   is that of the fp32 addition (add_rb in wkv7_device.hpp, checked on the
 //   device by tests/test_gpu_selftest.py).
-__device__ __forceinline__ void dot2x2(uint32_t a0, uint32_t b0, uint32_t a1, uint32_t b1,
-                                       float& r0, float& r1) {
-  asm("v_dot2_f32_bf16 %0, %2, %3, 0\n\t"
-      "v_dot2_f32_bf16 %1, %4, %5, 0\n\t"
-      "s_nop 2"
-      : "=&v"(r0), "=v"(r1)
-      : "v"(a0), "v"(b0), "v"(a1), "v"(b1));
-}
-__device__ __forceinline__ float dot2x1(uint32_t a, uint32_t b) {
-  float r;
-  asm("v_dot2_f32_bf16 %0, %1, %2, 0\n\t"
-      "s_nop 2"
-      : "=v"(r)
-      : "v"(a), "v"(b));
-  return r;
-}
-__device__ __forceinline__ uint32_t pack_rb(float lo, float hi) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
-}
+// A DOT result may be read by another VALU instruction three wait states
+// after it is written (what the compiler keeps after v_dot2 on gfx950: an
+// s_nop 2 directly after it, fewer nops when other instructions come
+// between), and the blocks keep the same spacing before a non-DOT
+// instruction overwrites a DOT result. Each block below interleaves
+// independent chains (the keys of a group, the next group's products, the
+// previous group's terms of the y sum) so that those slots hold work instead
+// of nops, and ends with s_nop 2, so code after it may read or overwrite any
+// of its results. The order of every rounded operation of one key is the
+// reference's.
 constexpr uint32_t kOnes = 0x3f803f80u;   // bf16 (1, 1)
+
+// the rounded sums of the sa chain for four keys (products p, formed by the
+// block before), with the next four keys' products formed in the chain's
+// wait slots
+template <bool kNext>
+__device__ __forceinline__ void sa_four(const float (&p)[4], uint32_t s01, uint32_t s23, uint4 a,
+                                        float (&pn)[4], float& z) {
+  uint32_t t;
+  if constexpr (kNext) {
+    asm("v_cvt_pk_bf16_f32 %[t], %[z], %[p0]\n\t"
+        "v_dot2_f32_bf16 %[z], %[t], %[one], 0\n\t"
+        "v_dot2_f32_bf16 %[n0], %[s01], %[ax], 0\n\t"
+        "v_dot2_f32_bf16 %[n1], %[s01], %[ay], 0\n\t"
+        "s_nop 0\n\t"
+        "v_cvt_pk_bf16_f32 %[t], %[z], %[p1]\n\t"
+        "v_dot2_f32_bf16 %[z], %[t], %[one], 0\n\t"
+        "v_dot2_f32_bf16 %[n2], %[s23], %[az], 0\n\t"
+        "v_dot2_f32_bf16 %[n3], %[s23], %[aw], 0\n\t"
+        "s_nop 0\n\t"
+        "v_cvt_pk_bf16_f32 %[t], %[z], %[p2]\n\t"
+        "v_dot2_f32_bf16 %[z], %[t], %[one], 0\n\t"
+        "s_nop 2\n\t"
+        "v_cvt_pk_bf16_f32 %[t], %[z], %[p3]\n\t"
+        "v_dot2_f32_bf16 %[z], %[t], %[one], 0\n\t"
+        "s_nop 2"
+        : [n0] "=&v"(pn[0]), [n1] "=&v"(pn[1]), [n2] "=&v"(pn[2]), [n3] "=&v"(pn[3]), [t] "=&v"(t),
+          [z] "+v"(z)
+        : [p0] "v"(p[0]), [p1] "v"(p[1]), [p2] "v"(p[2]), [p3] "v"(p[3]), [s01] "v"(s01), [s23] "v"(s23),
+          [ax] "v"(a.x), [ay] "v"(a.y), [az] "v"(a.z), [aw] "v"(a.w), [one] "v"(kOnes));
+  } else {
+    asm("v_cvt_pk_bf16_f32 %[t], %[z], %[p0]\n\t"
+        "v_dot2_f32_bf16 %[z], %[t], %[one], 0\n\t"
+        "s_nop 2\n\t"
+        "v_cvt_pk_bf16_f32 %[t], %[z], %[p1]\n\t"
+        "v_dot2_f32_bf16 %[z], %[t], %[one], 0\n\t"
+        "s_nop 2\n\t"
+        "v_cvt_pk_bf16_f32 %[t], %[z], %[p2]\n\t"
+        "v_dot2_f32_bf16 %[z], %[t], %[one], 0\n\t"
+        "s_nop 2\n\t"
+        "v_cvt_pk_bf16_f32 %[t], %[z], %[p3]\n\t"
+        "v_dot2_f32_bf16 %[z], %[t], %[one], 0\n\t"
+        "s_nop 2"
+        : [t] "=&v"(t), [z] "+v"(z)
+        : [p0] "v"(p[0]), [p1] "v"(p[1]), [p2] "v"(p[2]), [p3] "v"(p[3]), [one] "v"(kOnes));
+  }
+}
+// the products of the first four keys
+__device__ __forceinline__ void sa_products(uint32_t s01, uint32_t s23, uint4 a, float (&p)[4]) {
+  asm("v_dot2_f32_bf16 %[p0], %[s01], %[ax], 0\n\t"
+      "v_dot2_f32_bf16 %[p1], %[s01], %[ay], 0\n\t"
+      "v_dot2_f32_bf16 %[p2], %[s23], %[az], 0\n\t"
+      "v_dot2_f32_bf16 %[p3], %[s23], %[aw], 0\n\t"
+      "s_nop 2"
+      : [p0] "=&v"(p[0]), [p1] "=&v"(p[1]), [p2] "=&v"(p[2]), [p3] "=&v"(p[3])
+      : [s01] "v"(s01), [s23] "v"(s23), [ax] "v"(a.x), [ay] "v"(a.y), [az] "v"(a.z), [aw] "v"(a.w));
+}
+// four keys (two state pairs A and B) of the update and their four products
+// with r (yn); kLinks: the four terms of the y sum left by the block before
+// (yp) are added in between, their chain filling the update's wait slots
+template <bool kLinks>
+__device__ __forceinline__ void update_four(uint32_t& pa, uint32_t& pb, uint4 w, const float (&sb)[4],
+                                            const float (&kv)[4], uint4 r, const float (&yp)[4],
+                                            float (&yn)[4], float& zy) {
+  float a0, a1, b0, b1;
+  uint32_t ta0, ta1, tb0, tb1, t;
+  if constexpr (kLinks) {
+    asm("v_dot2_f32_bf16 %[a0], %[pa], %[w0], 0\n\t"
+        "v_dot2_f32_bf16 %[a1], %[pa], %[w1], 0\n\t"
+        "v_cvt_pk_bf16_f32 %[t], %[zy], %[yp0]\n\t"
+        "v_dot2_f32_bf16 %[zy], %[t], %[one], 0\n\t"
+        "v_dot2_f32_bf16 %[b0], %[pb], %[w2], 0\n\t"
+        "v_dot2_f32_bf16 %[b1], %[pb], %[w3], 0\n\t"
+        "v_cvt_pk_bf16_f32 %[ta0], %[a0], %[sb0]\n\t"
+        "v_cvt_pk_bf16_f32 %[t], %[zy], %[yp1]\n\t"
+        "v_dot2_f32_bf16 %[zy], %[t], %[one], 0\n\t"
+        "v_cvt_pk_bf16_f32 %[ta1], %[a1], %[sb1]\n\t"
+        "v_cvt_pk_bf16_f32 %[tb0], %[b0], %[sb2]\n\t"
+        "v_cvt_pk_bf16_f32 %[tb1], %[b1], %[sb3]\n\t"
+        "v_cvt_pk_bf16_f32 %[t], %[zy], %[yp2]\n\t"
+        "v_dot2_f32_bf16 %[zy], %[t], %[one], 0\n\t"
+        "v_dot2_f32_bf16 %[a0], %[ta0], %[one], 0\n\t"
+        "v_dot2_f32_bf16 %[a1], %[ta1], %[one], 0\n\t"
+        "v_dot2_f32_bf16 %[b0], %[tb0], %[one], 0\n\t"
+        "v_cvt_pk_bf16_f32 %[t], %[zy], %[yp3]\n\t"
+        "v_dot2_f32_bf16 %[zy], %[t], %[one], 0\n\t"
+        "v_dot2_f32_bf16 %[b1], %[tb1], %[one], 0\n\t"
+        "v_cvt_pk_bf16_f32 %[ta0], %[a0], %[kv0]\n\t"
+        "v_cvt_pk_bf16_f32 %[ta1], %[a1], %[kv1]\n\t"
+        "v_cvt_pk_bf16_f32 %[tb0], %[b0], %[kv2]\n\t"
+        "v_cvt_pk_bf16_f32 %[tb1], %[b1], %[kv3]\n\t"
+        "v_dot2_f32_bf16 %[a0], %[ta0], %[one], 0\n\t"
+        "v_dot2_f32_bf16 %[a1], %[ta1], %[one], 0\n\t"
+        "v_dot2_f32_bf16 %[b0], %[tb0], %[one], 0\n\t"
+        "v_dot2_f32_bf16 %[b1], %[tb1], %[one], 0\n\t"
+        "s_nop 0\n\t"
+        "v_cvt_pk_bf16_f32 %[pa], %[a0], %[a1]\n\t"
+        "v_dot2_f32_bf16 %[y0], %[pa], %[r0], 0\n\t"
+        "v_cvt_pk_bf16_f32 %[pb], %[b0], %[b1]\n\t"
+        "v_dot2_f32_bf16 %[y1], %[pa], %[r1], 0\n\t"
+        "v_dot2_f32_bf16 %[y2], %[pb], %[r2], 0\n\t"
+        "v_dot2_f32_bf16 %[y3], %[pb], %[r3], 0\n\t"
+        "s_nop 2"
+        : [a0] "=&v"(a0), [a1] "=&v"(a1), [b0] "=&v"(b0), [b1] "=&v"(b1), [ta0] "=&v"(ta0),
+          [ta1] "=&v"(ta1), [tb0] "=&v"(tb0), [tb1] "=&v"(tb1), [t] "=&v"(t), [y0] "=&v"(yn[0]),
+          [y1] "=&v"(yn[1]), [y2] "=&v"(yn[2]), [y3] "=&v"(yn[3]), [pa] "+v"(pa), [pb] "+v"(pb),
+          [zy] "+v"(zy)
+        : [w0] "v"(w.x), [w1] "v"(w.y), [w2] "v"(w.z), [w3] "v"(w.w), [sb0] "v"(sb[0]), [sb1] "v"(sb[1]),
+          [sb2] "v"(sb[2]), [sb3] "v"(sb[3]), [kv0] "v"(kv[0]), [kv1] "v"(kv[1]), [kv2] "v"(kv[2]),
+          [kv3] "v"(kv[3]), [r0] "v"(r.x), [r1] "v"(r.y), [r2] "v"(r.z), [r3] "v"(r.w),
+          [yp0] "v"(yp[0]), [yp1] "v"(yp[1]), [yp2] "v"(yp[2]), [yp3] "v"(yp[3]), [one] "v"(kOnes));
+  } else {
+    asm("v_dot2_f32_bf16 %[a0], %[pa], %[w0], 0\n\t"
+        "v_dot2_f32_bf16 %[a1], %[pa], %[w1], 0\n\t"
+        "v_dot2_f32_bf16 %[b0], %[pb], %[w2], 0\n\t"
+        "v_dot2_f32_bf16 %[b1], %[pb], %[w3], 0\n\t"
+        "v_cvt_pk_bf16_f32 %[ta0], %[a0], %[sb0]\n\t"
+        "v_cvt_pk_bf16_f32 %[ta1], %[a1], %[sb1]\n\t"
+        "v_cvt_pk_bf16_f32 %[tb0], %[b0], %[sb2]\n\t"
+        "v_cvt_pk_bf16_f32 %[tb1], %[b1], %[sb3]\n\t"
+        "v_dot2_f32_bf16 %[a0], %[ta0], %[one], 0\n\t"
+        "v_dot2_f32_bf16 %[a1], %[ta1], %[one], 0\n\t"
+        "v_dot2_f32_bf16 %[b0], %[tb0], %[one], 0\n\t"
+        "v_dot2_f32_bf16 %[b1], %[tb1], %[one], 0\n\t"
+        "v_cvt_pk_bf16_f32 %[ta0], %[a0], %[kv0]\n\t"
+        "v_cvt_pk_bf16_f32 %[ta1], %[a1], %[kv1]\n\t"
+        "v_cvt_pk_bf16_f32 %[tb0], %[b0], %[kv2]\n\t"
+        "v_cvt_pk_bf16_f32 %[tb1], %[b1], %[kv3]\n\t"
+        "v_dot2_f32_bf16 %[a0], %[ta0], %[one], 0\n\t"
+        "v_dot2_f32_bf16 %[a1], %[ta1], %[one], 0\n\t"
+        "v_dot2_f32_bf16 %[b0], %[tb0], %[one], 0\n\t"
+        "v_dot2_f32_bf16 %[b1], %[tb1], %[one], 0\n\t"
+        "s_nop 0\n\t"
+        "v_cvt_pk_bf16_f32 %[pa], %[a0], %[a1]\n\t"
+        "v_dot2_f32_bf16 %[y0], %[pa], %[r0], 0\n\t"
+        "v_cvt_pk_bf16_f32 %[pb], %[b0], %[b1]\n\t"
+        "v_dot2_f32_bf16 %[y1], %[pa], %[r1], 0\n\t"
+        "v_dot2_f32_bf16 %[y2], %[pb], %[r2], 0\n\t"
+        "v_dot2_f32_bf16 %[y3], %[pb], %[r3], 0\n\t"
+        "s_nop 2"
+        : [a0] "=&v"(a0), [a1] "=&v"(a1), [b0] "=&v"(b0), [b1] "=&v"(b1), [ta0] "=&v"(ta0),
+          [ta1] "=&v"(ta1), [tb0] "=&v"(tb0), [tb1] "=&v"(tb1), [y0] "=&v"(yn[0]), [y1] "=&v"(yn[1]),
+          [y2] "=&v"(yn[2]), [y3] "=&v"(yn[3]), [pa] "+v"(pa), [pb] "+v"(pb)
+        : [w0] "v"(w.x), [w1] "v"(w.y), [w2] "v"(w.z), [w3] "v"(w.w), [sb0] "v"(sb[0]), [sb1] "v"(sb[1]),
+          [sb2] "v"(sb[2]), [sb3] "v"(sb[3]), [kv0] "v"(kv[0]), [kv1] "v"(kv[1]), [kv2] "v"(kv[2]),
+          [kv3] "v"(kv[3]), [r0] "v"(r.x), [r1] "v"(r.y), [r2] "v"(r.z), [r3] "v"(r.w), [one] "v"(kOnes));
+    (void)t;
+  }
+}
+// the last four terms of the y sum
+__device__ __forceinline__ void y_links(const float (&yp)[4], float& zy) {
+  uint32_t t;
+  asm("v_cvt_pk_bf16_f32 %[t], %[zy], %[yp0]\n\t"
+      "v_dot2_f32_bf16 %[zy], %[t], %[one], 0\n\t"
+      "s_nop 2\n\t"
+      "v_cvt_pk_bf16_f32 %[t], %[zy], %[yp1]\n\t"
+      "v_dot2_f32_bf16 %[zy], %[t], %[one], 0\n\t"
+      "s_nop 2\n\t"
+      "v_cvt_pk_bf16_f32 %[t], %[zy], %[yp2]\n\t"
+      "v_dot2_f32_bf16 %[zy], %[t], %[one], 0\n\t"
+      "s_nop 2\n\t"
+      "v_cvt_pk_bf16_f32 %[t], %[zy], %[yp3]\n\t"
+      "v_dot2_f32_bf16 %[zy], %[t], %[one], 0\n\t"
+      "s_nop 2"
+      : [t] "=&v"(t), [zy] "+v"(zy)
+      : [yp0] "v"(yp[0]), [yp1] "v"(yp[1]), [yp2] "v"(yp[2]), [yp3] "v"(yp[3]), [one] "v"(kOnes));
+}
 
 __global__ __launch_bounds__(64) void wkv7_infer_bf16_kernel(InferBf16Params p) {
   __shared__ uint4 srow[kHead * 8];        // the state, 8 pieces of 16 bytes per row
@@ -330,41 +484,38 @@ __global__ __launch_bounds__(64) void wkv7_infer_bf16_kernel(InferBf16Params p) 
     // i is rb(z_i), and z_{i+1} = rb(z_i) + rb(product_{i+1}) in fp32, so
     // sa_{i+1} = rb(sa_i + rb(a_{i+1} S[j, i+1])) as kernel.rs:81-83 has it.
     float z = 0.0f;
+    float pz[4];
+    sa_products(sp[0], sp[1], opw[O_A][0], pz);
 #pragma unroll
     for (int i4 = 0; i4 < kHead / 4; ++i4) {
-      const uint4 a4 = opw[O_A][i4];
-      float p0, p1, p2, p3;
-      dot2x2(sp[2 * i4], a4.x, sp[2 * i4], a4.y, p0, p1);
-      dot2x2(sp[2 * i4 + 1], a4.z, sp[2 * i4 + 1], a4.w, p2, p3);
-      z = dot2x1(pack_rb(z, p0), kOnes);
-      z = dot2x1(pack_rb(z, p1), kOnes);
-      z = dot2x1(pack_rb(z, p2), kOnes);
-      z = dot2x1(pack_rb(z, p3), kOnes);
+      float pn[4];
+      if (i4 + 1 < kHead / 4) {
+        sa_four<true>(pz, sp[2 * i4 + 2], sp[2 * i4 + 3], opw[O_A][i4 + 1], pn, z);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) pz[e] = pn[e];
+      } else {
+        sa_four<false>(pz, 0u, 0u, uint4{}, pn, z);
+      }
     }
     const float sa = rb(z);
     float zy = 0.0f;
+    float yq[4] = {0.f, 0.f, 0.f, 0.f};   // the previous four keys' products with r
 #pragma unroll
     for (int i4 = 0; i4 < kHead / 4; ++i4) {
       const uint4 w4 = opw[O_W][i4], r4 = opw[O_R][i4];
       const float4 b4 = opf[O_B][i4], k4 = opf[O_K][i4];
-      const uint32_t wv[4] = {w4.x, w4.y, w4.z, w4.w}, rv[4] = {r4.x, r4.y, r4.z, r4.w};
-      const float bv[4] = {b4.x, b4.y, b4.z, b4.w}, kv[4] = {k4.x, k4.y, k4.z, k4.w};
+      // S[j,i] = rb(rb(rb(S w) + rb(sa b)) + rb(k v)) for keys 4 i4 .. + 3
+      const float sb[4] = {sa * b4.x, sa * b4.y, sa * b4.z, sa * b4.w};
+      const float kvv[4] = {k4.x * vj, k4.y * vj, k4.z * vj, k4.w * vj};
+      float yn[4];
+      if (i4 == 0)
+        update_four<false>(sp[0], sp[1], w4, sb, kvv, r4, yq, yn, zy);
+      else
+        update_four<true>(sp[2 * i4], sp[2 * i4 + 1], w4, sb, kvv, r4, yq, yn, zy);
 #pragma unroll
-      for (int e = 0; e < 4; e += 2) {
-        // S[j,i] = rb(rb(rb(S w) + rb(sa b)) + rb(k v)) for keys i, i + 1,
-        // the two new values rounded by one packed conversion
-        uint32_t& pair = sp[2 * i4 + e / 2];
-        float u0, u1;
-        dot2x2(pair, wv[e], pair, wv[e + 1], u0, u1);                        // S w
-        dot2x2(pack_rb(u0, sa * bv[e]), kOnes, pack_rb(u1, sa * bv[e + 1]), kOnes, u0, u1);
-        dot2x2(pack_rb(u0, kv[e] * vj), kOnes, pack_rb(u1, kv[e + 1] * vj), kOnes, u0, u1);
-        pair = pack_rb(u0, u1);
-        float y0, y1;
-        dot2x2(pair, rv[e], pair, rv[e + 1], y0, y1);                        // S r
-        zy = dot2x1(pack_rb(zy, y0), kOnes);
-        zy = dot2x1(pack_rb(zy, y1), kOnes);
-      }
+      for (int e = 0; e < 4; ++e) yq[e] = yn[e];
     }
+    y_links(yq, zy);
     const float y = rb(zy);
     p.y[off] = (bf16_t)(__float_as_uint(y) >> 16);
     ++valid_t;
