@@ -506,7 +506,8 @@ hipError_t launch_backward(const BackwardDesc& d, hipStream_t stream) {
   if (d.B == 0 || d.H == 0) return hipSuccess;
   if (!d.kc.step_only) {
     if (chunk_backward_supported(d)) return launch_backward_chunked(d, stream);
-    if (chunk_f32_backward_supported(d)) return launch_backward_chunked_f32(d, stream);
+    if (chunk_f32_backward_supported(d) && chunk_f32_backward_preferred(d))
+      return launch_backward_chunked_f32(d, stream);
   }
   return d.dtype == Dtype::BF16 ? launch_bwd_t<bf16_t>(d, stream) : launch_bwd_t<float>(d, stream);
 }

@@ -928,6 +928,19 @@ bool chunk_f32_backward_supported(const BackwardDesc& d) {
   return d.dtype == Dtype::F32 && d.C % kL == 0 && d.T % d.C == 0 && d.T > 0;
 }
 
+// Between checkpoints the chunked backward rebuilds each 16-step chunk's
+// start state by the reference's reversal, on its key waves, a pass per
+// rebuilt chunk that the step kernels (which reverse every step anyway) do
+// not pay: one of every two chunks at chunk_len 32, three of four at 64.
+// Backward alone, one box, fp32: at chunk_len 32 the chunked kernel is as
+// fast or faster from 64 (batch, head) pairs up (2% at 128, 10% at 256) and
+// 1-3% slower at 8-16 pairs; at chunk_len 64 it is 7-10% slower at 8-128
+// pairs and 0.5-3% faster at 256 (one workgroup per CU). At chunk_len 16
+// every chunk starts at a checkpoint and it is 15-26% faster throughout.
+bool chunk_f32_backward_preferred(const BackwardDesc& d) {
+  return d.C <= 2 * kL || (int64_t)d.B * d.H >= 256;
+}
+
 hipError_t launch_backward_chunked_f32(const BackwardDesc& d, hipStream_t stream) {
   F32BwdParams p;
   p.in[I_X] = static_cast<const float*>(d.w);

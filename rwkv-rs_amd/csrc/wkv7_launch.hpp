@@ -84,8 +84,11 @@ hipError_t launch_forward_chunked_f32(const ForwardDesc& d, hipStream_t stream);
 bool chunk_backward_supported(const BackwardDesc& d);
 hipError_t launch_backward_chunked(const BackwardDesc& d, hipStream_t stream);
 // Chunked fp32 matrix-core backward (wkv7_f32_chunk.hip): fp32 operands,
-// chunk_len a multiple of 16, T a positive multiple of chunk_len.
+// chunk_len a multiple of 16, T a positive multiple of chunk_len; picked by
+// launch_backward where chunk_f32_backward_preferred holds as well, the step
+// kernels otherwise.
 bool chunk_f32_backward_supported(const BackwardDesc& d);
+bool chunk_f32_backward_preferred(const BackwardDesc& d);
 hipError_t launch_backward_chunked_f32(const BackwardDesc& d, hipStream_t stream);
 hipError_t launch_backward(const BackwardDesc& d, hipStream_t stream);
 hipError_t launch_infer(const InferDesc& d, hipStream_t stream);

@@ -152,10 +152,13 @@ CRITERION_SHAPES = [   # (B, T, H, chunk_len): crates/rwkv-nn/benches/kernels/mo
 
 @pytest.mark.parametrize("shape", CRITERION_SHAPES)
 @pytest.mark.parametrize("conditioned", [True, False], ids=["w_near_1", "synthetic"])
-def test_fp32_chunked_kernels_at_the_criterion_shapes(wk, oracle, shape, conditioned):
-    # The reference's Criterion bench shapes with fp32 operands, which the
-    # library runs on its fp32 chunked matrix-core kernels (chunk lengths that
-    # are multiples of 16). The benches draw every input N(0, 1), under which
+def test_fp32_at_the_criterion_shapes(wk, oracle, shape, conditioned):
+    # The reference's Criterion bench shapes with fp32 operands: the forward
+    # runs on the fp32 chunked matrix-core kernel (chunk lengths that are
+    # multiples of 16), the backward on the fp32 chunked kernel at chunk_len
+    # 32 and on the step kernel at chunk_len 64 with 64 (batch, head) pairs,
+    # the faster of the two there (test_fp32_backward_kernel_choice below).
+    # The benches draw every input N(0, 1), under which
     # the state grows without bound (timing inputs, not a parity case), so
     # the inputs here are the synthetic distributions. With the decay logits
     # shifted by -6 (w~ within 0.2% of one) the reversal between checkpoints
@@ -198,14 +201,18 @@ def test_fp32_chunked_kernels_at_the_criterion_shapes(wk, oracle, shape, conditi
 @pytest.mark.parametrize("case", [
     # (B, T, H, chunk_len, s0_std, seed)
     (3, 32, 100, 16, 0.1, 60),   # 300 (batch, head) pairs: more workgroups than CUs
-    (1, 144, 2, 48, 0.1, 61),    # three 16-step chunks per checkpoint
+    (1, 144, 2, 48, 0.1, 61),    # three 16-step chunks per checkpoint (step backward)
     (2, 64, 5, 32, None, 62),    # zero initial state, an odd head count
     (1, 16, 3, 16, 0.1, 63),     # one chunk: the start state by the reversal alone
+    (2, 96, 128, 48, 0.1, 64),   # 256 pairs: the chunked backward at chunk_len 48
+    (1, 64, 256, 64, None, 65),  # 256 pairs: the chunked backward at chunk_len 64
 ])
 def test_fp32_chunked_kernels_more_shapes(wk, oracle, case):
     # More shapes on the fp32 chunked kernels, with the decay logits shifted
     # by -6 as above, so that every tensor, dw, dr and da included, is held
-    # to 1e-5 against the oracle at any chunk_len.
+    # to 1e-5 against the oracle at any chunk_len. Past chunk_len 32 the
+    # backward runs the chunked kernel from 256 (batch, head) pairs up, the
+    # step kernel below.
     B, T, H, C, s0_std, seed = case
     announce("fp32 chunked, w~ near 1", case)
     d = load_pkg().synthetic.make_inputs(B, T, H, 64, seed=seed, s0_std=s0_std)
@@ -216,6 +223,38 @@ def test_fp32_chunked_kernels_more_shapes(wk, oracle, case):
     fwd, bwd = run_gpu(wk, d, C, torch.float32, dsT=dsT)
     ofwd, obwd = run_oracle(oracle, d, C, dsT=dsT)
     compare(fwd, bwd, ofwd, obwd, FP32_TOL, f"fp32 chunked w~1 {case}")
+
+
+@pytest.mark.parametrize("case", [
+    # (B, T, H, chunk_len, expected kernel of the backward)
+    (4, 128, 16, 64, "step"),      # 64 pairs, chunk_len 64: the step kernel
+    (4, 64, 16, 32, "chunked"),    # 64 pairs, chunk_len 32: the chunked kernel
+    (1, 64, 256, 64, "chunked"),   # 256 pairs (one per CU), chunk_len 64: chunked
+    (1, 32, 8, 16, "chunked"),     # chunk_len 16: chunked at any size
+])
+def test_fp32_backward_kernel_choice(wk, case):
+    # The fp32 backward's kernel choice (chunk_f32_backward_preferred in
+    # wkv7_f32_chunk.hip): the default call gives the step kernels' result bit
+    # for bit where they are picked, and another result (the chunked kernel's
+    # different summation order) where the chunked kernel is. Decay logits
+    # shifted by -6 (w~ near 1), so that the reversal between checkpoints
+    # keeps the two kernels' results close at chunk_len 64.
+    B, T, H, C, expected = case
+    announce("fp32 backward kernel choice", case)
+    d = load_pkg().synthetic.make_inputs(B, T, H, 64, seed=66, s0_std=0.1)
+    d["w"] = (d["w"] - 6.0).astype(np.float32)
+    ins = [to_dev(d[n], torch.float32) for n in NAMES]
+    s0 = to_dev(d["s0"])
+    fwd = wk.wkv7_statepass_forward(*ins, s0, C)
+    dy = to_dev(d["dy"], torch.float32)
+    dsT = torch.zeros_like(s0)
+    auto = wk.wkv7_statepass_backward(*ins, fwd.state, fwd.removal_state, dy, dsT, C)
+    step = wk.wkv7_backward_ex(*ins, fwd.state, fwd.removal_state, dy, dsT, C, kernels="step")
+    torch.cuda.synchronize()
+    same = all(torch.equal(getattr(auto, gn), getattr(step, gn)) for gn in GRAD_NAMES)
+    assert same == (expected == "step"), (case, same)
+    for gn in GRAD_NAMES:   # either way both are the reference's gradients
+        assert rel_l2(to_np(getattr(auto, gn)), to_np(getattr(step, gn))) < 1e-3, gn
 
 
 @pytest.mark.parametrize("case", [
