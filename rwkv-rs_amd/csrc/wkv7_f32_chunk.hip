@@ -8,9 +8,11 @@
 // the bf16 kernels) on v_mfma_f32_16x16x4_f32, which multiplies fp32 values
 // in fp32 and sums in fp32. The decays are formed as the reference forms them,
 // w~ = exp(W_SCALE * sigmoid(x)) with sigmoid(x) = 1 / (1 + exp(-x)), and
-// multiplied up within a chunk (gamma_t = w~_0 ... w~_t), so the chunk's
-// decay products carry the rounding of the reference's step-by-step
-// multiplications.
+// multiplied up within a chunk by a scan across the 16 lanes of a row
+// (gamma_t = w~_0 ... w~_t, four fp32 multiplications deep). The reference's
+// step-by-step recurrence never forms these products; it multiplies the state
+// by one w~ per step. The two orders round differently, inside the fp32 bar
+// (tests/test_gpu_parity.py).
 //
 // Matrix-core layout (v_mfma_f32_16x16x4_f32, lane l, quad qd = l / 16,
 // t = l % 16): MFMA number r (r < 4) of a 16x16x16 product reads
@@ -153,7 +155,7 @@ struct F32ChunkOps {
 // group's row reads and writes spread over the banks
 __device__ __forceinline__ int dx_at(int t, int g) { return t * 64 + 4 * (g ^ t); }
 // gamma_t of one key at step t = lane t of a DPP row: the product of the
-// chunk's w~ up to t, in step order, w~ = exp(W_SCALE sigmoid(x))
+// chunk's w~ up to t (a lane scan), w~ = exp(W_SCALE sigmoid(x))
 __device__ __forceinline__ float gamma_of(float x) {
   return row_prod16(expf(kWScale * (1.0f / (1.0f + expf(-x)))));
 }
