@@ -41,21 +41,24 @@
  *     about 16 significant bits where fp32 has 24. Measured against the
  *     reference-order fp32 result: the state family about 3e-6 relative L2,
  *     the bf16 outputs and gradients at their own bf16 rounding (1e-4 to 7e-4);
- *   - fp32 operands at chunk_len a multiple of 16 (the fp32 chunked
- *     kernels; the backward at chunk_len 16 and 32, and beyond 32 with
- *     B*H >= 256, where it is the faster of the two families, the step
- *     backward otherwise): fp32 products on the fp32 matrix cores and fp32 sums, in the
- *     chunked matrix form (16-step blocks as matrix products rather than
- *     step by step); the backward rebuilds start states between checkpoints
- *     by the reference's reversal in its operation order, which amplifies
- *     any fp32 difference by about 1.35 per step. Measured against the
- *     reference-order fp32 result at config[0]: output 2.6e-7 relative L2,
- *     checkpoints 1.7e-7, the gradients through the rebuilt start states
- *     (dw, dr, da) 6.2e-6, 4.6e-6, 6.0e-6, the others 2.5e-7 to 4e-7 (the
- *     step kernels on the same call: 1.8e-7, 7e-8, 3.7e-6, 3.0e-6, 4.3e-6);
- *   - bf16 operands at every other chunk_len (the forward at chunk_len > 16
- *     included), fp32 operands at chunk lengths that are not multiples of
- *     16, and the fp32 backward at chunk_len > 32 with B*H < 256: the step
+ *   - the fp32 chunked kernels: the forward of fp32 operands at chunk_len
+ *     16 and 32 and of bf16 operands at 32 (bf16 rows are widened to fp32
+ *     exactly, as the reference casts them, and y is rounded to bf16 as it
+ *     is stored), the backward of fp32 operands at chunk_len 16 and 32 and,
+ *     past 32, with B*H >= 256 (where it is the faster family): fp32
+ *     products on the fp32 matrix cores and fp32 sums, in the chunked matrix
+ *     form (16-step blocks as matrix products rather than step by step); the
+ *     backward rebuilds start states between checkpoints by the reference's
+ *     reversal in its operation order, which amplifies any fp32 difference
+ *     by about 1.35 per step. Measured against the reference-order fp32
+ *     result at config[0]: output 2.6e-7 relative L2, checkpoints 1.7e-7,
+ *     the gradients through the rebuilt start states (dw, dr, da) 6.2e-6,
+ *     4.6e-6, 6.0e-6, the others 2.5e-7 to 4e-7 (the step kernels on the
+ *     same call: 1.8e-7, 7e-8, 3.7e-6, 3.0e-6, 4.3e-6);
+ *   - everything else (chunk lengths that are not multiples of 16, the
+ *     forward past chunk_len 32, whose checkpoints in the reference's order
+ *     keep the rebuilt-state gradients at the reference algorithm's own
+ *     accuracy, and the fp32 backward past 32 with B*H < 256): the step
  *     kernels, fp32 products and sums in the reference's operation order.
  * wkv7_forward_ex / wkv7_backward_ex with WKV7_KERNELS_STEP run the step
  * kernels, i.e. the reference's operation order, for every case.
@@ -169,9 +172,10 @@ int wkv7_backward(const void *weight_decay, const void *receptance,
  * Explicit kernel choice. No counterpart in the reference (whose backend picks
  * one kernel per element type). wkv7_forward / wkv7_backward and the trait
  * entry points use WKV7_KERNELS_AUTO: the chunked matrix-core kernels for
- * bf16 operands (forward at chunk_len 16, backward at chunk_len a multiple of
- * 16) and for fp32 operands (chunk_len a multiple of 16; the backward past
- * chunk_len 32 only with B*H >= 256), the step-by-step kernels otherwise;
+ * bf16 operands (the forward at chunk_len 16 split-bf16 and at 32 on the
+ * fp32 matrix cores, the backward at any multiple of 16) and for fp32
+ * operands (the forward at chunk_len 16 and 32, the backward at 16 and 32
+ * and, past 32, with B*H >= 256), the step-by-step kernels otherwise;
  * the arithmetic of each family is described at the top
  * of this file. WKV7_KERNELS_STEP runs the step kernels for every case (to
  * compare the families on one input). handover_spin_limit bounds the polls

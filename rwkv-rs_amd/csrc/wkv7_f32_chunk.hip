@@ -3,7 +3,9 @@
 // Computes what wkv7_forward_kernel and wkv7_backward_kernel do
 // (crates/rwkv-nn/src/kernels/wkv7_common/kernel.rs:6-114 and 116-308,
 // launched by wkv7_common/host.rs:29-183 and 185-369) for fp32 operands at
-// chunk lengths that are multiples of 16, with every product an fp32
+// chunk lengths that are multiples of 16 (and the forward of bf16 operands,
+// widened to fp32 as the reference casts them; the launchers' comments say
+// where each kernel is picked), with every product an fp32
 // product: the chunked matrix form of wkv7_chunk.hpp (the same identities as
 // the bf16 kernels) on v_mfma_f32_16x16x4_f32, which multiplies fp32 values
 // in fp32 and sums in fp32. The decays are formed as the reference forms them,
@@ -174,12 +176,16 @@ struct F32Flags {
   int fault;               // a wave gave up a wait
 };
 
+// Tin: the operand and output type, float or bf16 (bf16 rows are widened to
+// fp32 exactly as they load, as the reference casts them before its kernel,
+// host.rs:45-64; y is rounded to bf16 as it is stored)
+template <typename Tin>
 struct F32FwdParams {
-  const float* in[R_COUNT];   // [B,T,H,64] each, in R_* order
+  const Tin* in[R_COUNT];     // [B,T,H,64] each, in R_* order
   const float* s0;            // [B,H,64(value),64(key)] or null
   float* ckpt;                // [B,H,T/C,64(key),64(value)]
   float* sa;                  // [B,T,H,64]
-  float* y;                   // [B,T,H,64]
+  Tin* y;                     // [B,T,H,64]
   float* sT;                  // [B,H,64,64] or null
   unsigned int* faults;       // the chunked forwards' hand-over fault counter
   int T, H, C;
@@ -189,24 +195,38 @@ struct F32FwdParams {
 // step t of chunk c, keys (or values) 16 kk + 4 qd .. + 3 of a row tensor:
 // the A or B operand fragment of a contraction over keys. The rows are read
 // once per launch, with the non-temporal hint.
-__device__ __forceinline__ f32x4 row_frag4(const float* base, int64_t tstride, int c, int t, int kk,
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+template <typename Tin>
+__device__ __forceinline__ f32x4 row_frag4(const Tin* base, int64_t tstride, int c, int t, int kk,
                                            int qd) {
-  return __builtin_nontemporal_load(
-      reinterpret_cast<const f32x4*>(base + (int64_t)(kL * c + t) * tstride + 16 * kk + 4 * qd));
+  const Tin* const q = base + (int64_t)(kL * c + t) * tstride + 16 * kk + 4 * qd;
+  if constexpr (std::is_same<Tin, float>::value) {
+    return __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(q));
+  } else {
+    const u32x2 x = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(q));
+    return f32x4{__uint_as_float(x[0] << 16), __uint_as_float(x[0] & 0xffff0000u),
+                 __uint_as_float(x[1] << 16), __uint_as_float(x[1] & 0xffff0000u)};
+  }
 }
 // steps 4 qd + r of chunk c, value 16 vb + t: the B operand fragment of a
 // contraction over steps
-__device__ __forceinline__ f32x4 col_frag4(const float* base, int64_t tstride, int c, int t, int vb,
+template <typename Tin>
+__device__ __forceinline__ f32x4 col_frag4(const Tin* base, int64_t tstride, int c, int t, int vb,
                                            int qd) {
   f32x4 x;
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
-    x[r] = __builtin_nontemporal_load(base + (int64_t)(kL * c + 4 * qd + r) * tstride + 16 * vb + t);
+  for (int r = 0; r < 4; ++r) {
+    const Tin* const q = base + (int64_t)(kL * c + 4 * qd + r) * tstride + 16 * vb + t;
+    if constexpr (std::is_same<Tin, float>::value)
+      x[r] = __builtin_nontemporal_load(q);
+    else
+      x[r] = __uint_as_float((uint32_t)__builtin_nontemporal_load(q) << 16);
+  }
   return x;
 }
 
-template <bool kHasS0>
-__global__ __launch_bounds__(kBlock, 1) void wkv7_fwd_f32_chunk_kernel(const F32FwdParams p) {
+template <typename Tin, bool kHasS0>
+__global__ __launch_bounds__(kBlock, 1) void wkv7_fwd_f32_chunk_kernel(const F32FwdParams<Tin> p) {
   __shared__ F32ChunkOps ops[kSlots];
   __shared__ F32PrepLds prep[kSlots];
   __shared__ __attribute__((aligned(16))) float dx[kSlots][kL * 64];
@@ -233,12 +253,12 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_fwd_f32_chunk_kernel(const F32
     const int s = wave - kChainWaves;
     F32PrepLds& my = prep[s];
     if (s < nchunks) {
-      const float* const bx = p.in[R_X] + tok0;
-      const float* const brr = p.in[R_R] + tok0;
-      const float* const bk = p.in[R_K] + tok0;
-      const float* const bv = p.in[R_V] + tok0;
-      const float* const ba = p.in[R_A] + tok0;
-      const float* const bb = p.in[R_B] + tok0;
+      const Tin* const bx = p.in[R_X] + tok0;
+      const Tin* const brr = p.in[R_R] + tok0;
+      const Tin* const bk = p.in[R_K] + tok0;
+      const Tin* const bv = p.in[R_V] + tok0;
+      const Tin* const ba = p.in[R_A] + tok0;
+      const Tin* const bb = p.in[R_B] + tok0;
       // the chunk's rows: x, r, k, a, b at step t, keys 16 kk + 4 qd + r;
       // V at steps 4 qd + r, values 16 vb + t. Each register set is reloaded
       // with the wave's next chunk as soon as this chunk has consumed it.
@@ -441,7 +461,7 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_fwd_f32_chunk_kernel(const F32
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         p.sa[cbase + (int64_t)(4 * qd + r) * tstride + jcol] = sa[r];
-        p.y[cbase + (int64_t)(4 * qd + r) * tstride + jcol] = y[r];
+        Io<Tin>::put1(&p.y[cbase + (int64_t)(4 * qd + r) * tstride + jcol], y[r]);
       }
       if ((c + 1) % per_ckpt == 0) store_ckpt((c + 1) / per_ckpt - 1);
     }
@@ -460,7 +480,7 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_fwd_f32_chunk_kernel(const F32
     const float nan = __builtin_nanf("");
     for (int64_t i = tid; i < (int64_t)T * kHead; i += kBlock) {
       const int64_t off = tok0 + (i >> 6) * tstride + (i & 63);
-      p.y[off] = nan;
+      Io<Tin>::put1(&p.y[off], nan);
       p.sa[off] = nan;
     }
     float* const ck = p.ckpt + bh * (T / p.C) * (kHead * kHead);
@@ -888,22 +908,34 @@ __global__ __launch_bounds__(kBlock, 1) void wkv7_bwd_f32_chunk_kernel(const F32
 
 }  // namespace
 
+// fp32 operands at chunk_len 16 and 32, bf16 operands at 32 (at 16 the
+// split-bf16 chunked forward runs). Past 32 the step forward runs: the
+// backward rebuilds the start states between checkpoints by the reference's
+// reversal, which multiplies a checkpoint's deviation by about 1.35 per
+// step, and this kernel's checkpoints (chunked products of the decays) sit
+// 1.7e-7 from the reference order's where the step forward's sit 5-7e-8.
+// Measured against exact gradients, at chunk_len 48 and 64 that left dw,
+// dr, da 2-3 times further off than the reference algorithm itself, while
+// from the step forward's checkpoints they match its accuracy; at 32 both
+// stay within 1.2 times of it (and within bf16 rounding for bf16 operands).
 bool chunk_f32_forward_supported(const ForwardDesc& d) {
-  return d.dtype == Dtype::F32 && d.C % kL == 0 && d.T % d.C == 0;
+  const bool io = d.dtype == Dtype::F32 || (d.dtype == Dtype::BF16 && d.C > kL);
+  return io && d.C % kL == 0 && d.C <= 2 * kL && d.T % d.C == 0;
 }
 
-hipError_t launch_forward_chunked_f32(const ForwardDesc& d, hipStream_t stream) {
-  F32FwdParams p;
-  p.in[R_X] = static_cast<const float*>(d.w);
-  p.in[R_R] = static_cast<const float*>(d.r);
-  p.in[R_K] = static_cast<const float*>(d.k);
-  p.in[R_V] = static_cast<const float*>(d.v);
-  p.in[R_A] = static_cast<const float*>(d.a);
-  p.in[R_B] = static_cast<const float*>(d.b);
+template <typename Tin>
+static hipError_t launch_fwd_f32(const ForwardDesc& d, hipStream_t stream) {
+  F32FwdParams<Tin> p;
+  p.in[R_X] = static_cast<const Tin*>(d.w);
+  p.in[R_R] = static_cast<const Tin*>(d.r);
+  p.in[R_K] = static_cast<const Tin*>(d.k);
+  p.in[R_V] = static_cast<const Tin*>(d.v);
+  p.in[R_A] = static_cast<const Tin*>(d.a);
+  p.in[R_B] = static_cast<const Tin*>(d.b);
   p.s0 = d.s0;
   p.ckpt = d.ckpt;
   p.sa = d.sa;
-  p.y = static_cast<float*>(d.y);
+  p.y = static_cast<Tin*>(d.y);
   p.sT = d.sT;
   p.T = d.T;
   p.H = d.H;
@@ -916,10 +948,14 @@ hipError_t launch_forward_chunked_f32(const ForwardDesc& d, hipStream_t stream) 
   if (e != hipSuccess) return e;
   const dim3 grid(d.H, d.B, 1), block(kBlock, 1, 1);
   if (d.s0)
-    hipLaunchKernelGGL(wkv7_fwd_f32_chunk_kernel<true>, grid, block, 0, stream, p);
+    hipLaunchKernelGGL((wkv7_fwd_f32_chunk_kernel<Tin, true>), grid, block, 0, stream, p);
   else
-    hipLaunchKernelGGL(wkv7_fwd_f32_chunk_kernel<false>, grid, block, 0, stream, p);
+    hipLaunchKernelGGL((wkv7_fwd_f32_chunk_kernel<Tin, false>), grid, block, 0, stream, p);
   return hipGetLastError();
+}
+
+hipError_t launch_forward_chunked_f32(const ForwardDesc& d, hipStream_t stream) {
+  return d.dtype == Dtype::BF16 ? launch_fwd_f32<bf16_t>(d, stream) : launch_fwd_f32<float>(d, stream);
 }
 
 }  // namespace wkv7

@@ -72,9 +72,9 @@ hipError_t take_handover_faults(hipStream_t stream, uint32_t* count);
 // that counter's device address on the current device
 hipError_t handover_fault_counter(unsigned int** counter);
 
-// Chunked fp32 matrix-core forward (wkv7_f32_chunk.hip): fp32 operands,
-// chunk_len a multiple of 16; picked by launch_forward under the same choice.
-// Its hand-over faults count in the same counter.
+// Chunked fp32 matrix-core forward (wkv7_f32_chunk.hip): fp32 operands at
+// chunk_len 16 and 32, bf16 operands at 32; picked by launch_forward under
+// the same choice. Its hand-over faults count in the same counter.
 bool chunk_f32_forward_supported(const ForwardDesc& d);
 hipError_t launch_forward_chunked_f32(const ForwardDesc& d, hipStream_t stream);
 

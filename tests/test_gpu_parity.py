@@ -153,11 +153,11 @@ CRITERION_SHAPES = [   # (B, T, H, chunk_len): crates/rwkv-nn/benches/kernels/mo
 @pytest.mark.parametrize("shape", CRITERION_SHAPES)
 @pytest.mark.parametrize("conditioned", [True, False], ids=["w_near_1", "synthetic"])
 def test_fp32_at_the_criterion_shapes(wk, oracle, shape, conditioned):
-    # The reference's Criterion bench shapes with fp32 operands: the forward
-    # runs on the fp32 chunked matrix-core kernel (chunk lengths that are
-    # multiples of 16), the backward on the fp32 chunked kernel at chunk_len
-    # 32 and on the step kernel at chunk_len 64 with 64 (batch, head) pairs,
-    # the faster of the two there (test_fp32_backward_kernel_choice below).
+    # The reference's Criterion bench shapes with fp32 operands: at chunk_len
+    # 32 the forward and the backward run on the fp32 chunked matrix-core
+    # kernels; at 64 with 64 (batch, head) pairs both run on the step
+    # kernels (test_forward_kernel_choice and test_fp32_backward_kernel_choice
+    # below).
     # The benches draw every input N(0, 1), under which
     # the state grows without bound (timing inputs, not a parity case), so
     # the inputs here are the synthetic distributions. With the decay logits
@@ -201,7 +201,7 @@ def test_fp32_at_the_criterion_shapes(wk, oracle, shape, conditioned):
 @pytest.mark.parametrize("case", [
     # (B, T, H, chunk_len, s0_std, seed)
     (3, 32, 100, 16, 0.1, 60),   # 300 (batch, head) pairs: more workgroups than CUs
-    (1, 144, 2, 48, 0.1, 61),    # three 16-step chunks per checkpoint (step backward)
+    (1, 144, 2, 48, 0.1, 61),    # three 16-step chunks per checkpoint (step kernels)
     (2, 64, 5, 32, None, 62),    # zero initial state, an odd head count
     (1, 16, 3, 16, 0.1, 63),     # one chunk: the start state by the reversal alone
     (2, 96, 128, 48, 0.1, 64),   # 256 pairs: the chunked backward at chunk_len 48
@@ -211,8 +211,8 @@ def test_fp32_chunked_kernels_more_shapes(wk, oracle, case):
     # More shapes on the fp32 chunked kernels, with the decay logits shifted
     # by -6 as above, so that every tensor, dw, dr and da included, is held
     # to 1e-5 against the oracle at any chunk_len. Past chunk_len 32 the
-    # backward runs the chunked kernel from 256 (batch, head) pairs up, the
-    # step kernel below.
+    # forward runs the step kernel, and the backward the chunked kernel from
+    # 256 (batch, head) pairs up, the step kernel below.
     B, T, H, C, s0_std, seed = case
     announce("fp32 chunked, w~ near 1", case)
     d = load_pkg().synthetic.make_inputs(B, T, H, 64, seed=seed, s0_std=s0_std)
@@ -223,6 +223,38 @@ def test_fp32_chunked_kernels_more_shapes(wk, oracle, case):
     fwd, bwd = run_gpu(wk, d, C, torch.float32, dsT=dsT)
     ofwd, obwd = run_oracle(oracle, d, C, dsT=dsT)
     compare(fwd, bwd, ofwd, obwd, FP32_TOL, f"fp32 chunked w~1 {case}")
+
+
+@pytest.mark.parametrize("case", [
+    # (dtype, B, T, H, chunk_len, expected kernel of the forward)
+    ("f32", 2, 64, 4, 16, "chunked"),
+    ("f32", 2, 64, 4, 32, "chunked"),
+    ("f32", 1, 96, 4, 48, "step"),
+    ("f32", 1, 128, 4, 64, "step"),
+    ("bf16", 2, 64, 4, 16, "chunked"),
+    ("bf16", 2, 64, 4, 32, "chunked"),
+    ("bf16", 1, 128, 4, 64, "step"),
+])
+def test_forward_kernel_choice(wk, case):
+    # The forward's kernel choice (chunk_forward_supported in
+    # wkv7_chunk_forward.hip, chunk_f32_forward_supported in
+    # wkv7_f32_chunk.hip): past chunk_len 32 the default call gives the step
+    # kernel's outputs and checkpoints bit for bit (their reference-order
+    # checkpoints keep the rebuilt-state gradients at the reference
+    # algorithm's accuracy); at 16 and 32 a chunked kernel's.
+    dtype, B, T, H, C, expected = case
+    announce("forward kernel choice", case)
+    bf16 = dtype == "bf16"
+    dt = torch.bfloat16 if bf16 else torch.float32
+    d = load_pkg().synthetic.make_inputs(B, T, H, 64, seed=67, s0_std=0.1, bf16=bf16)
+    ins = [to_dev(d[n], dt) for n in NAMES]
+    s0 = to_dev(d["s0"])
+    auto = wk.wkv7_statepass_forward(*ins, s0, C)
+    step = wk.wkv7_forward_ex(*ins, s0, C, kernels="step")
+    torch.cuda.synchronize()
+    same = torch.equal(auto.state, step.state) and torch.equal(auto.output, step.output)
+    assert same == (expected == "step"), (case, same)
+    assert rel_l2(to_np(auto.state), to_np(step.state)) < (1e-4 if bf16 else 1e-5)
 
 
 @pytest.mark.parametrize("case", [
@@ -289,14 +321,17 @@ def test_bf16_inputs_fp32_state(wk, oracle, case):
     (1, 192, 2, 64, 0.1, 23),   # four: start states rebuilt over up to 48 steps
 ])
 def test_bf16_long_chunks_on_the_chunked_kernels(wk, oracle, case):
-    # chunk_len > 16 with bf16 operands: the step forward (fp32 checkpoints
-    # every chunk_len steps) and the chunked backward, which rebuilds the start
-    # states of the 16-step chunks between checkpoints by the reference's
-    # reversal (kernel.rs:239-246). The forward and the gradients that do not
-    # read a rebuilt state are held to the bf16 bars against the oracle; dw, dr
-    # and da, which do, to the reference algorithm's own accuracy (the oracle
-    # in fp32 against exact fp64 gradients, which is what grows with
-    # chunk_len) plus bf16 rounding.
+    # chunk_len > 16 with bf16 operands: the forward in fp32 (at 32 the fp32
+    # chunked kernel, the bf16 rows widened as the reference casts them; past
+    # 32 the step kernel), fp32 checkpoints every chunk_len steps, and the
+    # chunked backward, which
+    # rebuilds the start states of the 16-step chunks between checkpoints by
+    # the reference's reversal (kernel.rs:239-246). The forward's fp32 state
+    # family is held to the fp32 bar, y and the gradients that do not read a
+    # rebuilt state to the bf16 bars against the oracle; dw, dr and da, which
+    # do, to the reference algorithm's own accuracy (the oracle in fp32
+    # against exact fp64 gradients, which is what grows with chunk_len) plus
+    # bf16 rounding.
     B, T, H, C, s0_std, seed = case
     announce("bf16 long chunk", case)
     pkg = load_pkg()
@@ -308,7 +343,7 @@ def test_bf16_long_chunks_on_the_chunked_kernels(wk, oracle, case):
     exact = oracle.grad_f64(*(d[n] for n in NAMES), d["s0"], d["dy"])
     assert rel_l2(to_np(fwd.output), pkg.synthetic.bf16_round(ofwd["output"])) <= BF16_TOL
     for key in ("removal_state", "state", "final_state"):
-        assert rel_l2(to_np(getattr(fwd, key)), ofwd[key]) <= BF16_STATE_TOL, key
+        assert rel_l2(to_np(getattr(fwd, key)), ofwd[key]) <= FP32_TOL, key
     assert fwd.state.shape[2] == T // C
     rebuilt = ("weight_decay_grad", "receptance_grad", "removal_grad")
     for gn in GRAD_NAMES + ("initial_state_grad",):
@@ -383,10 +418,10 @@ def test_bf16_statetune_on_the_chunked_kernels(wk, oracle):
 
 
 def test_long_chunk_bf16_backward_matches_step_backward(wk):
-    # chunk_len 32 with bf16 operands: the forward runs the step kernels (their
-    # fp32 checkpoints are what the rebuild between checkpoints needs) and the
-    # backward the chunked kernels; on the same checkpoints the step backward
-    # gives the same gradients to bf16 rounding
+    # chunk_len 32 with bf16 operands: the forward runs the fp32 chunked
+    # kernel (its fp32 checkpoints are what the rebuild between checkpoints
+    # needs) and the backward the chunked kernels; on the same checkpoints
+    # the step backward gives the same gradients to bf16 rounding
     announce("bf16 chunk_len 32 chunked vs step backward", (1, 64, 2, 32))
     pkg = load_pkg()
     d = pkg.synthetic.make_inputs(1, 64, 2, 64, seed=24, s0_std=0.1, bf16=True)
@@ -443,18 +478,21 @@ def test_sequence_split_is_exact(wk):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
-def test_empty_sequence(wk, dtype):
+@pytest.mark.parametrize("chunk_len", [16, 32])
+def test_empty_sequence(wk, dtype, chunk_len):
     # T = 0: final state = initial state, initial-state grad = final-state grad.
-    # bf16 at chunk_len 16 runs the chunked forward with no chunks.
-    announce("T=0", str(dtype))
+    # Both chunked forwards run with no chunks (bf16 at chunk_len 16 the
+    # split-bf16 one, fp32 and bf16 at 32 the fp32 one).
+    announce("T=0", str(dtype), chunk_len)
     B, H = 2, 3
     e = torch.empty(B, 0, H, 64, device="cuda", dtype=dtype)
     s0 = torch.randn(B, H, 64, 64, device="cuda")
-    out = wk.wkv7_statepass_forward(e, e, e, e, e, e, s0, 16)
+    out = wk.wkv7_statepass_forward(e, e, e, e, e, e, s0, chunk_len)
     assert out.output.shape == (B, 0, H, 64) and out.state.shape == (B, H, 0, 64, 64)
     assert torch.equal(out.final_state, s0)
     dsT = torch.randn(B, H, 64, 64, device="cuda")
-    g = wk.wkv7_statepass_backward(e, e, e, e, e, e, out.state, out.removal_state, e, dsT, 16)
+    g = wk.wkv7_statepass_backward(e, e, e, e, e, e, out.state, out.removal_state, e, dsT,
+                                   chunk_len)
     assert torch.equal(g.initial_state_grad, dsT)
 
 
@@ -500,15 +538,16 @@ def test_two_streams_match_one(wk):
             assert torch.equal(getattr(g1, gn), getattr(g2, gn)), gn
 
 
-@pytest.mark.parametrize("dtype", ["bf16", "f32"])
-def test_graph_replays_match_eager(wk, dtype):
+@pytest.mark.parametrize("dtype,chunk_len", [("bf16", 16), ("f32", 16), ("bf16", 32)])
+def test_graph_replays_match_eager(wk, dtype, chunk_len):
     # The forward and backward launch kernels only (no memsets, copies or
     # allocations inside the library), so a caller can capture them in a HIP
     # graph: each of several replays, with eager work between them, gives
     # the eager results bit for bit (bf16 and fp32 operands: the chunked
-    # kernels of each; the fp32 forward looks up its fault counter's address
-    # at every launch, captured ones included).
-    announce("graph replay", dtype)
+    # kernels of each, bf16 at chunk_len 32 on the fp32 chunked forward and
+    # the long-chunk bf16 backward; the fp32 forward looks up its fault
+    # counter's address at every launch, captured ones included).
+    announce("graph replay", dtype, chunk_len)
     bf16 = dtype == "bf16"
     dt = torch.bfloat16 if bf16 else torch.float32
     d = load_pkg().synthetic.make_inputs(2, 128, 4, 64, seed=41, s0_std=0.1, bf16=bf16)
@@ -517,8 +556,8 @@ def test_graph_replays_match_eager(wk, dtype):
     zero = torch.zeros_like(s0)
 
     def run():
-        f = wk.wkv7_statepass_forward(*ins, s0, 16)
-        return f, wk.wkv7_statepass_backward(*ins, f.state, f.removal_state, dy, zero, 16)
+        f = wk.wkv7_statepass_forward(*ins, s0, chunk_len)
+        return f, wk.wkv7_statepass_backward(*ins, f.state, f.removal_state, dy, zero, chunk_len)
 
     ef, eg = run()
     torch.cuda.synchronize()
@@ -702,9 +741,10 @@ def test_bf16_chunked_backward_matches_step_backward(wk, case):
     assert err < BF16_STATE_TOL, err
 
 
-@pytest.mark.parametrize("dtype", ["bf16", "f32"])
-def test_handover_fault_poisons_outputs_and_is_reported(wk, dtype):
-    """The chunked forwards' waves (bf16 and fp32 operands) hand chunks over
+@pytest.mark.parametrize("dtype,chunk_len", [("bf16", 16), ("f32", 16), ("bf16", 32)])
+def test_handover_fault_poisons_outputs_and_is_reported(wk, dtype, chunk_len):
+    """The chunked forwards' waves (bf16 operands at chunk_len 16, fp32
+    operands, and bf16 operands past 16 on the fp32 kernel) hand chunks over
     through LDS flags with bounded waits. With the bound forced down to a
     single poll (the handover_spin_limit option) waves give up waits, which a
     correct run never does: every (batch, head) whose launch saw that must
@@ -712,7 +752,7 @@ def test_handover_fault_poisons_outputs_and_is_reported(wk, dtype):
     the count of such launches must be reported by wkv7_take_faults as
     WKV7_ERR_HANDOVER, and every other (batch, head) must equal the normal run
     bit for bit. A normal run afterwards reports no fault."""
-    announce("hand-over fault path (forced from the host)", dtype)
+    announce("hand-over fault path (forced from the host)", dtype, chunk_len)
     pkg = load_pkg()
     B, T, H = 2, 256, 8
     bf16 = dtype == "bf16"
@@ -720,9 +760,9 @@ def test_handover_fault_poisons_outputs_and_is_reported(wk, dtype):
     ins = [to_dev(d[n], torch.bfloat16 if bf16 else torch.float32) for n in NAMES]
     s0 = to_dev(d["s0"])
     assert wk.take_faults() == 0
-    good = wk.wkv7_statepass_forward(*ins, s0, 16)
+    good = wk.wkv7_statepass_forward(*ins, s0, chunk_len)
     assert wk.take_faults() == 0
-    bad = wk.wkv7_forward_ex(*ins, s0, 16, handover_spin_limit=1)
+    bad = wk.wkv7_forward_ex(*ins, s0, chunk_len, handover_spin_limit=1)
     faults = wk.take_faults()
     poisoned = 0
     for b in range(B):
@@ -738,18 +778,18 @@ def test_handover_fault_poisons_outputs_and_is_reported(wk, dtype):
                 assert torch.equal(bad.final_state[b, h], good.final_state[b, h]), (b, h)
     print("forced hand-over faults:", faults, "poisoned pairs:", poisoned, flush=True)
     assert faults == poisoned and faults > 0
-    again = wk.wkv7_statepass_forward(*ins, s0, 16)
+    again = wk.wkv7_statepass_forward(*ins, s0, chunk_len)
     assert wk.take_faults() == 0
     assert torch.equal(again.output, good.output)
     # the C ABI's own status for the same event
     native = load_pkg()._native
-    wk.wkv7_forward_ex(*ins, s0, 16, handover_spin_limit=1)
+    wk.wkv7_forward_ex(*ins, s0, chunk_len, handover_spin_limit=1)
     n = ctypes.c_uint32(0)
     rc = native.lib().wkv7_take_faults(torch.cuda.current_stream().cuda_stream, ctypes.byref(n))
     assert rc == native.WKV7_ERR_HANDOVER and n.value > 0, (rc, n.value)
     assert wk.take_faults() == 0
     # and the Python side raises it where the caller polls
-    wk.wkv7_forward_ex(*ins, s0, 16, handover_spin_limit=1)
+    wk.wkv7_forward_ex(*ins, s0, chunk_len, handover_spin_limit=1)
     with pytest.raises(native.Wkv7Error, match="hand-over"):
         wk.check_faults()
     wk.check_faults()      # the counter was reset
